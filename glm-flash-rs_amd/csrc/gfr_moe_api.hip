@@ -1,0 +1,413 @@
+// The C ABI of include/gfr_moe.h: engines that own scratch (allocated once, zeroed) and issue the gfx950 kernels
+// on the caller's stream. Mirrors the reference's Rust owners (grouping.rs, experts.rs, fast_experts.rs, moe.rs):
+// same buffer contracts, same precondition checks, no allocation / free / host sync inside run.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+#include <string>
+
+#include "../../include/gfr_moe.h"
+#include "launch.hpp"
+#include "prefill.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+// hipError_t -> the reference's "CUDA {code} {name}: {msg}" shape (cuda.rs:102-123)
+int hip_fail(hipError_t e, const char* what) {
+    return fail((int)e, "HIP %d %s: %s (%s)", (int)e, hipGetErrorName(e), hipGetErrorString(e), what);
+}
+
+
+template <typename T>
+int alloc_zero(T** p, size_t count, const char* what) {
+    *p = nullptr;
+    if (count == 0) count = 1;
+    hipError_t e = hipMalloc((void**)p, count * sizeof(T));
+    if (e != hipSuccess) return hip_fail(e, what);
+    e = hipMemset(*p, 0, count * sizeof(T));
+    if (e != hipSuccess) return hip_fail(e, what);
+    return 0;
+}
+
+void free_all(std::initializer_list<void*> ps) {
+    for (void* p : ps)
+        if (p) (void)hipFree(p);
+}
+
+int check_weights(const gfr_exl3_experts* w, int hidden, int inter) {
+    if (!w) return fail(GFR_EINVAL, "null weights");
+    if (w->hidden != hidden || w->inter != inter)
+        return fail(GFR_EINVAL, "weights shape %dx%d, engine %dx%d", w->hidden, w->inter, hidden, inter);
+    if (w->bits < 2 || w->bits > 5) return fail(GFR_EINVAL, "bits %d outside 2..5", w->bits);
+    if (w->experts <= 0) return fail(GFR_EINVAL, "experts %d", w->experts);
+    if (!w->gt || !w->ut || !w->dt || !w->suh_g || !w->suh_u || !w->suh_d || !w->svh_g || !w->svh_u || !w->svh_d)
+        return fail(GFR_EINVAL, "null weight tensor");
+    return 0;
+}
+
+int check_shape(int hidden, int inter) {
+    if (hidden <= 0 || inter <= 0 || hidden % 128 || inter % 128)
+        return fail(GFR_EINVAL, "hidden %d / inter %d must be positive multiples of 128", hidden, inter);
+    if (hidden % 256 || inter % 256)
+        return fail(GFR_EINVAL, "hidden %d / inter %d must be multiples of 256 (k split of the GEMV)", hidden, inter);
+    return 0;
+}
+
+}  // namespace
+
+struct gfr_grouping {
+    int experts, slots, max_rows;
+    uint32_t* bits;
+    int *prefix, *counts, *ids, *count, *members;
+};
+
+struct gfr_experts {
+    int hidden, inter, slots, exl3_slots, max_rows;
+    uint16_t *xg, *xu, *xd;
+    float *z, *y;
+};
+
+struct gfr_linear {
+    int kin, n, bits;
+    int *pick, *ids, *count, *members;
+    uint16_t* xh;
+    float* z;
+};
+
+struct gfr_moe {
+    int hidden, inter, routed, topk, slots, max_rows, decode_rows;
+    float* weights;
+    int* picks;
+    float* out;
+    gfr_grouping* group_dec;   // member stride = the decode engine's bound
+    gfr_grouping* group_pre;   // member stride = max_rows (prefill chunks)
+    gfr_experts* dec;
+    gfr_fast_experts* pre;
+};
+
+extern "C" {
+
+const char* gfr_last_error(void) { return g_last_error.c_str(); }
+const char* gfr_version(void) { return "gfr_moe 0.1 gfx950"; }
+
+// ---- grouping ---------------------------------------------------------------------------------------------------
+int gfr_grouping_create(gfr_grouping** out, int experts, int slots, int max_rows) {
+    if (!out) return fail(GFR_EINVAL, "null out");
+    *out = nullptr;
+    if (experts <= 0 || experts > 4096) return fail(GFR_EINVAL, "grouping experts %d outside 1..4096", experts);
+    if (slots <= 0 || slots > 32) return fail(GFR_EINVAL, "grouping slots %d outside 1..32", slots);
+    if (max_rows <= 0 || max_rows > (1 << 20)) return fail(GFR_EINVAL, "grouping capacity %d", max_rows);
+    gfr_grouping* g = new gfr_grouping{experts, slots, max_rows, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    const size_t nwd = (size_t)(max_rows + 31) / 32;
+    int rc;
+    if ((rc = alloc_zero(&g->bits, (size_t)experts * nwd, "grouping bits")) ||
+        (rc = alloc_zero(&g->prefix, (size_t)experts * nwd, "grouping prefix")) ||
+        (rc = alloc_zero(&g->counts, (size_t)experts, "grouping counts")) ||
+        (rc = alloc_zero(&g->ids, (size_t)experts, "grouping ids")) || (rc = alloc_zero(&g->count, 1, "count")) ||
+        (rc = alloc_zero(&g->members, (size_t)experts * max_rows, "grouping members"))) {
+        gfr_grouping_destroy(g);
+        return rc;
+    }
+    *out = g;
+    return 0;
+}
+
+int gfr_grouping_run(gfr_grouping* g, hipStream_t stream, const int32_t* picks, int rows) {
+    if (!g || !picks) return fail(GFR_EINVAL, "null grouping or picks");
+    if (rows <= 0 || rows > g->max_rows) return fail(GFR_EINVAL, "grouping rows %d exceed scratch %d", rows, g->max_rows);
+    hipError_t e;
+    if (rows <= gfr::GROUP_SMALL_ROWS && g->experts <= 1024)
+        e = gfr::launch_group_small(stream, picks, rows, g->slots, g->experts, g->ids, g->count, g->members,
+                                    g->max_rows);
+    else
+        e = gfr::launch_group_large(stream, picks, rows, g->slots, g->experts, g->bits, g->prefix, g->counts, g->ids,
+                                    g->count, g->members, g->max_rows);
+    if (e != hipSuccess) return hip_fail(e, "grouping launch");
+    return 0;
+}
+
+int32_t* gfr_grouping_ids(const gfr_grouping* g) { return g ? g->ids : nullptr; }
+int32_t* gfr_grouping_count(const gfr_grouping* g) { return g ? g->count : nullptr; }
+int32_t* gfr_grouping_members(const gfr_grouping* g) { return g ? g->members : nullptr; }
+
+int gfr_grouping_destroy(gfr_grouping* g) {
+    if (!g) return 0;
+    free_all({g->bits, g->prefix, g->counts, g->ids, g->count, g->members});
+    delete g;
+    return 0;
+}
+
+// ---- decode / verify experts ------------------------------------------------------------------------------------
+int gfr_experts_create(gfr_experts** out, int hidden, int inter, int slots, int exl3_slots, int max_rows) {
+    if (!out) return fail(GFR_EINVAL, "null out");
+    *out = nullptr;
+    int rc = check_shape(hidden, inter);
+    if (rc) return rc;
+    if (slots <= 0 || slots > 32 || exl3_slots < 0 || exl3_slots > slots)
+        return fail(GFR_EINVAL, "slots %d / exl3_slots %d", slots, exl3_slots);
+    if (max_rows <= 0 || max_rows > 64) return fail(GFR_EINVAL, "expert verifier scratch bound: max_rows %d", max_rows);
+    gfr_experts* ex = new gfr_experts{hidden, inter, slots, exl3_slots, max_rows, nullptr, nullptr, nullptr, nullptr,
+                                      nullptr};
+    const size_t P = (size_t)max_rows * slots;
+    const size_t SK = (size_t)(gfr::gemv_splits(hidden) > gfr::gemv_splits(inter) ? gfr::gemv_splits(hidden)
+                                                                                  : gfr::gemv_splits(inter));
+    const size_t zn = 2 * SK * P * (size_t)(hidden > inter ? hidden : inter);
+    if ((rc = alloc_zero(&ex->xg, P * hidden, "experts xg")) || (rc = alloc_zero(&ex->xu, P * hidden, "experts xu")) ||
+        (rc = alloc_zero(&ex->xd, P * inter, "experts xd")) || (rc = alloc_zero(&ex->z, zn, "experts z")) ||
+        (rc = alloc_zero(&ex->y, P * hidden, "experts y"))) {
+        gfr_experts_destroy(ex);
+        return rc;
+    }
+    *out = ex;
+    return 0;
+}
+
+int gfr_experts_run_rows(gfr_experts* ex, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
+                         int input_stride, const int32_t* picks, const int32_t* ids, const int32_t* count,
+                         const int32_t* members, int rows, int maxm) {
+    if (!ex) return fail(GFR_EINVAL, "null experts");
+    int rc = check_weights(w, ex->hidden, ex->inter);
+    if (rc) return rc;
+    if (!(rows > 0 && rows <= ex->max_rows && maxm >= rows && maxm <= ex->max_rows))
+        return fail(GFR_EINVAL, "expert verifier row/member bounds: rows %d maxm %d max_rows %d", rows, maxm,
+                    ex->max_rows);
+    if (!input || !picks || !ids || !count || !members) return fail(GFR_EINVAL, "null input");
+    if (input_stride < ex->hidden) return fail(GFR_EINVAL, "input stride %d < hidden %d", input_stride, ex->hidden);
+    const int P = rows * ex->slots, D = ex->hidden, N = ex->inter;
+    const int maxu = P < w->experts ? P : w->experts;
+    hipError_t e;
+    if ((e = gfr::launch_rot_in(stream, input, input_stride, false, picks, w->suh_g, w->suh_u, ex->xg, ex->xu, D, P,
+                                ex->slots, ex->exl3_slots, 2)) != hipSuccess)
+        return hip_fail(e, "rot_in");
+    if ((e = gfr::launch_gemv(stream, ex->xg, ex->xu, w->gt, w->ut, ids, count, members, ex->z, D, N, P, maxm,
+                              ex->slots, w->experts, w->bits, 2, maxu)) != hipSuccess)
+        return hip_fail(e, "gate/up gemv");
+    if ((e = gfr::launch_gateup_epilogue(stream, ex->z, picks, w->svh_g, w->svh_u, w->suh_d, ex->xd, P, N,
+                                         gfr::gemv_splits(D), ex->slots, ex->exl3_slots, 10.f)) != hipSuccess)
+        return hip_fail(e, "gate/up epilogue");
+    if ((e = gfr::launch_gemv(stream, ex->xd, ex->xd, w->dt, w->dt, ids, count, members, ex->z, N, D, P, maxm,
+                              ex->slots, w->experts, w->bits, 1, maxu)) != hipSuccess)
+        return hip_fail(e, "down gemv");
+    if ((e = gfr::launch_down_epilogue(stream, ex->z, picks, w->svh_d, ex->y, P, D, gfr::gemv_splits(N), ex->slots,
+                                       ex->exl3_slots)) != hipSuccess)
+        return hip_fail(e, "down epilogue");
+    return 0;
+}
+
+float* gfr_experts_y(const gfr_experts* ex) { return ex ? ex->y : nullptr; }
+uint16_t* gfr_experts_xd(const gfr_experts* ex) { return ex ? ex->xd : nullptr; }
+
+int gfr_experts_destroy(gfr_experts* ex) {
+    if (!ex) return 0;
+    free_all({ex->xg, ex->xu, ex->xd, ex->z, ex->y});
+    delete ex;
+    return 0;
+}
+
+// ---- single linear ----------------------------------------------------------------------------------------------
+int gfr_linear_create(gfr_linear** out, int kin, int n, int bits) {
+    if (!out) return fail(GFR_EINVAL, "null out");
+    *out = nullptr;
+    int rc = check_shape(kin, n);
+    if (rc) return rc;
+    if (bits < 2 || bits > 5) return fail(GFR_EINVAL, "bits %d outside 2..5", bits);
+    gfr_linear* l = new gfr_linear{kin, n, bits, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    if ((rc = alloc_zero(&l->pick, 1, "linear pick")) || (rc = alloc_zero(&l->ids, 1, "linear ids")) ||
+        (rc = alloc_zero(&l->count, 1, "linear count")) || (rc = alloc_zero(&l->members, 1, "linear members")) ||
+        (rc = alloc_zero(&l->xh, (size_t)kin, "linear xh")) ||
+        (rc = alloc_zero(&l->z, (size_t)gfr::gemv_splits(kin) * n, "linear z"))) {
+        gfr_linear_destroy(l);
+        return rc;
+    }
+    const int one = 1;  // one expert (id 0, already zero), one member: row 0 slot 0 (code 0, already zero)
+    hipError_t e = hipMemcpy(l->count, &one, sizeof one, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        gfr_linear_destroy(l);
+        return hip_fail(e, "linear init");
+    }
+    *out = l;
+    return 0;
+}
+
+int gfr_linear_run(gfr_linear* l, hipStream_t stream, const uint16_t* x, const uint32_t* trellis, const uint16_t* suh,
+                   const uint16_t* svh, float* y) {
+    if (!l || !x || !trellis || !suh || !svh || !y) return fail(GFR_EINVAL, "null argument");
+    hipError_t e;
+    if ((e = gfr::launch_rot_in(stream, x, l->kin, true, l->pick, suh, suh, l->xh, l->xh, l->kin, 1, 1, 1, 1)) !=
+        hipSuccess)
+        return hip_fail(e, "linear rot");
+    if ((e = gfr::launch_gemv(stream, l->xh, l->xh, trellis, trellis, l->ids, l->count, l->members, l->z, l->kin, l->n,
+                              1, 1, 1, 1, l->bits, 1, 1)) != hipSuccess)
+        return hip_fail(e, "linear gemv");
+    if ((e = gfr::launch_down_epilogue(stream, l->z, l->pick, svh, y, 1, l->n, gfr::gemv_splits(l->kin), 1, 1)) !=
+        hipSuccess)
+        return hip_fail(e, "linear epilogue");
+    return 0;
+}
+
+int gfr_linear_destroy(gfr_linear* l) {
+    if (!l) return 0;
+    free_all({l->pick, l->ids, l->count, l->members, l->xh, l->z});
+    delete l;
+    return 0;
+}
+
+// ---- debug decode -----------------------------------------------------------------------------------------------
+int gfr_exl3_decode_tiles(hipStream_t stream, const uint32_t* trellis, int kin, int n, int bits, uint16_t* out) {
+    if (!trellis || !out) return fail(GFR_EINVAL, "null argument");
+    if (kin <= 0 || n <= 0 || kin % 16 || n % 16) return fail(GFR_EINVAL, "kin %d / n %d not multiples of 16", kin, n);
+    if (bits < 2 || bits > 5) return fail(GFR_EINVAL, "bits %d outside 2..5", bits);
+    hipError_t e = gfr::launch_decode_tiles(stream, trellis, kin, n, bits, out);
+    if (e != hipSuccess) return hip_fail(e, "decode tiles");
+    return 0;
+}
+
+// ---- prefill experts --------------------------------------------------------------------------------------------
+int gfr_fast_experts_create(gfr_fast_experts** out, int hidden, int inter, int slots, int exl3_slots, int experts,
+                            int max_rows) {
+    if (!out) return fail(GFR_EINVAL, "null out");
+    *out = nullptr;
+    int rc = check_shape(hidden, inter);
+    if (rc) return rc;
+    if (slots <= 0 || slots > 32 || exl3_slots < 0 || exl3_slots > slots)
+        return fail(GFR_EINVAL, "slots %d / exl3_slots %d", slots, exl3_slots);
+    if (experts <= 0 || experts > 4096) return fail(GFR_EINVAL, "experts %d", experts);
+    if (max_rows <= 0 || max_rows > (1 << 16)) return fail(GFR_EINVAL, "expert prefill scratch bound: %d", max_rows);
+    gfr_fast_experts* fx = nullptr;
+    hipError_t e = gfr::prefill_create(&fx, hidden, inter, slots, exl3_slots, experts, max_rows);
+    if (e != hipSuccess) return hip_fail(e, "prefill scratch");
+    *out = fx;
+    return 0;
+}
+
+int gfr_fast_experts_run(gfr_fast_experts* fx, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
+                         int input_stride, const int32_t* picks, const int32_t* ids, const int32_t* count,
+                         const int32_t* members, int rows, int maxm, int shared_x) {
+    if (!fx) return fail(GFR_EINVAL, "null fast experts");
+    const gfr::PrefillDims d = gfr::prefill_dims(fx);
+    int rc = check_weights(w, d.hidden, d.inter);
+    if (rc) return rc;
+    if (!(rows > 0 && rows <= d.max_rows && maxm >= rows && maxm <= d.max_rows))
+        return fail(GFR_EINVAL, "expert rows/member stride outside scratch: rows %d maxm %d max_rows %d", rows, maxm,
+                    d.max_rows);
+    if (w->experts > d.experts) return fail(GFR_EINVAL, "weights hold %d experts, engine %d", w->experts, d.experts);
+    if (!input || !picks || !ids || !count || !members) return fail(GFR_EINVAL, "null input");
+    if (input_stride < d.hidden) return fail(GFR_EINVAL, "input stride %d < hidden %d", input_stride, d.hidden);
+    hipError_t e = gfr::prefill_run(fx, stream, w, input, input_stride, picks, ids, count, members, rows, maxm,
+                                    shared_x != 0);
+    if (e != hipSuccess) return hip_fail(e, "prefill run");
+    return 0;
+}
+
+float* gfr_fast_experts_output(const gfr_fast_experts* fx) { return fx ? gfr::prefill_output(fx) : nullptr; }
+uint16_t* gfr_fast_experts_xd(const gfr_fast_experts* fx) { return fx ? gfr::prefill_xd(fx) : nullptr; }
+int gfr_fast_experts_destroy(gfr_fast_experts* fx) {
+    gfr::prefill_destroy(fx);
+    return 0;
+}
+
+// ---- one MoE layer ----------------------------------------------------------------------------------------------
+int gfr_moe_create(gfr_moe** out, int hidden, int inter, int routed, int topk, int max_rows) {
+    if (!out) return fail(GFR_EINVAL, "null out");
+    *out = nullptr;
+    int rc = check_shape(hidden, inter);
+    if (rc) return rc;
+    if (routed <= 0 || routed > 1023) return fail(GFR_EINVAL, "routed experts %d outside 1..1023", routed);
+    if (topk <= 0 || topk > 31 || topk > routed) return fail(GFR_EINVAL, "topk %d", topk);
+    if (max_rows <= 0 || max_rows > (1 << 16)) return fail(GFR_EINVAL, "max_rows %d", max_rows);
+    gfr_moe* m = new gfr_moe{hidden, inter, routed, topk, topk + 1, max_rows, 64 < max_rows ? 64 : max_rows,
+                             nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    const size_t P = (size_t)max_rows * m->slots;
+    if ((rc = alloc_zero(&m->weights, P, "moe weights")) || (rc = alloc_zero(&m->picks, P, "moe picks")) ||
+        (rc = alloc_zero(&m->out, (size_t)max_rows * hidden, "moe output")) ||
+        (rc = gfr_grouping_create(&m->group_dec, routed + 1, m->slots, m->decode_rows)) ||
+        (rc = gfr_experts_create(&m->dec, hidden, inter, m->slots, m->slots, m->decode_rows))) {
+        gfr_moe_destroy(m);
+        return rc;
+    }
+    if (max_rows > m->decode_rows &&
+        ((rc = gfr_grouping_create(&m->group_pre, routed + 1, m->slots, max_rows)) ||
+         (rc = gfr_fast_experts_create(&m->pre, hidden, inter, m->slots, m->slots, routed + 1, max_rows)))) {
+        gfr_moe_destroy(m);
+        return rc;
+    }
+    *out = m;
+    return 0;
+}
+
+int gfr_moe_set_decode_rows(gfr_moe* m, int decode_rows) {
+    if (!m) return fail(GFR_EINVAL, "null moe");
+    if (decode_rows < 0 || decode_rows > m->dec->max_rows || decode_rows > m->group_dec->max_rows)
+        return fail(GFR_EINVAL, "decode_rows %d outside 0..%d", decode_rows, m->dec->max_rows);
+    if (decode_rows < m->max_rows && !m->pre)
+        return fail(GFR_EINVAL, "decode_rows %d leaves rows for the prefill engine, which this layer lacks",
+                    decode_rows);
+    m->decode_rows = decode_rows;
+    return 0;
+}
+
+int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
+                const float* logits, int rows) {
+    if (!m) return fail(GFR_EINVAL, "null moe");
+    int rc = check_weights(w, m->hidden, m->inter);
+    if (rc) return rc;
+    if (w->experts != m->routed + 1)
+        return fail(GFR_EINVAL, "weights hold %d experts, layer needs %d routed + 1 shared", w->experts, m->routed);
+    if (rows <= 0 || rows > m->max_rows) return fail(GFR_EINVAL, "rows %d outside 1..%d", rows, m->max_rows);
+    if (!input || !logits) return fail(GFR_EINVAL, "null input");
+    hipError_t e;
+    if ((e = gfr::launch_route(stream, logits, rows, m->routed, m->topk, m->routed, m->picks, m->weights)) !=
+        hipSuccess)
+        return hip_fail(e, "route");
+    const float* y;
+    if (rows <= m->decode_rows) {
+        gfr_grouping* g = m->group_dec;
+        if ((rc = gfr_grouping_run(g, stream, m->picks, rows))) return rc;
+        if ((rc = gfr_experts_run_rows(m->dec, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members,
+                                       rows, g->max_rows)))
+            return rc;
+        y = m->dec->y;
+    } else {
+        gfr_grouping* g = m->group_pre;
+        if ((rc = gfr_grouping_run(g, stream, m->picks, rows))) return rc;
+        if ((rc = gfr_fast_experts_run(m->pre, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members,
+                                       rows, g->max_rows, 0)))
+            return rc;
+        y = gfr::prefill_output(m->pre);
+    }
+    if ((e = gfr::launch_combine(stream, y, m->weights, rows, m->slots, m->hidden, m->out)) != hipSuccess)
+        return hip_fail(e, "combine");
+    return 0;
+}
+
+float* gfr_moe_output(const gfr_moe* m) { return m ? m->out : nullptr; }
+int32_t* gfr_moe_picks(const gfr_moe* m) { return m ? m->picks : nullptr; }
+float* gfr_moe_weights(const gfr_moe* m) { return m ? m->weights : nullptr; }
+
+int gfr_moe_destroy(gfr_moe* m) {
+    if (!m) return 0;
+    gfr_grouping_destroy(m->group_dec);
+    gfr_grouping_destroy(m->group_pre);
+    gfr_experts_destroy(m->dec);
+    gfr_fast_experts_destroy(m->pre);
+    free_all({m->weights, m->picks, m->out});
+    delete m;
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,216 @@
+// Token -> expert bucketing on gfx950, bit-exact to glm-flash-rs native/grouping.cu (group_clear/mark/prefix/ids/
+// scatter and group_small) and to the host oracle of src/grouping.rs:141-192.
+//
+// Output contract (grouping.rs:12-112): count = number of distinct experts in picks[rows][slots]; ids[u] = the u-th
+// smallest of them; members[u * maxm + i] = the codes r * 32 + slot of expert ids[u], rows ascending (a row counts
+// once, with the first slot that holds the expert), then -1 up to maxm; members rows u in [count, E) are all -1.
+// The order never depends on atomic arrival: rows are marked in a bitmap (atomicOr is order-free) and read back
+// in bit order.
+//
+// Two paths: rows <= GROUP_SMALL_ROWS (launch.hpp) runs in one 1024-thread workgroup with the bitmap in LDS; larger windows run three
+// launches (per-256-row LDS bitmaps, per-expert popcount prefix, per-expert scatter), which also lifts the
+// reference's 8192-row limit.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gfr {
+
+// Inclusive scan of x over the workgroup (blockDim.x a multiple of 64, at most 1024). `scratch` holds 16 ints.
+// Returns the inclusive prefix; *total receives the sum.
+__device__ __forceinline__ int block_scan(int x, int* scratch, int* total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int v = __shfl_up(x, d, 64);
+        if (lane >= d) x += v;
+    }
+    if (lane == 63) scratch[wave] = x;
+    __syncthreads();
+    int off = 0, all = 0;
+    for (int w = 0; w < nw; ++w) {
+        const int s = scratch[w];
+        if (w < wave) off += s;
+        all += s;
+    }
+    __syncthreads();
+    *total = all;
+    return x + off;
+}
+
+// First slot of row r that holds expert e (the row is known to hold it).
+__device__ __forceinline__ int first_slot(const int* __restrict__ picks, int r, int slots, int e) {
+    int s = 0;
+    while (s < slots - 1 && picks[r * slots + s] != e) ++s;
+    return s;
+}
+
+// One workgroup of 1024 threads. LDS: E * ceil(rows / 32) bitmap words + E counts.
+__global__ void __launch_bounds__(1024) group_small_kernel(const int* __restrict__ picks, int rows, int slots,
+                                                           int E, int* __restrict__ ids, int* __restrict__ count,
+                                                           int* __restrict__ members, int maxm) {
+    extern __shared__ uint32_t lds[];
+    __shared__ int scan_scratch[16];
+    const int NWD = (rows + 31) >> 5;
+    uint32_t* bits = lds;                                    // [E][NWD]
+    int* ucnt = reinterpret_cast<int*>(lds + (size_t)E * NWD);  // [E]: count of the u-th used expert
+    int* place = ucnt + E;                                   // [E]: u of expert e, or -1
+    for (int i = threadIdx.x; i < E * NWD; i += blockDim.x) bits[i] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < rows * slots; i += blockDim.x) {
+        const int r = i / slots, e = picks[i];
+        if (e >= 0 && e < E) atomicOr(&bits[e * NWD + (r >> 5)], 1u << (r & 31));
+    }
+    __syncthreads();
+    // experts in rounds of blockDim.x: count, then the ascending order of the used ones
+    int base = 0;
+    for (int e0 = 0; e0 < E; e0 += blockDim.x) {
+        const int e = e0 + threadIdx.x;
+        int c = 0;
+        if (e < E)
+            for (int w = 0; w < NWD; ++w) c += __popc(bits[e * NWD + w]);
+        int total;
+        const int incl = block_scan(c > 0, scan_scratch, &total);
+        if (e < E) {
+            place[e] = c > 0 ? base + incl - 1 : -1;
+            if (c > 0) {
+                ids[base + incl - 1] = e;
+                ucnt[base + incl - 1] = c;
+            }
+        }
+        base += total;
+    }
+    __syncthreads();
+    const int used = base;
+    if (threadIdx.x == 0) *count = used;
+    // members: thread per (expert, bitmap word); the word's offset is the popcount of the expert's earlier words
+    for (int i = threadIdx.x; i < E * NWD; i += blockDim.x) {
+        const int e = i / NWD, w = i % NWD;
+        uint32_t b = bits[i];
+        if (!b) continue;
+        int off = 0;
+        for (int q = 0; q < w; ++q) off += __popc(bits[e * NWD + q]);
+        const int u = place[e];
+        while (b) {
+            const int r = w * 32 + __builtin_ctz(b);
+            members[(size_t)u * maxm + off++] = r * 32 + first_slot(picks, r, slots, e);
+            b &= b - 1;
+        }
+    }
+    // every other entry of the E x maxm table is -1
+    for (size_t i = threadIdx.x; i < (size_t)E * maxm; i += blockDim.x) {
+        const int u = (int)(i / maxm), j = (int)(i % maxm);
+        if (u >= used || j >= ucnt[u]) members[i] = -1;
+    }
+}
+
+// Large windows, launch 1: the 256 rows of this workgroup marked in an LDS bitmap [E][8], stored to
+// bits[e][NWD] (each global word is owned by exactly one workgroup, so no clear launch is needed).
+__global__ void __launch_bounds__(256) group_mark_kernel(const int* __restrict__ picks, int rows, int slots, int E,
+                                                         uint32_t* __restrict__ bits) {
+    extern __shared__ uint32_t lb[];                         // [E][8]
+    const int NWD = (rows + 31) >> 5;
+    for (int i = threadIdx.x; i < E * 8; i += blockDim.x) lb[i] = 0;
+    __syncthreads();
+    const int r = blockIdx.x * 256 + threadIdx.x;
+    if (r < rows)
+        for (int s = 0; s < slots; ++s) {
+            const int e = picks[r * slots + s];
+            if (e >= 0 && e < E) atomicOr(&lb[e * 8 + (threadIdx.x >> 5)], 1u << (r & 31));
+        }
+    __syncthreads();
+    for (int i = threadIdx.x; i < E * 8; i += blockDim.x) {
+        const int e = i >> 3, w = blockIdx.x * 8 + (i & 7);
+        if (w < NWD) bits[(size_t)e * NWD + w] = lb[i];
+    }
+}
+
+// Launch 2, workgroup per expert: exclusive popcount prefix of its bitmap words, and its row count.
+__global__ void __launch_bounds__(256) group_prefix_kernel(const uint32_t* __restrict__ bits, int rows,
+                                                           int* __restrict__ prefix, int* __restrict__ counts) {
+    __shared__ int scan_scratch[16];
+    const int e = blockIdx.x, NWD = (rows + 31) >> 5;
+    const int per = (NWD + blockDim.x - 1) / blockDim.x, w0 = threadIdx.x * per;
+    const uint32_t* b = bits + (size_t)e * NWD;
+    int c = 0;
+    for (int w = w0; w < w0 + per && w < NWD; ++w) c += __popc(b[w]);
+    int total;
+    int run = block_scan(c, scan_scratch, &total) - c;
+    for (int w = w0; w < w0 + per && w < NWD; ++w) {
+        prefix[(size_t)e * NWD + w] = run;
+        run += __popc(b[w]);
+    }
+    if (threadIdx.x == 0) counts[e] = total;
+}
+
+// Launch 3, workgroup per expert: its place among the used experts, ids / count, its members and its -1 tail.
+__global__ void __launch_bounds__(256) group_scatter_kernel(const int* __restrict__ picks, int rows, int slots,
+                                                            int E, const uint32_t* __restrict__ bits,
+                                                            const int* __restrict__ prefix,
+                                                            const int* __restrict__ counts, int* __restrict__ ids,
+                                                            int* __restrict__ count, int* __restrict__ members,
+                                                            int maxm) {
+    __shared__ int scan_scratch[16];
+    __shared__ int below_sh, used_sh;
+    const int e = blockIdx.x, NWD = (rows + 31) >> 5;
+    int below = 0, used = 0;
+    for (int q = threadIdx.x; q < E; q += blockDim.x) {
+        const int c = counts[q] > 0;
+        used += c;
+        below += (q < e) & c;
+    }
+    int t1, t2;
+    block_scan(below, scan_scratch, &t1);
+    block_scan(used, scan_scratch, &t2);
+    if (threadIdx.x == 0) {
+        below_sh = t1;
+        used_sh = t2;
+    }
+    __syncthreads();
+    below = below_sh;
+    used = used_sh;
+    const int ce = counts[e];
+    if (e == 0 && threadIdx.x == 0) *count = used;
+    if (ce > 0) {
+        const int u = below;
+        if (threadIdx.x == 0) ids[u] = e;
+        for (int w = threadIdx.x; w < NWD; w += blockDim.x) {
+            uint32_t b = bits[(size_t)e * NWD + w];
+            int off = prefix[(size_t)e * NWD + w];
+            while (b) {
+                const int r = w * 32 + __builtin_ctz(b);
+                members[(size_t)u * maxm + off++] = r * 32 + first_slot(picks, r, slots, e);
+                b &= b - 1;
+            }
+        }
+        for (int j = ce + threadIdx.x; j < maxm; j += blockDim.x) members[(size_t)u * maxm + j] = -1;
+    }
+    // rows [used, E) of the table: owned by the workgroup with the same index (never a used row above)
+    if (e >= used)
+        for (int j = threadIdx.x; j < maxm; j += blockDim.x) members[(size_t)e * maxm + j] = -1;
+}
+
+}  // namespace gfr
+
+#include "launch.hpp"
+
+namespace gfr {
+
+hipError_t launch_group_small(hipStream_t s, const int* picks, int rows, int slots, int E, int* ids, int* count,
+                              int* members, int maxm) {
+    const size_t lds = ((size_t)E * ((rows + 31) / 32) + 2 * (size_t)E) * 4;
+    group_small_kernel<<<1, 1024, lds, s>>>(picks, rows, slots, E, ids, count, members, maxm);
+    return hipGetLastError();
+}
+
+hipError_t launch_group_large(hipStream_t s, const int* picks, int rows, int slots, int E, uint32_t* bits,
+                              int* prefix, int* counts, int* ids, int* count, int* members, int maxm) {
+    group_mark_kernel<<<(rows + 255) / 256, 256, (size_t)E * 8 * 4, s>>>(picks, rows, slots, E, bits);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    group_prefix_kernel<<<E, 256, 0, s>>>(bits, rows, prefix, counts);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    group_scatter_kernel<<<E, 256, 0, s>>>(picks, rows, slots, E, bits, prefix, counts, ids, count, members, maxm);
+    return hipGetLastError();
+}
+
+}  // namespace gfr

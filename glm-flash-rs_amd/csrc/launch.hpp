@@ -1,0 +1,37 @@
+// Host-side launchers of the gfx950 kernels (one per kernel family); the C ABI in gfr_moe_api.hip calls these.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gfr {
+
+// grouping.hip
+constexpr int GROUP_SMALL_ROWS = 256;
+hipError_t launch_group_small(hipStream_t s, const int* picks, int rows, int slots, int E, int* ids, int* count,
+                              int* members, int maxm);
+hipError_t launch_group_large(hipStream_t s, const int* picks, int rows, int slots, int E, uint32_t* bits,
+                              int* prefix, int* counts, int* ids, int* count, int* members, int maxm);
+
+// exl3_decode.hip
+hipError_t launch_decode_tiles(hipStream_t s, const uint32_t* T, int kin, int n, int bits, uint16_t* out);
+// in_f16: x is fp16 (the single-linear config) instead of bf16 (the reference's rot_in)
+hipError_t launch_rot_in(hipStream_t s, const uint16_t* x, int x_stride, bool in_f16, const int* pick,
+                         const uint16_t* suh0, const uint16_t* suh1, uint16_t* out0, uint16_t* out1, int K, int P,
+                         int slots, int exl3_slots, int mats);
+int gemv_splits(int Kin);  // K splits of the decode GEMV (fixed by the shape, so a row's bits never depend on rows)
+hipError_t launch_gemv(hipStream_t s, const uint16_t* X0, const uint16_t* X1, const uint32_t* T0, const uint32_t* T1,
+                       const int* uids, const int* ucount, const int* members, float* Z, int Kin, int N, int P,
+                       int maxm, int slots, int E, int bits, int mats, int maxu);
+hipError_t launch_gateup_epilogue(hipStream_t s, const float* Z, const int* pick, const uint16_t* svh_g,
+                                  const uint16_t* svh_u, const uint16_t* suh_d, uint16_t* xd, int P, int N, int SK,
+                                  int slots, int exl3_slots, float limit);
+hipError_t launch_down_epilogue(hipStream_t s, const float* Z, const int* pick, const uint16_t* svh_d, float* y,
+                                int P, int D, int SK, int slots, int exl3_slots);
+
+// router.hip
+hipError_t launch_route(hipStream_t s, const float* logits, int rows, int E, int topk, int shared_id, int* picks,
+                        float* weights);
+hipError_t launch_combine(hipStream_t s, const float* y, const float* weights, int rows, int slots, int D,
+                          float* out);
+
+}  // namespace gfr

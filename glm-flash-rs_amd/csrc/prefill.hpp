@@ -1,0 +1,24 @@
+// Prefill-chunk experts (FastExperts, glm-flash-rs src/fast_experts.rs:27-208) on gfx950: engine interface used by
+// the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "../../include/gfr_moe.h"
+
+namespace gfr {
+
+struct PrefillDims {
+    int hidden, inter, slots, exl3_slots, experts, max_rows;
+};
+
+hipError_t prefill_create(gfr_fast_experts** out, int hidden, int inter, int slots, int exl3_slots, int experts,
+                          int max_rows);
+PrefillDims prefill_dims(const gfr_fast_experts* fx);
+hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_experts* w, const uint16_t* input,
+                       int input_stride, const int* picks, const int* ids, const int* count, const int* members,
+                       int rows, int maxm, bool shared_x);
+float* prefill_output(const gfr_fast_experts* fx);
+uint16_t* prefill_xd(const gfr_fast_experts* fx);
+void prefill_destroy(gfr_fast_experts* fx);
+
+}  // namespace gfr

@@ -1,0 +1,291 @@
+"""Python mirror of the reference's expert-dispatch surface over libgfr_moe.so (include/gfr_moe.h).
+
+Class names and call shapes follow glm-flash-rs: Grouping (src/grouping.rs:12-112), ExpertGpu (src/experts.rs:365-564),
+FastExperts (src/fast_experts.rs:27-208), Moe (src/moe.rs:1-183). Device memory and streams come from PyTorch-ROCm
+(plumbing only); every computation runs in the HIP library. Importing this module on a machine without the built
+library raises: there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libgfr_moe.so")
+
+GFR_EINVAL = -1
+
+
+class GfrError(RuntimeError):
+    """A failed library call: code < 0 is a precondition (the reference's ensure!), code > 0 a hipError_t."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"gfr error {code}: {msg}")
+        self.code = code
+
+
+def _load() -> ctypes.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+    lib = ctypes.CDLL(LIB_PATH)
+    P, I, VP = ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p
+    sig = {
+        "gfr_last_error": ([], ctypes.c_char_p),
+        "gfr_version": ([], ctypes.c_char_p),
+        "gfr_grouping_create": ([ctypes.POINTER(VP), I, I, I], I),
+        "gfr_grouping_run": ([VP, P, P, I], I),
+        "gfr_grouping_ids": ([VP], P),
+        "gfr_grouping_count": ([VP], P),
+        "gfr_grouping_members": ([VP], P),
+        "gfr_grouping_destroy": ([VP], I),
+        "gfr_experts_create": ([ctypes.POINTER(VP), I, I, I, I, I], I),
+        "gfr_experts_run_rows": ([VP, P, P, P, I, P, P, P, P, I, I], I),
+        "gfr_experts_y": ([VP], P),
+        "gfr_experts_xd": ([VP], P),
+        "gfr_experts_destroy": ([VP], I),
+        "gfr_fast_experts_create": ([ctypes.POINTER(VP), I, I, I, I, I, I], I),
+        "gfr_fast_experts_run": ([VP, P, P, P, I, P, P, P, P, I, I, I], I),
+        "gfr_fast_experts_output": ([VP], P),
+        "gfr_fast_experts_xd": ([VP], P),
+        "gfr_fast_experts_destroy": ([VP], I),
+        "gfr_moe_create": ([ctypes.POINTER(VP), I, I, I, I, I], I),
+        "gfr_moe_run": ([VP, P, P, P, P, I], I),
+        "gfr_moe_output": ([VP], P),
+        "gfr_moe_picks": ([VP], P),
+        "gfr_moe_weights": ([VP], P),
+        "gfr_moe_set_decode_rows": ([VP, I], I),
+        "gfr_moe_destroy": ([VP], I),
+        "gfr_linear_create": ([ctypes.POINTER(VP), I, I, I], I),
+        "gfr_linear_run": ([VP, P, P, P, P, P, P], I),
+        "gfr_linear_destroy": ([VP], I),
+        "gfr_exl3_decode_tiles": ([P, P, I, I, I, P], I),
+    }
+    for name, (args, res) in sig.items():
+        f = getattr(lib, name)
+        f.argtypes = args
+        f.restype = res
+    return lib
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        _lib = _load()
+    return _lib
+
+
+def _check(rc: int):
+    if rc != 0:
+        raise GfrError(rc, lib().gfr_last_error().decode())
+
+
+def _ptr(t) -> int:
+    return 0 if t is None else t.data_ptr()
+
+
+def _stream(stream=None) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+class _DeviceArray:
+    """__cuda_array_interface__ over library-owned device memory."""
+
+    def __init__(self, ptr: int, shape, typestr: str):
+        self.__cuda_array_interface__ = {"shape": tuple(shape), "typestr": typestr, "data": (ptr, False),
+                                         "version": 3, "strides": None}
+
+
+_TYPESTR = {torch.float32: "<f4", torch.int32: "<i4", torch.float16: "<f2"}
+
+
+def _view(ptr: int, shape, dtype, device) -> torch.Tensor:
+    """A torch tensor over library-owned device memory (no copy; valid while the engine lives)."""
+    t = torch.as_tensor(_DeviceArray(ptr, shape, _TYPESTR[dtype]), device=device)
+    assert t.data_ptr() == ptr
+    return t
+
+
+@dataclass
+class Exl3Experts:
+    """One layer's EXL3 expert tensors (the reference's weights.layers[L].moe.experts.*, experts.rs:146-156).
+
+    gt, ut: [E, hidden/16, inter/16, 8*bits] int32; dt: [E, inter/16, hidden/16, 8*bits] int32;
+    suh_g, suh_u, svh_d: [E, hidden] fp16; suh_d, svh_g, svh_u: [E, inter] fp16.
+    """
+
+    gt: torch.Tensor
+    ut: torch.Tensor
+    dt: torch.Tensor
+    suh_g: torch.Tensor
+    suh_u: torch.Tensor
+    suh_d: torch.Tensor
+    svh_g: torch.Tensor
+    svh_u: torch.Tensor
+    svh_d: torch.Tensor
+    bits: int
+
+    @property
+    def experts(self) -> int:
+        return self.gt.shape[0]
+
+    @property
+    def hidden(self) -> int:
+        return self.suh_g.shape[1]
+
+    @property
+    def inter(self) -> int:
+        return self.suh_d.shape[1]
+
+    def check(self):
+        E, D, N, b = self.experts, self.hidden, self.inter, self.bits
+        want = {
+            "gt": ((E, D // 16, N // 16, 8 * b), torch.int32), "ut": ((E, D // 16, N // 16, 8 * b), torch.int32),
+            "dt": ((E, N // 16, D // 16, 8 * b), torch.int32),
+            "suh_g": ((E, D), torch.float16), "suh_u": ((E, D), torch.float16), "svh_d": ((E, D), torch.float16),
+            "suh_d": ((E, N), torch.float16), "svh_g": ((E, N), torch.float16), "svh_u": ((E, N), torch.float16),
+        }
+        for name, (shape, dtype) in want.items():
+            t = getattr(self, name)
+            if tuple(t.shape) != shape or t.dtype != dtype or not t.is_contiguous() or t.device.type != "cuda":
+                raise ValueError(f"{name}: {tuple(t.shape)} {t.dtype}, want {shape} {dtype} contiguous on GPU")
+
+    def struct(self) -> "_Exl3Struct":
+        self.check()
+        return _Exl3Struct(self.experts, self.hidden, self.inter, self.bits, *(
+            _ptr(getattr(self, n)) for n in ("gt", "ut", "dt", "suh_g", "suh_u", "suh_d", "svh_g", "svh_u", "svh_d")))
+
+
+class _Exl3Struct(ctypes.Structure):
+    _fields_ = [("experts", ctypes.c_int), ("hidden", ctypes.c_int), ("inter", ctypes.c_int), ("bits", ctypes.c_int)] + [
+        (n, ctypes.c_void_p) for n in ("gt", "ut", "dt", "suh_g", "suh_u", "suh_d", "svh_g", "svh_u", "svh_d")]
+
+
+class _Engine:
+    _destroy = None
+
+    def __init__(self):
+        self._h = ctypes.c_void_p()
+
+    def close(self):
+        if self._h:
+            getattr(lib(), self._destroy)(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Grouping(_Engine):
+    """Grouping::new / run (grouping.rs:29-112). ids, count, members are views of the engine's buffers."""
+
+    _destroy = "gfr_grouping_destroy"
+
+    def __init__(self, experts: int, slots: int, max_rows: int, device="cuda"):
+        super().__init__()
+        _check(lib().gfr_grouping_create(ctypes.byref(self._h), experts, slots, max_rows))
+        self.experts, self.slots, self.max_rows = experts, slots, max_rows
+        L = lib()
+        self.ids = _view(L.gfr_grouping_ids(self._h), (experts,), torch.int32, device)
+        self.count = _view(L.gfr_grouping_count(self._h), (1,), torch.int32, device)
+        self.members = _view(L.gfr_grouping_members(self._h), (experts, max_rows), torch.int32, device)
+
+    def run(self, picks: torch.Tensor, rows: int, stream=None):
+        if picks.dtype != torch.int32 or not picks.is_contiguous():
+            raise ValueError("picks must be contiguous int32")
+        _check(lib().gfr_grouping_run(self._h, _stream(stream), _ptr(picks), rows))
+
+
+class ExpertGpu(_Engine):
+    """ExpertGpu::with_policy / run_rows (experts.rs:385-563); y: [max_rows * slots, hidden] fp32."""
+
+    _destroy = "gfr_experts_destroy"
+
+    def __init__(self, hidden: int, inter: int, slots: int, exl3_slots: int, max_rows: int, device="cuda"):
+        super().__init__()
+        _check(lib().gfr_experts_create(ctypes.byref(self._h), hidden, inter, slots, exl3_slots, max_rows))
+        self.hidden, self.inter, self.slots, self.max_rows = hidden, inter, slots, max_rows
+        P = max_rows * slots
+        self.y = _view(lib().gfr_experts_y(self._h), (P, hidden), torch.float32, device)
+        self.xd = _view(lib().gfr_experts_xd(self._h), (P, inter), torch.float16, device)
+
+    def run_rows(self, w: Exl3Experts, input: torch.Tensor, picks, ids, count, members, rows: int, maxm: int,
+                 stream=None):
+        if input.dtype != torch.bfloat16:
+            raise ValueError("input must be bf16 [rows, stride]")
+        ws = w.struct()
+        _check(lib().gfr_experts_run_rows(self._h, _stream(stream), ctypes.byref(ws), _ptr(input), input.stride(0),
+                                          _ptr(picks), _ptr(ids), _ptr(count), _ptr(members), rows, maxm))
+
+
+class FastExperts(_Engine):
+    """FastExperts::new / run (fast_experts.rs:43-208); output: [max_rows * slots, hidden] fp32."""
+
+    _destroy = "gfr_fast_experts_destroy"
+
+    def __init__(self, hidden: int, inter: int, slots: int, exl3_slots: int, experts: int, max_rows: int,
+                 device="cuda"):
+        super().__init__()
+        _check(lib().gfr_fast_experts_create(ctypes.byref(self._h), hidden, inter, slots, exl3_slots, experts,
+                                             max_rows))
+        P = max_rows * slots
+        self.output = _view(lib().gfr_fast_experts_output(self._h), (P, hidden), torch.float32, device)
+        self.xd = _view(lib().gfr_fast_experts_xd(self._h), (P, inter), torch.float16, device)
+
+    def run(self, w: Exl3Experts, input, picks, ids, count, members, rows: int, maxm: int, shared_x: bool,
+            stream=None):
+        ws = w.struct()
+        _check(lib().gfr_fast_experts_run(self._h, _stream(stream), ctypes.byref(ws), _ptr(input), input.stride(0),
+                                          _ptr(picks), _ptr(ids), _ptr(count), _ptr(members), rows, maxm,
+                                          int(shared_x)))
+
+
+class Moe(_Engine):
+    """Moe::run_prefetched (moe.rs:66-182) for the benchmark's router: softmax top-k + EXL3 shared expert."""
+
+    _destroy = "gfr_moe_destroy"
+
+    def __init__(self, hidden: int, inter: int, routed: int, topk: int, max_rows: int, device="cuda"):
+        super().__init__()
+        _check(lib().gfr_moe_create(ctypes.byref(self._h), hidden, inter, routed, topk, max_rows))
+        self.hidden, self.routed, self.topk, self.max_rows = hidden, routed, topk, max_rows
+        L = lib()
+        self.output = _view(L.gfr_moe_output(self._h), (max_rows, hidden), torch.float32, device)
+        self.picks = _view(L.gfr_moe_picks(self._h), (max_rows, topk + 1), torch.int32, device)
+        self.weights = _view(L.gfr_moe_weights(self._h), (max_rows, topk + 1), torch.float32, device)
+
+    def set_decode_rows(self, n: int):
+        _check(lib().gfr_moe_set_decode_rows(self._h, n))
+
+    def run(self, w: Exl3Experts, input: torch.Tensor, logits: torch.Tensor, rows: int, stream=None):
+        ws = w.struct()
+        _check(lib().gfr_moe_run(self._h, _stream(stream), ctypes.byref(ws), _ptr(input), _ptr(logits), rows))
+
+
+class Linear(_Engine):
+    """One EXL3 linear on one fp16 token (benchmark config 1)."""
+
+    _destroy = "gfr_linear_destroy"
+
+    def __init__(self, kin: int, n: int, bits: int):
+        super().__init__()
+        _check(lib().gfr_linear_create(ctypes.byref(self._h), kin, n, bits))
+
+    def run(self, x, trellis, suh, svh, y, stream=None):
+        _check(lib().gfr_linear_run(self._h, _stream(stream), _ptr(x), _ptr(trellis), _ptr(suh), _ptr(svh), _ptr(y)))
+
+
+def decode_tiles(trellis: torch.Tensor, kin: int, n: int, bits: int, stream=None) -> torch.Tensor:
+    """Decoded fp16 weights [kin, n] of one trellis matrix (bit-exact parity entry point)."""
+    out = torch.empty((kin, n), dtype=torch.float16, device=trellis.device)
+    _check(lib().gfr_exl3_decode_tiles(_stream(stream), _ptr(trellis), kin, n, bits, _ptr(out)))
+    return out

@@ -1,0 +1,128 @@
+/* gfr_moe -- MI355X (gfx950) EXL3 MoE-expert path behind a C ABI.
+ *
+ * Drop-in for the expert-dispatch surface of glm-flash-rs (paths relative to the reference repository):
+ *   Grouping            src/grouping.rs:12-112        -> gfr_grouping_*
+ *   ExpertGpu           src/experts.rs:365-564        -> gfr_experts_*       (decode / verify windows)
+ *   FastExperts         src/fast_experts.rs:27-208    -> gfr_fast_experts_*  (prefill chunks)
+ *   Moe::run_prefetched src/moe.rs:66-182             -> gfr_moe_*           (router .. combine)
+ * The reference binds its kernels through the CUDA driver (src/cuda.rs); a Rust caller binds these functions with
+ * `extern "C"` declarations instead (INTEGRATION.md shows the stubs).
+ *
+ * Conventions (src/cuda.rs:102-123, experts.rs:461-464):
+ *   - every function returns 0 on success, a negative GFR_E* code when a precondition fails, or a positive
+ *     hipError_t; gfr_last_error() gives the thread's last message;
+ *   - pointers are device addresses, fp16 / bf16 data travel as uint16_t bit patterns;
+ *   - engines allocate their scratch once at create (zeroed); run functions never allocate, free or synchronise,
+ *     are ordered on the caller's stream and can be captured into a HIP graph;
+ *   - one host thread per engine; calls that overlap on one engine race on its scratch.
+ */
+#ifndef GFR_MOE_H
+#define GFR_MOE_H
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GFR_OK 0
+#define GFR_EINVAL (-1)   /* argument outside the engine's bounds (the reference's ensure!) */
+#define GFR_ENOMEM (-2)
+#define GFR_EUNSUPPORTED (-3)
+
+/* One layer's EXL3 expert tensors, the reference's weights.layers[L].moe.experts.{gt,ut,dt,suh_*,svh_*}
+ * (experts.rs:146-156, prepared.rs:369-377), generalised to any shape and bit width:
+ *   gt, ut  [experts][hidden/16][inter/16][8*bits] uint32   (gate, up:  hidden -> inter)
+ *   dt      [experts][inter/16][hidden/16][8*bits] uint32   (down:      inter -> hidden)
+ *   suh_g, suh_u [experts][hidden], suh_d, svh_g, svh_u [experts][inter], svh_d [experts][hidden]   fp16
+ * `experts` counts every EXL3 expert, the shared one included when it is EXL3 (then it is the last index). */
+typedef struct gfr_exl3_experts {
+    int experts;
+    int hidden;
+    int inter;
+    int bits; /* 2, 3, 4 or 5 */
+    const uint32_t* gt;
+    const uint32_t* ut;
+    const uint32_t* dt;
+    const uint16_t* suh_g;
+    const uint16_t* suh_u;
+    const uint16_t* suh_d;
+    const uint16_t* svh_g;
+    const uint16_t* svh_u;
+    const uint16_t* svh_d;
+} gfr_exl3_experts;
+
+const char* gfr_last_error(void);
+/* Library version string. */
+const char* gfr_version(void);
+
+/* ---- Grouping (grouping.rs:12-112) ---------------------------------------------------------------------------
+ * picks [rows][slots] int32 expert ids in [0, experts). After run: *count = distinct experts, ids[u] ascending,
+ * members[u * max_rows + i] = r * 32 + slot (rows ascending, the first slot of the expert in the row), -1 padded;
+ * members rows u in [count, experts) all -1. slots <= 32. */
+typedef struct gfr_grouping gfr_grouping;
+int gfr_grouping_create(gfr_grouping** out, int experts, int slots, int max_rows);  /* Grouping::new  :29-50 */
+int gfr_grouping_run(gfr_grouping* g, hipStream_t stream, const int32_t* picks, int rows); /* Grouping::run :51-112 */
+int32_t* gfr_grouping_ids(const gfr_grouping* g);      /* [experts]            (Grouping.ids)     */
+int32_t* gfr_grouping_count(const gfr_grouping* g);    /* [1]                  (Grouping.count)   */
+int32_t* gfr_grouping_members(const gfr_grouping* g);  /* [experts][max_rows]  (Grouping.members) */
+int gfr_grouping_destroy(gfr_grouping* g);
+
+/* ---- Decode / verify experts (ExpertGpu, experts.rs:365-564) -------------------------------------------------
+ * slots = picks per row (routed + shared); the first exl3_slots slots are EXL3 experts (the reference:
+ * slots - 1, its shared expert is FP8; the benchmark configs: slots, the shared expert is EXL3).
+ * run_rows: input [rows][input_stride] bf16; picks [rows][slots]; ids / count / members from a gfr_grouping with
+ * member stride maxm. Output gfr_experts_y: [rows * slots][hidden] fp32 (pairs with slot >= exl3_slots untouched).
+ * Bounds: 0 < rows <= max_rows, rows <= maxm <= max_rows, max_rows <= 64. */
+typedef struct gfr_experts gfr_experts;
+int gfr_experts_create(gfr_experts** out, int hidden, int inter, int slots, int exl3_slots, int max_rows);
+int gfr_experts_run_rows(gfr_experts* ex, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
+                         int input_stride, const int32_t* picks, const int32_t* ids, const int32_t* count,
+                         const int32_t* members, int rows, int maxm);  /* ExpertGpu::run_rows :447-563 */
+float* gfr_experts_y(const gfr_experts* ex);
+uint16_t* gfr_experts_xd(const gfr_experts* ex);   /* [rows * slots][inter] fp16, the down projection's input */
+int gfr_experts_destroy(gfr_experts* ex);
+
+/* ---- Prefill experts (FastExperts, fast_experts.rs:27-208) ---------------------------------------------------
+ * Same inputs as run_rows for a chunk of up to max_rows rows; the grouped GEMM runs on fp16 MFMA with one
+ * full-K accumulation chain per output. shared_x != 0 asserts suh_g == suh_u (one rotated copy of the rows).
+ * Output gfr_fast_experts_output: [rows * slots][hidden] fp32; gfr_fast_experts_xd [rows * slots][inter] fp16. */
+typedef struct gfr_fast_experts gfr_fast_experts;
+int gfr_fast_experts_create(gfr_fast_experts** out, int hidden, int inter, int slots, int exl3_slots, int experts,
+                            int max_rows);                                          /* FastExperts::new :43-64 */
+int gfr_fast_experts_run(gfr_fast_experts* fx, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
+                         int input_stride, const int32_t* picks, const int32_t* ids, const int32_t* count,
+                         const int32_t* members, int rows, int maxm, int shared_x);  /* FastExperts::run :91-208 */
+float* gfr_fast_experts_output(const gfr_fast_experts* fx);
+uint16_t* gfr_fast_experts_xd(const gfr_fast_experts* fx);
+int gfr_fast_experts_destroy(gfr_fast_experts* fx);
+
+/* ---- One MoE layer (Moe::run_prefetched, moe.rs:66-182) ------------------------------------------------------
+ * logits [rows][routed] fp32 router logits -> softmax top-k (renormalised) + the shared expert (id `routed`, EXL3,
+ * weight 1) -> grouping -> experts (decode path for rows <= decode_rows, prefill path above) -> combine ->
+ * output [rows][hidden] fp32. The weights hold routed + 1 experts. */
+typedef struct gfr_moe gfr_moe;
+int gfr_moe_create(gfr_moe** out, int hidden, int inter, int routed, int topk, int max_rows);  /* Moe::new :23-64 */
+int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
+                const float* logits, int rows);                                 /* Moe::run_prefetched :66-182 */
+float* gfr_moe_output(const gfr_moe* m);
+int32_t* gfr_moe_picks(const gfr_moe* m);        /* [rows][topk + 1] */
+float* gfr_moe_weights(const gfr_moe* m);        /* [rows][topk + 1] */
+int gfr_moe_set_decode_rows(gfr_moe* m, int decode_rows);  /* rows at or below run the decode path (default 64) */
+int gfr_moe_destroy(gfr_moe* m);
+
+/* ---- Single EXL3 linear (benchmark config 1; the decode path's GEMV with rot_in / down-epilogue formulas) ----
+ * y [n] fp32 = svh * had(W^T xh) / sqrt(128), xh = fp16(had(x * suh) / sqrt(128)), x [kin] fp16. */
+typedef struct gfr_linear gfr_linear;
+int gfr_linear_create(gfr_linear** out, int kin, int n, int bits);
+int gfr_linear_run(gfr_linear* l, hipStream_t stream, const uint16_t* x, const uint32_t* trellis,
+                   const uint16_t* suh, const uint16_t* svh, float* y);
+int gfr_linear_destroy(gfr_linear* l);
+
+/* ---- Debug / parity: decoded fp16 weights of one matrix [kin][n] (row = k), bit-exact to experts.rs:47-74 ---- */
+int gfr_exl3_decode_tiles(hipStream_t stream, const uint32_t* trellis, int kin, int n, int bits, uint16_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,75 @@
+"""The C-ABI library loads and exports every symbol include/gfr_moe.h declares; argument checks run on the host
+before any device call (no GPU needed)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gfr_moe.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gfr_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_reference_surface():
+    names = declared()
+    for must in ["gfr_grouping_create", "gfr_grouping_run", "gfr_experts_run_rows", "gfr_fast_experts_run",
+                 "gfr_moe_run", "gfr_exl3_decode_tiles", "gfr_last_error"]:
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    import gfr_moe
+    lib = ctypes.CDLL(gfr_moe.LIB_PATH)
+    missing = [n for n in declared() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_version_and_error_string():
+    import gfr_moe
+    assert b"gfx950" in gfr_moe.lib().gfr_version()
+
+
+@pytest.mark.parametrize("args,needle", [
+    ((0, 9, 16), "grouping experts"), ((289, 0, 16), "grouping slots"), ((289, 33, 16), "grouping slots"),
+    ((289, 9, 0), "grouping capacity"),
+])
+def test_grouping_create_rejects(args, needle):
+    import gfr_moe
+    h = ctypes.c_void_p()
+    rc = gfr_moe.lib().gfr_grouping_create(ctypes.byref(h), *args)
+    assert rc == gfr_moe.GFR_EINVAL and not h
+    assert needle in gfr_moe.lib().gfr_last_error().decode()
+
+
+@pytest.mark.parametrize("args,needle", [
+    ((2048, 1536, 5, 5, 65), "scratch bound"), ((2048, 1500, 5, 5, 1), "multiples"), ((2048, 1536, 5, 6, 1), "slots"),
+])
+def test_experts_create_rejects(args, needle):
+    import gfr_moe
+    h = ctypes.c_void_p()
+    rc = gfr_moe.lib().gfr_experts_create(ctypes.byref(h), *args)
+    assert rc == gfr_moe.GFR_EINVAL and needle in gfr_moe.lib().gfr_last_error().decode()
+
+
+def test_run_rejects_null_engine():
+    import gfr_moe
+    L = gfr_moe.lib()
+    assert L.gfr_grouping_run(None, None, None, 1) == gfr_moe.GFR_EINVAL
+    assert L.gfr_experts_run_rows(None, None, None, None, 0, None, None, None, None, 1, 1) == gfr_moe.GFR_EINVAL
+    assert L.gfr_moe_run(None, None, None, None, None, 1) == gfr_moe.GFR_EINVAL
+    assert L.gfr_exl3_decode_tiles(None, None, 16, 16, 4, None) == gfr_moe.GFR_EINVAL
+
+
+def test_moe_create_rejects():
+    import gfr_moe
+    h = ctypes.c_void_p()
+    L = gfr_moe.lib()
+    assert L.gfr_moe_create(ctypes.byref(h), 2048, 1536, 64, 0, 1) == gfr_moe.GFR_EINVAL
+    assert L.gfr_moe_create(ctypes.byref(h), 2048, 1536, 64, 65, 1) == gfr_moe.GFR_EINVAL
+    assert L.gfr_moe_create(ctypes.byref(h), 2048, 1536, 2000, 4, 1) == gfr_moe.GFR_EINVAL

@@ -1,0 +1,203 @@
+"""Decode / verify path on the GPU against the CPU oracle: decoded weights bit-exact, grouping bit-exact, layer
+outputs within the north star's 1e-2 relative (plus the reference probe's 1e-3 relative RMS, experts.rs:304-308)."""
+import numpy as np
+import pytest
+import torch
+
+from refs import DecodedExperts, assert_close, np_u16, np_u32
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5])
+def test_decode_tiles_bitexact(gfr, oracle, bits):
+    import synth
+    kin, n = 64, 384
+    w = synth.trellis((kin // 16, n // 16, 8 * bits), 77 + bits)
+    w[0, 0].zero_()
+    w[0, 1].fill_(-1)
+    w[1, 2].zero_()
+    w[1, 2, 3] = 1 << 7
+    got = np_u16(gfr.decode_tiles(w, kin, n, bits))
+    torch.cuda.synchronize()
+    want = oracle.unpack(np_u32(w), kin, n, bits)
+    assert np.array_equal(got, want), f"{np.sum(got != want)} of {got.size} decoded weights differ"
+
+
+def _xorshift_picks(rows, concentrated, seed):
+    M = (1 << 64) - 1
+    picks = []
+    for r in range(rows):
+        seed ^= (seed << 13) & M
+        seed ^= seed >> 7
+        seed ^= (seed << 17) & M
+        start = 0 if concentrated else seed % 288
+        picks.append([(288 if s == 8 else (start + s * 37) % 288) for s in range(9)])
+    return np.array(picks, np.int32), seed
+
+
+@pytest.mark.parametrize("capacity,row_counts", [
+    (8192, [8192, 1, 2, 31, 32, 33, 63, 64, 65, 129, 1024, 4097, 8191, 8192]),
+    (16, [1, 2, 3, 8, 15, 16]),
+])
+def test_grouping_reference_probe(gfr, oracle, capacity, row_counts):
+    """grouping.rs:123-215: seeded xorshift64 routing, poisoned outputs, exact count / ids / full members table,
+    graph replays."""
+    g = gfr.Grouping(289, 9, capacity)
+    seed = 0x0123456789ABCDEF
+    for rows in row_counts:
+        for concentrated in (True, False):
+            p, seed = _xorshift_picks(rows, concentrated, seed)
+            picks = torch.from_numpy(p).cuda()
+            c, ids, mem = oracle.group(p, rows, 9, 289, capacity)
+            g.ids.fill_(-77)
+            g.members.fill_(12345)
+            g.run(picks, rows)
+            torch.cuda.synchronize()
+
+            def check():
+                assert int(g.count.item()) == c, (rows, concentrated)
+                assert np.array_equal(g.ids[:c].cpu().numpy(), ids), (rows, concentrated)
+                assert np.array_equal(g.members.cpu().numpy(), mem), (rows, concentrated)
+
+            check()
+            if rows in (1, 65, 4097):
+                graph = torch.cuda.CUDAGraph()
+                s = torch.cuda.Stream()
+                with torch.cuda.stream(s):
+                    g.run(picks, rows, stream=s)   # warm
+                    s.synchronize()
+                    with torch.cuda.graph(graph, stream=s):
+                        g.run(picks, rows, stream=s)
+                for _ in range(3):
+                    g.members.fill_(12345)
+                    torch.cuda.synchronize()
+                    graph.replay()
+                    torch.cuda.synchronize()
+                    check()
+
+
+@pytest.mark.parametrize("E,slots,rows", [(65, 5, 1), (65, 5, 32), (161, 9, 16384), (65, 5, 8192), (161, 9, 300)])
+def test_grouping_benchmark_shapes(gfr, oracle, E, slots, rows):
+    import synth
+    lg = synth.zipf_logits(rows, E - 1, slots - 1, 1.1, seed=rows + E) if rows <= 2048 else synth.logits(rows, E - 1, 5)
+    p, _ = oracle.route(lg.cpu().numpy(), slots - 1, E - 1)
+    g = gfr.Grouping(E, slots, rows)
+    g.run(torch.from_numpy(p).cuda(), rows)
+    torch.cuda.synchronize()
+    c, ids, mem = oracle.group(p, rows, slots, E, rows)
+    assert int(g.count.item()) == c
+    assert np.array_equal(g.ids[:c].cpu().numpy(), ids)
+    assert np.array_equal(g.members.cpu().numpy(), mem)
+
+
+def test_linear_config1(gfr, oracle):
+    """one EXL3 linear 2048 -> 1536, K = 4, one fp16 token."""
+    import synth
+    kin, n, bits = 2048, 1536, 4
+    t = synth.trellis((kin // 16, n // 16, 8 * bits), 11)
+    suh, svh = synth.scales((kin,), 12), synth.scales((n,), 13)
+    x = torch.randn(kin, generator=torch.Generator(device="cuda").manual_seed(14), device="cuda").half()
+    y = torch.empty(n, device="cuda")
+    lin = gfr.Linear(kin, n, bits)
+    lin.run(x, t, suh, svh, y)
+    torch.cuda.synchronize()
+    want = oracle.linear(np_u16(x), oracle.unpack_f32(np_u32(t), kin, n, bits), np_u16(suh), np_u16(svh))
+    assert_close(y.cpu().numpy(), want, what="linear")
+
+
+def _moe_inputs(E_routed, D, N, bits, rows, topk, seed, zipf=False):
+    import synth
+    w = synth.experts(E_routed + 1, D, N, bits, seed=seed)
+    x = synth.activations(rows, D, seed + 100)
+    lg = synth.zipf_logits(rows, E_routed, topk, 1.1, seed + 200) if zipf else synth.logits(rows, E_routed, seed + 200)
+    return w, x, lg
+
+
+@pytest.mark.parametrize("rows,zipf", [(1, False), (4, True)])
+def test_experts_run_rows_vs_oracle(gfr, oracle, rows, zipf):
+    """ExpertGpu::run_rows at the C2 / C3 shape (hidden 2048, inter 1536, 64 + 1 EXL3 experts, top-4 + shared)."""
+    E, D, N, bits, topk = 64, 2048, 1536, 4, 4
+    slots = topk + 1
+    w, x, lg = _moe_inputs(E, D, N, bits, rows, topk, 31 + rows, zipf)
+    p, _ = oracle.route(lg.cpu().numpy(), topk, E)
+    picks = torch.from_numpy(p).cuda()
+    g = gfr.Grouping(E + 1, slots, 16)
+    ex = gfr.ExpertGpu(D, N, slots, slots, 16)
+    g.run(picks, rows)
+    ex.run_rows(w, x, picks, g.ids, g.count, g.members, rows, 16)
+    torch.cuda.synchronize()
+    y = ex.y.cpu().numpy()
+    dec = DecodedExperts(oracle, w)
+    xb = np_u16(x)
+    for r in range(rows):
+        for s in range(slots):
+            want, _ = dec.row(xb[r], int(p[r, s]))
+            assert_close(y[r * slots + s], want, what=f"row {r} slot {s} expert {p[r, s]}")
+
+
+def test_batched_rows_equal_serial_rows(gfr, oracle):
+    """window_experts_probe.rs:14-188: a 16-row batched run is byte-identical to per-row runs (row independence),
+    for identical, partially overlapping and disjoint routing."""
+    E, D, N, bits, topk = 64, 2048, 1536, 4, 4
+    slots = topk + 1
+    w, x, _ = _moe_inputs(E, D, N, bits, 16, topk, 5)
+    g = gfr.Grouping(E + 1, slots, 16)
+    ex = gfr.ExpertGpu(D, N, slots, slots, 16)
+    one_g = gfr.Grouping(E + 1, slots, 1)
+    one = gfr.ExpertGpu(D, N, slots, slots, 1)
+    for pattern in range(3):
+        p = np.array([[(s * 13 + (0 if pattern == 0 else r * 13 if pattern == 1 else r * 4)) % E for s in range(topk)]
+                      + [E] for r in range(16)], np.int32)
+        picks = torch.from_numpy(p).cuda()
+        for rows in (1, 2, 7, 16):
+            g.run(picks, rows)
+            ex.run_rows(w, x, picks, g.ids, g.count, g.members, rows, 16)
+            batched = ex.y[:rows * slots].clone()
+            for r in range(rows):
+                pr = picks[r:r + 1].contiguous()
+                one_g.run(pr, 1)
+                one.run_rows(w, x[r:r + 1], pr, one_g.ids, one_g.count, one_g.members, 1, 1)
+                assert torch.equal(one.y[:slots], batched[r * slots:(r + 1) * slots]), (pattern, rows, r)
+
+
+def test_experts_graph_replay_bytes(gfr):
+    E, D, N, bits, topk = 64, 2048, 1536, 4, 4
+    slots = topk + 1
+    w, x, lg = _moe_inputs(E, D, N, bits, 3, topk, 8)
+    picks = torch.tensor([[1, 5, 9, 33, 64], [5, 2, 9, 40, 64], [63, 0, 1, 2, 64]], dtype=torch.int32, device="cuda")
+    g = gfr.Grouping(E + 1, slots, 4)
+    ex = gfr.ExpertGpu(D, N, slots, slots, 4)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        g.run(picks, 3, stream=s)
+        ex.run_rows(w, x, picks, g.ids, g.count, g.members, 3, 4, stream=s)
+        s.synchronize()
+        eager = ex.y.clone()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            g.run(picks, 3, stream=s)
+            ex.run_rows(w, x, picks, g.ids, g.count, g.members, 3, 4, stream=s)
+    for _ in range(3):
+        ex.y.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ex.y, eager)
+
+
+def test_moe_layer_decode_vs_oracle(gfr, oracle):
+    """Moe layer, config 2 (bs = 1 decode): router -> grouping -> experts -> combine."""
+    E, D, N, bits, topk = 64, 2048, 1536, 4, 4
+    w, x, lg = _moe_inputs(E, D, N, bits, 1, topk, 21)
+    m = gfr.Moe(D, N, E, topk, 1)
+    m.run(w, x, lg, 1)
+    torch.cuda.synchronize()
+    p, wt = oracle.route(lg.cpu().numpy(), topk, E)
+    assert np.array_equal(m.picks.cpu().numpy(), p)
+    np.testing.assert_allclose(m.weights.cpu().numpy(), wt, rtol=1e-6)
+    dec = DecodedExperts(oracle, w)
+    xb = np_u16(x)
+    ys = np.stack([dec.row(xb[0], int(e))[0] for e in p[0]])
+    want = oracle.combine(ys, wt, 1, topk + 1)
+    assert_close(m.output.cpu().numpy(), want, what="moe output")
