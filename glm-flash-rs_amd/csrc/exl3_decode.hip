@@ -88,8 +88,8 @@ __global__ void __launch_bounds__(64) rot_in_kernel(const uint16_t* __restrict__
 // Grouped trellis GEMV. Program (distinct expert u, 128-column block cb, mat * SK + split): the members of expert
 // uids[u] (rows of X, RB at a time) times W_q[mat] over k tiles [split * NW * KTW, (split + 1) * NW * KTW) for the
 // block's 128 columns; wave w owns k tiles split * NW * KTW + w * KTW + [0, KTW).
-// Z[((mat * SK + split) * P + pair) * N + n].
-template <int K, int KTW, int NW, int RB>
+// Z[((mat * SK + split) * P + pair) * N + n]. MATS = 2 (gate + up) or 1 (down): separate kernels for the profiler.
+template <int K, int KTW, int NW, int RB, int MATS>
 __global__ void __launch_bounds__(NW * 64) gemv_kernel(
     const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1, const uint32_t* __restrict__ T0,
     const uint32_t* __restrict__ T1, const int* __restrict__ uids, const int* __restrict__ ucount,
@@ -106,7 +106,7 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(
     if (u >= ucount[0]) return;
     const int e = uids[u];
     if (e >= E) return;                          // not an EXL3 expert
-    const int cb = blockIdx.y, split = blockIdx.z % SK, mat = blockIdx.z / SK;
+    const int cb = blockIdx.y, split = blockIdx.z % SK, mat = MATS == 1 ? 0 : blockIdx.z / SK;
     const uint16_t* __restrict__ X = mat ? X1 : X0;
     const uint32_t* __restrict__ T = mat ? T1 : T0;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, t = lane >> 3, i = lane & 7;
@@ -287,18 +287,18 @@ static int gemv_ktw(int Kin) {
 
 int gemv_splits(int Kin) { return Kin / 16 / (GEMV_NW * gemv_ktw(Kin)); }
 
-template <int K>
+template <int K, int MATS>
 static void gemv_dispatch(int ktw, dim3 grid, hipStream_t s, const uint16_t* X0, const uint16_t* X1,
                           const uint32_t* T0, const uint32_t* T1, const int* uids, const int* ucount,
                           const int* members, float* Z, int Kin, int N, int P, int SK, int maxm, int slots, int E) {
     if (ktw == 4)
-        gemv_kernel<K, 4, GEMV_NW, GEMV_RB><<<grid, GEMV_NW * 64, 0, s>>>(X0, X1, T0, T1, uids, ucount, members, Z,
+        gemv_kernel<K, 4, GEMV_NW, GEMV_RB, MATS><<<grid, GEMV_NW * 64, 0, s>>>(X0, X1, T0, T1, uids, ucount, members, Z,
                                                                           Kin, N, P, SK, maxm, slots, E);
     else if (ktw == 2)
-        gemv_kernel<K, 2, GEMV_NW, GEMV_RB><<<grid, GEMV_NW * 64, 0, s>>>(X0, X1, T0, T1, uids, ucount, members, Z,
+        gemv_kernel<K, 2, GEMV_NW, GEMV_RB, MATS><<<grid, GEMV_NW * 64, 0, s>>>(X0, X1, T0, T1, uids, ucount, members, Z,
                                                                           Kin, N, P, SK, maxm, slots, E);
     else
-        gemv_kernel<K, 1, GEMV_NW, GEMV_RB><<<grid, GEMV_NW * 64, 0, s>>>(X0, X1, T0, T1, uids, ucount, members, Z,
+        gemv_kernel<K, 1, GEMV_NW, GEMV_RB, MATS><<<grid, GEMV_NW * 64, 0, s>>>(X0, X1, T0, T1, uids, ucount, members, Z,
                                                                           Kin, N, P, SK, maxm, slots, E);
 }
 
@@ -307,11 +307,21 @@ hipError_t launch_gemv(hipStream_t s, const uint16_t* X0, const uint16_t* X1, co
                        int maxm, int slots, int E, int bits, int mats, int maxu) {
     const int ktw = gemv_ktw(Kin), SK = gemv_splits(Kin);
     const dim3 grid(maxu, N / 128, mats * SK);
+    if (mats == 2) {
+        switch (bits) {
+            case 2: gemv_dispatch<2, 2>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
+            case 3: gemv_dispatch<3, 2>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
+            case 4: gemv_dispatch<4, 2>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
+            case 5: gemv_dispatch<5, 2>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     switch (bits) {
-        case 2: gemv_dispatch<2>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
-        case 3: gemv_dispatch<3>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
-        case 4: gemv_dispatch<4>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
-        case 5: gemv_dispatch<5>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
+        case 2: gemv_dispatch<2, 1>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
+        case 3: gemv_dispatch<3, 1>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
+        case 4: gemv_dispatch<4, 1>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
+        case 5: gemv_dispatch<5, 1>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -267,6 +267,28 @@ int gfr_linear_destroy(gfr_linear* l) {
     return 0;
 }
 
+// ---- grouped GEMV alone ---------------------------------------------------------------------------------------
+int gfr_exl3_gemv_splits(int kin) {
+    if (kin <= 0 || kin % 64) return fail(GFR_EINVAL, "kin %d not a positive multiple of 64", kin);
+    return gfr::gemv_splits(kin);
+}
+
+int gfr_exl3_grouped_gemv(hipStream_t stream, const uint16_t* x0, const uint16_t* x1, const uint32_t* t0,
+                          const uint32_t* t1, const int32_t* uids, const int32_t* ucount, const int32_t* members,
+                          float* z, int kin, int n, int pairs, int maxm, int slots, int experts, int bits, int mats,
+                          int maxu) {
+    if (!x0 || !t0 || !uids || !ucount || !members || !z || (mats == 2 && (!x1 || !t1)))
+        return fail(GFR_EINVAL, "null argument");
+    if (kin <= 0 || kin % 64 || n <= 0 || n % 128) return fail(GFR_EINVAL, "kin %d / n %d", kin, n);
+    if (bits < 2 || bits > 5 || (mats != 1 && mats != 2)) return fail(GFR_EINVAL, "bits %d / mats %d", bits, mats);
+    if (pairs <= 0 || maxm <= 0 || slots <= 0 || slots > 32 || experts <= 0 || maxu <= 0)
+        return fail(GFR_EINVAL, "pairs %d maxm %d slots %d experts %d maxu %d", pairs, maxm, slots, experts, maxu);
+    hipError_t e = gfr::launch_gemv(stream, x0, x1 ? x1 : x0, t0, t1 ? t1 : t0, uids, ucount, members, z, kin, n,
+                                    pairs, maxm, slots, experts, bits, mats, maxu);
+    if (e != hipSuccess) return hip_fail(e, "grouped gemv");
+    return 0;
+}
+
 // ---- debug decode -----------------------------------------------------------------------------------------------
 int gfr_exl3_decode_tiles(hipStream_t stream, const uint32_t* trellis, int kin, int n, int bits, uint16_t* out) {
     if (!trellis || !out) return fail(GFR_EINVAL, "null argument");

@@ -62,6 +62,8 @@ def _load() -> ctypes.CDLL:
         "gfr_linear_run": ([VP, P, P, P, P, P, P], I),
         "gfr_linear_destroy": ([VP], I),
         "gfr_exl3_decode_tiles": ([P, P, I, I, I, P], I),
+        "gfr_exl3_gemv_splits": ([I], I),
+        "gfr_exl3_grouped_gemv": ([P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I], I),
     }
     for name, (args, res) in sig.items():
         f = getattr(lib, name)

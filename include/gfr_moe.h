@@ -119,6 +119,17 @@ int gfr_linear_run(gfr_linear* l, hipStream_t stream, const uint16_t* x, const u
                    const uint16_t* suh, const uint16_t* svh, float* y);
 int gfr_linear_destroy(gfr_linear* l);
 
+/* ---- The grouped trellis GEMV alone (exl3.cu:145-170 / :325-330, exl3_grouped_8_4) -------------------------
+ * Z[((mat * SK + split) * P + pair) * N + n] = sum over split's k of X_mat[pair][k] * W_mat[uids[u]][k][n] for every
+ * member pair of every distinct expert u < *ucount with uids[u] < experts; mats = 2 (X0/T0 gate, X1/T1 up) or 1.
+ * X [P][kin] fp16 (rotated rows), trellis [experts][kin/16][n/16][8*bits]. SK = gfr_exl3_gemv_splits(kin) is fixed
+ * by kin, so a row's result never depends on the other rows. maxu = grid bound on distinct experts. */
+int gfr_exl3_gemv_splits(int kin);
+int gfr_exl3_grouped_gemv(hipStream_t stream, const uint16_t* x0, const uint16_t* x1, const uint32_t* t0,
+                          const uint32_t* t1, const int32_t* uids, const int32_t* ucount, const int32_t* members,
+                          float* z, int kin, int n, int pairs, int maxm, int slots, int experts, int bits, int mats,
+                          int maxu);
+
 /* ---- Debug / parity: decoded fp16 weights of one matrix [kin][n] (row = k), bit-exact to experts.rs:47-74 ---- */
 int gfr_exl3_decode_tiles(hipStream_t stream, const uint32_t* trellis, int kin, int n, int bits, uint16_t* out);
 

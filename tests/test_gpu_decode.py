@@ -201,3 +201,57 @@ def test_moe_layer_decode_vs_oracle(gfr, oracle):
     ys = np.stack([dec.row(xb[0], int(e))[0] for e in p[0]])
     want = oracle.combine(ys, wt, 1, topk + 1)
     assert_close(m.output.cpu().numpy(), want, what="moe output")
+
+
+def test_moe_graph_replay_bytes(gfr):
+    """A captured MoE layer (router .. combine) replays to the eager bytes, across different weights and routing."""
+    import synth
+    E, D, N, bits, topk = 64, 2048, 1536, 4, 4
+    ws = [synth.experts(E + 1, D, N, bits, seed=s) for s in (3, 4)]
+    x = synth.activations(2, D, 1)
+    lg = synth.logits(2, E, 2)
+    m = gfr.Moe(D, N, E, topk, 1)
+    s = torch.cuda.Stream()
+    eager = []
+    with torch.cuda.stream(s):
+        for j in range(2):
+            m.run(ws[j], x[j:j + 1], lg[j:j + 1], 1, stream=s)
+            s.synchronize()
+            eager.append(m.output.clone())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            m.run(ws[0], x[0:1], lg[0:1], 1, stream=s)
+            m.run(ws[1], x[1:2], lg[1:2], 1, stream=s)
+    for _ in range(3):
+        m.output.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(m.output, eager[1])
+
+
+def test_grouped_gemv_entry_matches_run_rows(gfr):
+    """gfr_exl3_grouped_gemv (the exported GEMV) computes the Z partials run_rows uses: sum of splits equals the
+    fp32 dot products of the rotated rows with the decoded weights to rounding."""
+    import synth
+    L = gfr.lib()
+    E, D, N, bits = 3, 512, 256, 4
+    w = synth.experts(E, D, N, bits, seed=9)
+    g = gfr.Grouping(E, 2, 2)
+    picks = torch.tensor([[0, 2], [2, 1]], dtype=torch.int32, device="cuda")
+    g.run(picks, 2)
+    X = torch.randn((2, 4, D), device="cuda").half()
+    SK = L.gfr_exl3_gemv_splits(D)
+    Z = torch.zeros((2, SK, 4, N), device="cuda")
+    gfr._check(L.gfr_exl3_grouped_gemv(torch.cuda.current_stream().cuda_stream, X[0].data_ptr(), X[1].data_ptr(),
+                                       w.gt.data_ptr(), w.ut.data_ptr(), g.ids.data_ptr(), g.count.data_ptr(),
+                                       g.members.data_ptr(), Z.data_ptr(), D, N, 4, 2, 2, E, bits, 2, 4))
+    torch.cuda.synchronize()
+    p = picks.cpu().numpy().reshape(-1)
+    for mat, t in enumerate((w.gt, w.ut)):
+        for pair in range(4):
+            W = gfr.decode_tiles(t[int(p[pair])], D, N, bits).float()
+            want = X[mat, pair].float() @ W
+            got = Z[mat, :, pair].sum(0)
+            assert torch.allclose(got, want, rtol=1e-3, atol=1e-3 * want.abs().max().item())
