@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include "exl3_format.hpp"
+#include "route.hpp"
 
 namespace gfr {
 
@@ -44,20 +45,18 @@ __global__ void __launch_bounds__(64) decode_tiles_kernel(const uint32_t* __rest
 #pragma unroll
     for (int j = 0; j < K; ++j) w[j] = src[j];
     const uint32_t prev = prev_word(w[K - 1], i);
-    h2_t d[2][2][4];
+    h2_t d[2][8];
     decode_lane<K>(w, prev, d);
     if (!ok) return;
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int l = 0; l < 4; ++l) {
-                const int row = kt * 16 + 2 * l + 8 * h, col = nt * 16 + i + 8 * c;
-                const uint32_t v = h2_bits(d[c][h][l]);
-                out[(size_t)row * n + col] = (uint16_t)v;
-                out[(size_t)(row + 1) * n + col] = (uint16_t)(v >> 16);
-            }
+        for (int m = 0; m < 8; ++m) {
+            const int col = nt * 16 + i + 8 * c;
+            const uint32_t v = h2_bits(d[c][m]);
+            out[(size_t)(kt * 16 + pair_row(K, m, 0)) * n + col] = (uint16_t)v;
+            out[(size_t)(kt * 16 + pair_row(K, m, 1)) * n + col] = (uint16_t)(v >> 16);
+        }
 }
 
 // rot_in (exl3.cu:224-241): Xh[mat][p][blk] = fp16(had(bf16 x[row] * suh[mat][e]) * HAD) for every pair
@@ -81,107 +80,345 @@ __global__ void __launch_bounds__(64) rot_in_kernel(const uint16_t* __restrict__
     for (int j = 0; j < 2; ++j) v[j] = (F16IN ? f16_to_f32(xr[j]) : bf16_to_f32(xr[j])) * f16_to_f32(suh[j]);
     fwht128_w64(v, lane);
     uint16_t* o = (mat ? out1 : out0) + (size_t)p * K + k;
-    const uint32_t packed = (uint32_t)f32_to_f16(v[0] * HAD_SCALE) | ((uint32_t)f32_to_f16(v[1] * HAD_SCALE) << 16);
+    const uint32_t packed = (uint32_t)f16_of_product(v[0], HAD_SCALE) | ((uint32_t)f16_of_product(v[1], HAD_SCALE) << 16);
     *reinterpret_cast<uint32_t*>(o) = packed;
 }
 
-// Grouped trellis GEMV. Program (distinct expert u, 128-column block cb, mat * SK + split): the members of expert
-// uids[u] (rows of X, RB at a time) times W_q[mat] over k tiles [split * NW * KTW, (split + 1) * NW * KTW) for the
-// block's 128 columns; wave w owns k tiles split * NW * KTW + w * KTW + [0, KTW).
-// Z[((mat * SK + split) * P + pair) * N + n]. MATS = 2 (gate + up) or 1 (down): separate kernels for the profiler.
-template <int K, int KTW, int NW, int RB, int MATS>
-__global__ void __launch_bounds__(NW * 64) gemv_kernel(
-    const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1, const uint32_t* __restrict__ T0,
-    const uint32_t* __restrict__ T1, const int* __restrict__ uids, const int* __restrict__ ucount,
-    const int* __restrict__ members, float* __restrict__ Z, int Kin, int N, int P, int SK, int maxm, int slots,
-    int E) {
-    constexpr int KC = NW * KTW;                 // k tiles a workgroup
-    constexpr int MAXM = 64;                     // member rows a workgroup can hold (the engine's max_rows bound)
-    __shared__ int rows_sh[MAXM];
-    __shared__ int cnt_sh;
-    __shared__ __attribute__((aligned(16))) uint16_t xs[RB][KC * 16];
+// Position of tile row r (0..15) in the packed pair order of pair_row: pair m, low half (2m) or high half (2m + 1).
+__host__ __device__ constexpr int pair_pos(int K, int r) {
+    if (K == 2) {
+        const int lo = (r & 3) >= 2;                       // rows r + 2 of a pair sit in the low half
+        const int base = lo ? r - 2 : r;                   // the pair's r = 4v + (u & 1) + 8 (u >> 1)
+        const int m = 4 * ((base >> 2) & 1) + (base & 1) + 2 * (base >> 3);
+        return 2 * m + (lo ? 0 : 1);
+    }
+    const int lo = r >= 8;                                 // rows 2l + 8 + h in the low half
+    const int base = lo ? r - 8 : r;                       // 2l + h
+    return 2 * base + (lo ? 0 : 1);
+}
+
+// Arguments of the decode GEMV (one struct in the kernarg segment).
+struct GemvArgs {
+    const uint16_t* x0;      // XSRC 0: fp16 rotated rows [P][Kin] (matrix 0); XSRC 1: bf16 input rows [rows][x_stride]
+    const uint16_t* x1;      // XSRC 0: fp16 rotated rows of matrix 1
+    int x_stride;
+    const uint16_t* suh0;    // XSRC 1: input scales [E][Kin] of the two matrices; XSRC 2: suh_d [E][Kin]
+    const uint16_t* suh1;
+    const uint32_t* t0;      // trellis [E][Kin/16][N/16][8K]
+    const uint32_t* t1;
+    const int* uids;
+    const int* ucount;
+    const int* members;      // [E][maxm]
+    float* z;                // [MATS][SK][P][N] split partials (output)
+    int Kin, N, P, SK, maxm, slots, E;
+    const float* zgu;        // XSRC 2: the gate/up split partials [2][SKgu][P][Kin]
+    int SKgu;
+    const uint16_t* svh_g;   // XSRC 2: gate / up output scales [E][Kin]
+    const uint16_t* svh_u;
+    float limit;
+    uint16_t* xd;            // XSRC 2: the down input, also stored (column block 0 only) [P][Kin] fp16
+    const float* logits;     // ROUTE1: the token's router logits [routed]
+    int routed;
+    int* pick_out;           // ROUTE1 outputs (program 0): picks / weights [slots], ids [slots], count, members
+    float* weight_out;
+    int* ids_out;
+    int* count_out;
+    int* members_out;
+};
+
+// The 128 activations of one Hadamard block for one member, already in fp32 lanes v[0..1] = elements 2 lane + j,
+// rounded to fp16 and stored into the wave's pair-ordered LDS slots of k tiles kk0 .. kk0 + 7.
+template <int K>
+__device__ __forceinline__ void store_block(uint16_t* slots16, const float (&v)[2], int lane) {
+    const int kk = (2 * lane) >> 4, r = (2 * lane) & 15;
+    slots16[kk * 16 + pair_pos(K, r)] = f16_of_product(v[0], HAD_SCALE);
+    slots16[kk * 16 + pair_pos(K, r + 1)] = f16_of_product(v[1], HAD_SCALE);
+}
+
+// Grouped trellis GEMV of the decode path. Program (distinct expert u, 128-column block cb, mat * SK + split): the
+// members of expert uids[u] (RB rows at a time) times W_q[mat] over k tiles [split * NW KTW, (split + 1) * NW KTW)
+// for the block's 128 columns; wave w owns k tiles split * NW KTW + w KTW + [0, KTW), ascending, one v_dot2_f32_f16
+// chain a column; the waves are added in order through LDS into Z[mat][split][pair][n] (every sum has a fixed order,
+// so a row's result never depends on the other rows or on RB).
+//   Prologue: the window's count, the expert id and the member codes in one round trip (ROUTE1: computed here
+//   instead), then the activation loads, then the trellis words, so that the activations are built while the
+//   trellis streams in. Activation sources (each bit for bit the reference's formula), staged per wave in LDS:
+//   XSRC 0  rotated fp16 rows (exl3.cu's grouped kernel input);
+//   XSRC 1  rot_in fused (exl3.cu:224-241): bf16 input row * suh -> 128-point transform -> fp16; KTW = 8, one block;
+//   XSRC 2  the gate/up epilogue fused (exl3.cu:260-296): the gate / up split partials of one 128-block summed in
+//           order -> transforms, scales, limited SwiGLU, suh_d, transform -> fp16 (the down projection's input).
+//   ROUTE1  (one-token windows) the wave routes the token itself (route.hpp) from a.logits: the window's experts
+//           are the token's slots; program (0, 0, 0) stores picks / weights / ids / count / members for the later
+//           launches.
+template <int K, int KTW, int NW, int MATS, int XSRC, int RB, bool ROUTE1>
+__global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) {
+    constexpr int KC = NW * KTW;
+    static_assert(XSRC == 0 || KTW == 8, "a wave that builds its activations covers one 128-point block");
+    static_assert(XSRC != 0 || RB * KTW <= 64, "one lane a (member, k tile) when staging rotated rows");
+    __shared__ __attribute__((aligned(16))) uint16_t xs[NW][RB][KTW * 16];
     __shared__ float red[NW][RB][128];
 
-    const int u = blockIdx.x;
-    if (u >= ucount[0]) return;
-    const int e = uids[u];
-    if (e >= E) return;                          // not an EXL3 expert
-    const int cb = blockIdx.y, split = blockIdx.z % SK, mat = MATS == 1 ? 0 : blockIdx.z / SK;
-    const uint16_t* __restrict__ X = mat ? X1 : X0;
-    const uint32_t* __restrict__ T = mat ? T1 : T0;
+    const int u = blockIdx.x, cb = blockIdx.y;
+    const int split = blockIdx.z % a.SK, mat = MATS == 1 ? 0 : blockIdx.z / a.SK;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, t = lane >> 3, i = lane & 7;
-    const int KT = Kin >> 4, NT = N >> 4;
+    const int KT = a.Kin >> 4, NT = a.N >> 4;
     const int kt0 = split * KC + wave * KTW;
 
-    // this wave's trellis words, all KTW k tiles issued before anything else
+    int e, code;
+    if constexpr (ROUTE1) {
+        int pick;
+        float weight;
+        route_token_regs(a.logits, a.routed, a.slots - 1, a.routed, pick, weight);
+        int rank = 0;                                    // ascending order of the token's slots' experts
+        for (int j = 0; j < a.slots; ++j) rank += __builtin_amdgcn_readlane(pick, j) < pick;
+        const uint64_t mine = __ballot(lane < a.slots && rank == u);
+        if (mine == 0) return;                           // u >= slots: no such expert
+        const int slot = __builtin_ctzll(mine);
+        e = __builtin_amdgcn_readlane(pick, slot);
+        code = lane == 0 ? slot : -1;                    // row 0, this slot
+        if (u == 0 && cb == 0 && blockIdx.z == 0 && wave == 0 && lane < a.slots) {
+            a.pick_out[lane] = pick;
+            a.weight_out[lane] = weight;
+            a.ids_out[rank] = pick;
+            a.members_out[(size_t)rank * a.maxm] = lane;
+            for (int j = 1; j < a.maxm; ++j) a.members_out[(size_t)rank * a.maxm + j] = -1;
+            if (lane == 0) a.count_out[0] = a.slots;
+        }
+        if (e >= a.E) return;
+    } else {
+        const int cntu = a.ucount[0];
+        e = a.uids[u];
+        code = lane < a.maxm ? a.members[(size_t)u * a.maxm + lane] : -1;
+        if (u >= cntu || e >= a.E) return;               // past the window's experts, or not an EXL3 expert
+    }
+    const int cnt = __popcll(__ballot(code >= 0));        // members come first
+    const int pair_l = code >= 0 ? (code >> 5) * a.slots + (code & 31) : 0;
+
+    // ---- activation loads of a chunk of members (before the trellis words for the first chunk)
+    uint32_t xv[RB], sv = 0, sg = 0, su = 0;             // XSRC 1: bf16 pairs; scale pairs
+    uint4 va = {0, 0, 0, 0}, vb = {0, 0, 0, 0};           // XSRC 0: this lane's k tile of one member
+    float gsum[RB][2], usum[RB][2];
+    auto load_acts = [&](int r0, int nr) {
+        if constexpr (XSRC == 1) {
+            sv = *reinterpret_cast<const uint32_t*>((mat ? a.suh1 : a.suh0) + (size_t)e * a.Kin + kt0 * 16 + 2 * lane);
+#pragma unroll
+            for (int m = 0; m < RB; ++m) {
+                const int row = __builtin_amdgcn_readlane(code, r0 + (m < nr ? m : 0)) >> 5;
+                xv[m] = *reinterpret_cast<const uint32_t*>(a.x0 + (size_t)row * a.x_stride + kt0 * 16 + 2 * lane);
+            }
+        } else if constexpr (XSRC == 2) {
+            const size_t o = (size_t)e * a.Kin + kt0 * 16 + 2 * lane;
+            sg = *reinterpret_cast<const uint32_t*>(a.svh_g + o);
+            su = *reinterpret_cast<const uint32_t*>(a.svh_u + o);
+            sv = *reinterpret_cast<const uint32_t*>(a.suh0 + o);
+#pragma unroll
+            for (int m = 0; m < RB; ++m) gsum[m][0] = gsum[m][1] = usum[m][0] = usum[m][1] = 0.f;
+            const int n = kt0 * 16 + 2 * lane;
+            for (int s0 = 0; s0 < a.SKgu; s0 += 4) {      // partials in split order, four in flight
+                float2 zg[RB][4], zu[RB][4];
+#pragma unroll
+                for (int m = 0; m < RB; ++m) {
+                    const int p = __builtin_amdgcn_readlane(pair_l, r0 + (m < nr ? m : 0));
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if (s0 + q < a.SKgu) {
+                            zg[m][q] = *reinterpret_cast<const float2*>(a.zgu + ((size_t)(s0 + q) * a.P + p) * a.Kin + n);
+                            zu[m][q] = *reinterpret_cast<const float2*>(
+                                a.zgu + ((size_t)(a.SKgu + s0 + q) * a.P + p) * a.Kin + n);
+                        }
+                }
+#pragma unroll
+                for (int m = 0; m < RB; ++m)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if (s0 + q < a.SKgu) {
+                            gsum[m][0] += zg[m][q].x; gsum[m][1] += zg[m][q].y;
+                            usum[m][0] += zu[m][q].x; usum[m][1] += zu[m][q].y;
+                        }
+            }
+        } else {
+            const int m = lane / KTW, kk = lane % KTW;
+            const int p = __shfl(pair_l, (r0 + m) & 63, 64);
+            if (m < nr) {
+                const uint16_t* X = mat ? a.x1 : a.x0;
+                const uint4* src = reinterpret_cast<const uint4*>(X + (size_t)p * a.Kin + (size_t)(kt0 + kk) * 16);
+                va = src[0];
+                vb = src[1];
+            }
+        }
+    };
+    // ---- the loaded activations of a chunk -> this wave's pair-ordered LDS slots
+    auto build_acts = [&](int r0, int nr) {
+        if constexpr (XSRC == 1) {
+            const float s0 = f16_to_f32((uint16_t)sv), s1 = f16_to_f32((uint16_t)(sv >> 16));
+#pragma unroll
+            for (int m = 0; m < RB; ++m)
+                if (m < nr) {
+                    float v[2] = {bf16_to_f32((uint16_t)xv[m]) * s0, bf16_to_f32((uint16_t)(xv[m] >> 16)) * s1};
+                    fwht128_w64(v, lane);
+                    store_block<K>(&xs[wave][m][0], v, lane);
+                }
+        } else if constexpr (XSRC == 2) {
+            const float svg[2] = {f16_to_f32((uint16_t)sg), f16_to_f32((uint16_t)(sg >> 16))};
+            const float svu[2] = {f16_to_f32((uint16_t)su), f16_to_f32((uint16_t)(su >> 16))};
+            const float sdd[2] = {f16_to_f32((uint16_t)sv), f16_to_f32((uint16_t)(sv >> 16))};
+            const int n = kt0 * 16 + 2 * lane;
+#pragma unroll
+            for (int m = 0; m < RB; ++m)
+                if (m < nr) {
+                    float gv[2] = {gsum[m][0], gsum[m][1]}, uv[2] = {usum[m][0], usum[m][1]};
+                    fwht128_w64(gv, lane);
+                    fwht128_w64(uv, lane);
+                    float v[2];
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const float gg = fminf(bf16r(gv[j] * HAD_SCALE * svg[j]), a.limit);
+                        const float uu = fminf(fmaxf(bf16r(uv[j] * HAD_SCALE * svu[j]), -a.limit), a.limit);
+                        const float act = bf16r(bf16r(gg / (1.f + expf(-gg))) * uu);
+                        v[j] = act * sdd[j];
+                    }
+                    fwht128_w64(v, lane);
+                    store_block<K>(&xs[wave][m][0], v, lane);
+                    if (cb == 0 && a.xd) {
+                        const int p = __builtin_amdgcn_readlane(pair_l, r0 + m);
+                        *reinterpret_cast<uint32_t*>(a.xd + (size_t)p * a.Kin + n) =
+                            (uint32_t)f16_of_product(v[0], HAD_SCALE) | ((uint32_t)f16_of_product(v[1], HAD_SCALE) << 16);
+                    }
+                }
+        } else {
+            const int m = lane / KTW, kk = lane % KTW;
+            if (m < nr) {
+                const uint32_t xa[4] = {va.x, va.y, va.z, va.w}, xb[4] = {vb.x, vb.y, vb.z, vb.w};
+                uint32_t o[8];
+                pair_activations<K>(xa, xb, o);
+                uint4* dst = reinterpret_cast<uint4*>(&xs[wave][m][kk * 16]);
+                dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+                dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+            }
+        }
+        // the slots are this wave's own: a wave-level barrier orders the LDS stores before the reads
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+
+    const int nr0 = cnt < RB ? cnt : RB;
+    load_acts(0, nr0);
     uint32_t wr[KTW][K];
     {
+        const uint32_t* T = mat ? a.t1 : a.t0;
         const uint32_t* src = T + (((size_t)e * KT + kt0) * NT + cb * 8 + t) * (8 * K) + i * K;
 #pragma unroll
         for (int kk = 0; kk < KTW; ++kk) load_words<K>(src + (size_t)kk * NT * (8 * K), wr[kk]);
     }
 
-    if (tid == 0) cnt_sh = 0;
-    __syncthreads();
-    for (int m = tid; m < maxm && m < MAXM; m += NW * 64) {
-        const int code = members[(size_t)u * maxm + m];
-        rows_sh[m] = code >= 0 ? (code >> 5) * slots + (code & 31) : -1;
-        if (code >= 0) atomicMax(&cnt_sh, m + 1);   // members come first
-    }
-    __syncthreads();
-    const int cnt = cnt_sh;
-
     for (int r0 = 0; r0 < cnt; r0 += RB) {
         const int nr = cnt - r0 < RB ? cnt - r0 : RB;
-        // the member rows' k range into LDS (16-byte chunks)
-        for (int c = tid; c < nr * KC * 2; c += NW * 64) {
-            const int m = c / (KC * 2), q = c % (KC * 2);
-            const uint16_t* src = X + (size_t)rows_sh[r0 + m] * Kin + (size_t)split * KC * 16 + q * 8;
-            *reinterpret_cast<uint4*>(&xs[m][q * 8]) = *reinterpret_cast<const uint4*>(src);
-        }
-        __syncthreads();
+        if (r0 > 0) load_acts(r0, nr);
+        build_acts(r0, nr);
         float acc[RB][2];
 #pragma unroll
         for (int m = 0; m < RB; ++m) acc[m][0] = acc[m][1] = 0.f;
 #pragma unroll
         for (int kk = 0; kk < KTW; ++kk) {
             const uint32_t prev = prev_word(wr[kk][K - 1], i);
-            h2_t d[2][2][4];
+            h2_t d[2][8];
             decode_lane<K>(wr[kk], prev, d);
-            const int kx = (wave * KTW + kk) * 16;
 #pragma unroll
             for (int m = 0; m < RB; ++m) {
                 if (m < nr) {
-                    const uint4 xa = *reinterpret_cast<const uint4*>(&xs[m][kx]);
-                    const uint4 xb = *reinterpret_cast<const uint4*>(&xs[m][kx + 8]);
-                    const uint32_t xl[2][4] = {{xa.x, xa.y, xa.z, xa.w}, {xb.x, xb.y, xb.z, xb.w}};
+                    const uint4 xa = *reinterpret_cast<const uint4*>(&xs[wave][m][kk * 16]);
+                    const uint4 xb = *reinterpret_cast<const uint4*>(&xs[wave][m][kk * 16 + 8]);
+                    const uint32_t xp[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
 #pragma unroll
-                    for (int l = 0; l < 4; ++l)
-#pragma unroll
-                        for (int h = 0; h < 2; ++h) {
-                            const h2_t xv = bits_h2(xl[h][l]);
-                            acc[m][0] = __builtin_amdgcn_fdot2(d[0][h][l], xv, acc[m][0], false);
-                            acc[m][1] = __builtin_amdgcn_fdot2(d[1][h][l], xv, acc[m][1], false);
-                        }
+                    for (int q = 0; q < 8; ++q) {
+                        acc[m][0] = __builtin_amdgcn_fdot2(d[0][q], bits_h2(xp[q]), acc[m][0], false);
+                        acc[m][1] = __builtin_amdgcn_fdot2(d[1][q], bits_h2(xp[q]), acc[m][1], false);
+                    }
                 }
             }
         }
+        if constexpr (NW == 1) {
 #pragma unroll
-        for (int m = 0; m < RB; ++m)
-            if (m < nr) {
-                red[wave][m][16 * t + i] = acc[m][0];
-                red[wave][m][16 * t + i + 8] = acc[m][1];
+            for (int m = 0; m < RB; ++m)
+                if (m < nr) {
+                    const int p = __builtin_amdgcn_readlane(pair_l, r0 + m);
+                    float* zr = a.z + ((size_t)(mat * a.SK + split) * a.P + p) * a.N + cb * 128 + 16 * t + i;
+                    zr[0] = acc[m][0];
+                    zr[8] = acc[m][1];
+                }
+        } else {
+#pragma unroll
+            for (int m = 0; m < RB; ++m)
+                if (m < nr) {
+                    red[wave][m][16 * t + i] = acc[m][0];
+                    red[wave][m][16 * t + i + 8] = acc[m][1];
+                }
+            __syncthreads();
+            for (int idx = tid; idx < nr * 128; idx += NW * 64) {
+                const int m = idx >> 7, col = idx & 127;
+                float sum = red[0][m][col];
+#pragma unroll
+                for (int w = 1; w < NW; ++w) sum += red[w][m][col];
+                const int p = __builtin_amdgcn_readlane(pair_l, r0 + m);
+                a.z[((size_t)(mat * a.SK + split) * a.P + p) * a.N + cb * 128 + col] = sum;
             }
-        __syncthreads();
-        for (int idx = tid; idx < nr * 128; idx += NW * 64) {
-            const int m = idx >> 7, col = idx & 127;
-            float s = red[0][m][col];
-#pragma unroll
-            for (int w = 1; w < NW; ++w) s += red[w][m][col];
-            Z[((size_t)(mat * SK + split) * P + rows_sh[r0 + m]) * N + cb * 128 + col] = s;
+            if (r0 + RB < cnt) __syncthreads();            // red is rewritten by the next chunk
         }
-        __syncthreads();                             // xs / red are rewritten by the next chunk
     }
+}
+
+// Down epilogue (exl3.cu:300-321) and, with weights, the slot-ordered combine of a token. Program (token row,
+// 128-column block), one wave a slot (up to 16 at a time): pair p = row * slots + s, its SK down partials summed in
+// order, transformed, scaled by svh_d -> y[p]; then out[row] = sum over the slots in order of weights * y.
+__global__ void __launch_bounds__(1024) down_finish_kernel(const float* __restrict__ Z, const int* __restrict__ pick,
+                                                            const uint16_t* __restrict__ svh_d, float* __restrict__ y,
+                                                            int P, int D, int SK, int slots, int exl3_slots,
+                                                            const float* __restrict__ weights,
+                                                            float* __restrict__ out) {
+    __shared__ float2 ys[16][64];
+    const int row = blockIdx.x, blk = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nwv = blockDim.x >> 6;
+    const int n = blk * 128 + 2 * lane;
+    float o0 = 0.f, o1 = 0.f;
+    for (int s0 = 0; s0 < exl3_slots; s0 += nwv) {
+        const int s = s0 + wave;
+        if (s < exl3_slots) {
+            const int p = row * slots + s;
+            const int e = pick[p];
+            float2 zs[8];
+            float v[2] = {0.f, 0.f};
+            for (int k0 = 0; k0 < SK; k0 += 8) {            // partials in split order, eight in flight
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    if (k0 + k < SK) zs[k] = *reinterpret_cast<const float2*>(Z + ((size_t)(k0 + k) * P + p) * D + n);
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    if (k0 + k < SK) {
+                        v[0] += zs[k].x;
+                        v[1] += zs[k].y;
+                    }
+            }
+            const uint32_t sv = *reinterpret_cast<const uint32_t*>(svh_d + (size_t)e * D + n);
+            fwht128_w64(v, lane);
+            float2 yv;
+            yv.x = v[0] * HAD_SCALE * f16_to_f32((uint16_t)sv);
+            yv.y = v[1] * HAD_SCALE * f16_to_f32((uint16_t)(sv >> 16));
+            *reinterpret_cast<float2*>(y + (size_t)p * D + n) = yv;
+            ys[wave][lane] = yv;
+        }
+        if (weights) {
+            __syncthreads();
+            if (wave == 0)
+                for (int q = 0; q < nwv && s0 + q < exl3_slots; ++q) {
+                    const float w = weights[row * slots + s0 + q];
+                    o0 += w * ys[q][lane].x;
+                    o1 += w * ys[q][lane].y;
+                }
+            __syncthreads();
+        }
+    }
+    if (weights && wave == 0) *reinterpret_cast<float2*>(out + (size_t)row * D + n) = make_float2(o0, o1);
 }
 
 // gateup epilogue (exl3.cu:260-296): ordered split sums of gate and up, rotation, svh scales, GLM's limited SwiGLU
@@ -221,7 +458,7 @@ __global__ void __launch_bounds__(64) gateup_epilogue_kernel(const float* __rest
         v[j] = act * f16_to_f32(suh_d[(size_t)e * N + n + j]);
     }
     fwht128_w64(v, lane);
-    const uint32_t packed = (uint32_t)f32_to_f16(v[0] * HAD_SCALE) | ((uint32_t)f32_to_f16(v[1] * HAD_SCALE) << 16);
+    const uint32_t packed = (uint32_t)f16_of_product(v[0], HAD_SCALE) | ((uint32_t)f16_of_product(v[1], HAD_SCALE) << 16);
     *reinterpret_cast<uint32_t*>(xd + (size_t)p * N + n) = packed;
 }
 
@@ -278,52 +515,95 @@ hipError_t launch_rot_in(hipStream_t s, const uint16_t* x, int x_stride, bool in
     return hipGetLastError();
 }
 
-constexpr int GEMV_NW = 4, GEMV_RB = 8;
-
-static int gemv_ktw(int Kin) {
+// Split counts are fixed by the shape (never by the rows in the window), so a row's bits never depend on its window.
+static int ktw_for(int Kin) {
     const int KT = Kin / 16;
-    return KT % (GEMV_NW * 4) == 0 ? 4 : KT % (GEMV_NW * 2) == 0 ? 2 : 1;
+    return KT % 16 == 0 ? 4 : KT % 8 == 0 ? 2 : 1;
 }
 
-int gemv_splits(int Kin) { return Kin / 16 / (GEMV_NW * gemv_ktw(Kin)); }
+int gemv_splits(int Kin) { return Kin / 16 / (4 * ktw_for(Kin)); }
+// waves a workgroup of the block-building GEMVs: one 128-block each, as many as divide the blocks
+static int nw_gateup(int D) { return (D / 128) % 4 == 0 ? 4 : 2; }   // hidden: a multiple of 256
+static int nw_down(int) { return 2; }                                   // inter: a multiple of 256
+int gemv_gateup_splits(int D) { return D / 128 / nw_gateup(D); }
+int gemv_down_splits(int N) { return N / 128 / nw_down(N); }
 
-template <int K, int MATS>
-static void gemv_dispatch(int ktw, dim3 grid, hipStream_t s, const uint16_t* X0, const uint16_t* X1,
-                          const uint32_t* T0, const uint32_t* T1, const int* uids, const int* ucount,
-                          const int* members, float* Z, int Kin, int N, int P, int SK, int maxm, int slots, int E) {
-    if (ktw == 4)
-        gemv_kernel<K, 4, GEMV_NW, GEMV_RB, MATS><<<grid, GEMV_NW * 64, 0, s>>>(X0, X1, T0, T1, uids, ucount, members, Z,
-                                                                          Kin, N, P, SK, maxm, slots, E);
-    else if (ktw == 2)
-        gemv_kernel<K, 2, GEMV_NW, GEMV_RB, MATS><<<grid, GEMV_NW * 64, 0, s>>>(X0, X1, T0, T1, uids, ucount, members, Z,
-                                                                          Kin, N, P, SK, maxm, slots, E);
-    else
-        gemv_kernel<K, 1, GEMV_NW, GEMV_RB, MATS><<<grid, GEMV_NW * 64, 0, s>>>(X0, X1, T0, T1, uids, ucount, members, Z,
-                                                                          Kin, N, P, SK, maxm, slots, E);
+template <int K, int KTW, int NW, int MATS, int XSRC, bool ROUTE1>
+static hipError_t gemv_go(int rb, dim3 grid, hipStream_t s, const GemvArgs& a) {
+    if (ROUTE1 || rb == 1) expert_gemv_kernel<K, KTW, NW, MATS, XSRC, 1, ROUTE1><<<grid, NW * 64, 0, s>>>(a);
+    else if (rb == 2) expert_gemv_kernel<K, KTW, NW, MATS, XSRC, 2, false><<<grid, NW * 64, 0, s>>>(a);
+    else if (rb == 4) expert_gemv_kernel<K, KTW, NW, MATS, XSRC, 4, false><<<grid, NW * 64, 0, s>>>(a);
+    else expert_gemv_kernel<K, KTW, NW, MATS, XSRC, 8, false><<<grid, NW * 64, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+// member rows a chunk: the smallest of 1, 2, 4, 8 that holds the window's rows (an expert has at most `rows`)
+static int rb_for(int rows) { return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8; }
+
+template <int KTW, int NW, int MATS, int XSRC, bool ROUTE1 = false>
+static hipError_t gemv_bits(int bits, int rb, dim3 grid, hipStream_t s, const GemvArgs& a) {
+    switch (bits) {
+        case 2: return gemv_go<2, KTW, NW, MATS, XSRC, ROUTE1>(rb, grid, s, a);
+        case 3: return gemv_go<3, KTW, NW, MATS, XSRC, ROUTE1>(rb, grid, s, a);
+        case 4: return gemv_go<4, KTW, NW, MATS, XSRC, ROUTE1>(rb, grid, s, a);
+        case 5: return gemv_go<5, KTW, NW, MATS, XSRC, ROUTE1>(rb, grid, s, a);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_gemv(hipStream_t s, const uint16_t* X0, const uint16_t* X1, const uint32_t* T0, const uint32_t* T1,
                        const int* uids, const int* ucount, const int* members, float* Z, int Kin, int N, int P,
                        int maxm, int slots, int E, int bits, int mats, int maxu) {
-    const int ktw = gemv_ktw(Kin), SK = gemv_splits(Kin);
-    const dim3 grid(maxu, N / 128, mats * SK);
+    GemvArgs a{};
+    a.x0 = X0; a.x1 = X1; a.t0 = T0; a.t1 = T1; a.uids = uids; a.ucount = ucount; a.members = members; a.z = Z;
+    a.Kin = Kin; a.N = N; a.P = P; a.SK = gemv_splits(Kin); a.maxm = maxm; a.slots = slots; a.E = E;
+    const int ktw = ktw_for(Kin), rb = rb_for(maxm);
+    const dim3 grid(maxu, N / 128, mats * a.SK);
     if (mats == 2) {
-        switch (bits) {
-            case 2: gemv_dispatch<2, 2>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
-            case 3: gemv_dispatch<3, 2>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
-            case 4: gemv_dispatch<4, 2>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
-            case 5: gemv_dispatch<5, 2>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
-            default: return hipErrorInvalidValue;
-        }
-        return hipGetLastError();
+        if (ktw == 4) return gemv_bits<4, 4, 2, 0>(bits, rb, grid, s, a);
+        if (ktw == 2) return gemv_bits<2, 4, 2, 0>(bits, rb, grid, s, a);
+        return gemv_bits<1, 4, 2, 0>(bits, rb, grid, s, a);
     }
-    switch (bits) {
-        case 2: gemv_dispatch<2, 1>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
-        case 3: gemv_dispatch<3, 1>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
-        case 4: gemv_dispatch<4, 1>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
-        case 5: gemv_dispatch<5, 1>(ktw, grid, s, X0, X1, T0, T1, uids, ucount, members, Z, Kin, N, P, SK, maxm, slots, E); break;
-        default: return hipErrorInvalidValue;
+    if (ktw == 4) return gemv_bits<4, 4, 1, 0>(bits, rb, grid, s, a);
+    if (ktw == 2) return gemv_bits<2, 4, 1, 0>(bits, rb, grid, s, a);
+    return gemv_bits<1, 4, 1, 0>(bits, rb, grid, s, a);
+}
+
+hipError_t launch_expert_gateup(hipStream_t s, const uint16_t* x, int x_stride, const uint16_t* suh_g,
+                                const uint16_t* suh_u, const uint32_t* gt, const uint32_t* ut, const int* uids,
+                                const int* ucount, const int* members, float* Zgu, int D, int N, int P, int rows,
+                                int maxm, int slots, int E, int bits, int maxu, const RouteOne* route) {
+    GemvArgs a{};
+    a.x0 = x; a.x_stride = x_stride; a.suh0 = suh_g; a.suh1 = suh_u; a.t0 = gt; a.t1 = ut;
+    a.uids = uids; a.ucount = ucount; a.members = members; a.z = Zgu; a.Kin = D; a.N = N; a.P = P;
+    a.SK = gemv_gateup_splits(D); a.maxm = maxm; a.slots = slots; a.E = E;
+    const dim3 grid(maxu, N / 128, 2 * a.SK);
+    const int nw = nw_gateup(D), rb = rb_for(rows);
+    if (route) {
+        a.logits = route->logits; a.routed = route->routed; a.pick_out = route->picks; a.weight_out = route->weights;
+        a.ids_out = route->ids; a.count_out = route->count; a.members_out = route->members;
+        return nw == 4 ? gemv_bits<8, 4, 2, 1, true>(bits, 1, grid, s, a) : gemv_bits<8, 2, 2, 1, true>(bits, 1, grid, s, a);
     }
+    return nw == 4 ? gemv_bits<8, 4, 2, 1>(bits, rb, grid, s, a) : gemv_bits<8, 2, 2, 1>(bits, rb, grid, s, a);
+}
+
+hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, const uint16_t* svh_g, const uint16_t* svh_u,
+                              const uint16_t* suh_d, float limit, uint16_t* xd, const uint32_t* dt, const int* uids,
+                              const int* ucount, const int* members, float* Zd, int N, int P, int rows, int maxm,
+                              int slots, int E, int bits, int maxu) {
+    GemvArgs a{};
+    a.zgu = Zgu; a.SKgu = gemv_gateup_splits(D); a.svh_g = svh_g; a.svh_u = svh_u; a.suh0 = suh_d; a.limit = limit;
+    a.xd = xd; a.t0 = dt; a.t1 = dt; a.uids = uids; a.ucount = ucount; a.members = members; a.z = Zd;
+    a.Kin = N; a.N = D; a.P = P; a.SK = gemv_down_splits(N); a.maxm = maxm; a.slots = slots; a.E = E;
+    return gemv_bits<8, 2, 1, 2>(bits, rb_for(rows), dim3(maxu, D / 128, a.SK), s, a);
+}
+
+hipError_t launch_down_finish(hipStream_t s, const float* Zd, const int* pick, const uint16_t* svh_d, float* y,
+                              int rows, int P, int D, int SK, int slots, int exl3_slots, const float* weights,
+                              float* out) {
+    const int nwv = exl3_slots < 16 ? (exl3_slots > 0 ? exl3_slots : 1) : 16;
+    down_finish_kernel<<<dim3(rows, D / 128), 64 * nwv, 0, s>>>(Zd, pick, svh_d, y, P, D, SK, slots, exl3_slots,
+                                                                weights, out);
     return hipGetLastError();
 }
 

@@ -9,6 +9,7 @@
 // Lane layout used here ("8 lanes a tile"): lane i (0..7) of a tile owns values 32i..32i+31 = words Ki..Ki+K-1 and
 // needs the low bits of word Ki-1 (the previous lane's last word; lane 0 wraps to lane 7). Those 32 values are
 // columns i and i+8 of all 16 rows, so one lane produces two output columns' worth of products per k tile.
+// Value q (0..31) of lane i is tile value p = 32i + q: row 2(q/8) + (j&1) + 8((j>>1)&1), column i + 8(j>>2), j = q%8.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -22,43 +23,106 @@ typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t h2_bits(h2_t v) { return __builtin_bit_cast(uint32_t, v); }
 __device__ __forceinline__ h2_t bits_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
 
-// The scrambled state: two fp16 halves whose sum is the codebook value (experts.rs:43-46).
-__device__ __forceinline__ uint32_t mcg_x(uint32_t s) { return ((s * 0xCBAC1FEDu) & 0x8FFF8FFFu) ^ 0x3B603B60u; }
-
-// Codebook values of two 16-bit states as packed fp16 (first state in the low half). The per-state sum lo + hi is
-// one fp16 round-to-nearest add, as the reference's half2 add.
-__device__ __forceinline__ h2_t mcg2(uint32_t s0, uint32_t s1) {
-    const uint32_t x0 = mcg_x(s0), x1 = mcg_x(s1);
-    const uint32_t lo = __builtin_amdgcn_perm(x1, x0, 0x05040100u);  // x0.lo | x1.lo << 16
-    const uint32_t hi = __builtin_amdgcn_perm(x1, x0, 0x07060302u);  // x0.hi | x1.hi << 16
-    return bits_h2(lo) + bits_h2(hi);
+// Codebook values of two 16-bit states packed in one register (S = s_a | s_b << 16), as packed fp16 (w_a, w_b).
+// experts.rs:43-46 per state: x = s * 0xCBAC1FED mod 2^32, (x & 0x8FFF8FFF) ^ 0x3B603B60, value = fp16(x.lo) +
+// fp16(x.hi) rounded to fp16. Computed two states at a time in 16-bit lanes: x.lo = (s * 0x1FED) mod 2^16 and
+// x.hi = (s * 0xCBAC + ((s * 0x1FED) >> 16)) mod 2^16, with s * 0x1FED < 2^29 exact in a 24-bit multiply.
+// hipcc emits 8 VALU ops a pair: 2 v_mul_u32_u24 (SDWA word select), 2 v_perm, v_pk_mad_u16, 2 v_bitop3, v_pk_add_f16.
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ h2_t decode_pair(uint32_t S) {
+    const uint32_t pa = (S & 0xffffu) * 0x1FEDu;
+    const uint32_t pb = (S >> 16) * 0x1FEDu;
+    const uint32_t lo = __builtin_amdgcn_perm(pb, pa, 0x05040100u);   // (x_a.lo, x_b.lo)
+    const uint32_t cy = __builtin_amdgcn_perm(pb, pa, 0x07060302u);   // carries into the high halves
+    const u16x2_t hv = __builtin_bit_cast(u16x2_t, S) * (u16x2_t){0xCBAC, 0xCBAC} + __builtin_bit_cast(u16x2_t, cy);
+    const uint32_t hi = __builtin_bit_cast(uint32_t, hv);                   // (x_a.hi, x_b.hi)
+    const uint32_t lm = (lo & 0x8FFF8FFFu) ^ 0x3B603B60u;
+    const uint32_t hm = (hi & 0x8FFF8FFFu) ^ 0x3B603B60u;
+    return bits_h2(lm) + bits_h2(hm);
 }
 
-// The 16-bit state of the lane's value q (0..31): window ending at bit (q + 1) K of the lane's bit range, whose
-// first word is w[0]; prev = the word before w[0] in the circular stream. All positions are compile-time.
+// Right funnel shift of the lane's bit stream so that the window of value Q ends at bit 0 (junk above bit 15).
 template <int K, int Q>
-__device__ __forceinline__ uint32_t lane_state(const uint32_t (&w)[K], uint32_t prev) {
+__device__ __forceinline__ uint32_t lane_window(const uint32_t (&w)[K], uint32_t prev) {
     constexpr int e = (Q + 1) * K;               // window end, in bits from the lane's first bit
     constexpr int hiw = (e - 1) >> 5;            // word holding the window's last bit
     constexpr int shift = 32 * (hiw + 1) - e;    // right shift that brings the window end to bit 0
     if constexpr (shift + 16 <= 32) {
-        return (w[hiw] >> shift) & 0xffffu;
+        return w[hiw] >> shift;
     } else {
         const uint32_t hi = hiw == 0 ? prev : w[hiw > 0 ? hiw - 1 : 0];
-        return __builtin_amdgcn_alignbit(hi, w[hiw], shift) & 0xffffu;
+        return __builtin_amdgcn_alignbit(hi, w[hiw], shift);
     }
 }
 
-// Decode the lane's 32 values into 16 packed pairs: d[c][h][l] = rows (2l + 8h, 2l + 8h + 1) of column i + 8c.
+// Row pairs: decode_lane produces, for each of the lane's two columns (i, i + 8), 8 packed weight pairs
+// d[c][m] = (W[ra(m)][col], W[rb(m)][col]) (low, high half). The pairing depends on K so that the two states of a
+// pair come out of one register cheaply; rows are those of the tile (0..15). The activations are stored in the same
+// pair order (row_of_slot), so one dot2 per pair multiplies the right rows.
+//   K != 2: m = 2l + h  -> rows (2l + 8 + h, 2l + h)             values (8l + j + 2, 8l + j), j = h or 4 + h
+//   K == 2: m = 4v + u  -> rows (r + 2, r), r = 4v + (u&1) + 8(u>>1)  values (16v + j + 8, 16v + j), j = u or 4 + u
+__host__ __device__ constexpr int pair_row(int K, int m, int half) {
+    return K == 2 ? (4 * (m >> 2) + ((m & 3) & 1) + 8 * ((m & 3) >> 1) + (half ? 0 : 2))
+                  : (2 * (m >> 1) + (m & 1) + (half ? 0 : 8));
+}
+
+// Decode the lane's 32 values into d[c][m] (see pair_row).
 template <int K>
-__device__ __forceinline__ void decode_lane(const uint32_t (&w)[K], uint32_t prev, h2_t (&d)[2][2][4]) {
-#define GFR_DEC(L)                                                                                         \
-    d[0][0][L] = mcg2(lane_state<K, 8 * L + 0>(w, prev), lane_state<K, 8 * L + 1>(w, prev));                \
-    d[0][1][L] = mcg2(lane_state<K, 8 * L + 2>(w, prev), lane_state<K, 8 * L + 3>(w, prev));                \
-    d[1][0][L] = mcg2(lane_state<K, 8 * L + 4>(w, prev), lane_state<K, 8 * L + 5>(w, prev));                \
-    d[1][1][L] = mcg2(lane_state<K, 8 * L + 6>(w, prev), lane_state<K, 8 * L + 7>(w, prev));
-    GFR_DEC(0) GFR_DEC(1) GFR_DEC(2) GFR_DEC(3)
-#undef GFR_DEC
+__device__ __forceinline__ void decode_lane(const uint32_t (&w)[K], uint32_t prev, h2_t (&d)[2][8]) {
+    if constexpr (K == 4) {
+        // four words, each holding the windows of values 8l .. 8l + 7 at right shifts 28 - 4j of (p : w); pairs
+        // (j + 2, j) sit 8 bits apart, so one byte permute of (p : w) or of (p : w) >> 4 packs a pair
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t p = l == 0 ? prev : w[l > 0 ? l - 1 : 0];
+            const uint32_t a = __builtin_amdgcn_alignbit(p, w[l], 4);
+            const uint32_t b = p >> 4;
+            d[1][2 * l + 1] = decode_pair(__builtin_amdgcn_perm(p, w[l], 0x02010100u));  // (s7, s5)
+            d[0][2 * l + 1] = decode_pair(__builtin_amdgcn_perm(p, w[l], 0x04030302u));  // (s3, s1)
+            d[1][2 * l] = decode_pair(__builtin_amdgcn_perm(b, a, 0x02010100u));         // (s6, s4)
+            d[0][2 * l] = decode_pair(__builtin_amdgcn_perm(b, a, 0x04030302u));         // (s2, s0)
+        }
+    } else if constexpr (K == 2) {
+        // two words; values q and q + 8 are 16 bits apart: one funnel shift holds the pair (q + 8 low, q high)
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+            const uint32_t p = v == 0 ? prev : w[0];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                d[j >> 2][4 * v + (j & 3)] = decode_pair(__builtin_amdgcn_alignbit(p, w[v], 14 - 2 * j));
+        }
+    } else {
+#define GFR_PAIR(L, J)                                                                                       \
+        d[(J) >> 2][2 * (L) + ((J) & 1)] = decode_pair(__builtin_amdgcn_perm(                                 \
+            lane_window<K, 8 * (L) + (J)>(w, prev), lane_window<K, 8 * (L) + (J) + 2>(w, prev), 0x05040100u));
+#define GFR_WORDS(L) GFR_PAIR(L, 0) GFR_PAIR(L, 1) GFR_PAIR(L, 4) GFR_PAIR(L, 5)
+        GFR_WORDS(0) GFR_WORDS(1) GFR_WORDS(2) GFR_WORDS(3)
+#undef GFR_WORDS
+#undef GFR_PAIR
+    }
+}
+
+// The 16 activations of one k tile, natural order in (a = halves 0..7, b = halves 8..15), rearranged into the 8
+// packed pairs of pair_row: out[m] = (x[ra(m)], x[rb(m)]).
+template <int K>
+__device__ __forceinline__ void pair_activations(const uint32_t (&a)[4], const uint32_t (&b)[4], uint32_t (&out)[8]) {
+    if constexpr (K == 2) {
+        // m = 4v + u: u = 0 (r = 4v), 1 (4v + 1), 2 (4v + 8), 3 (4v + 9); pair (x[r + 2], x[r])
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+            out[4 * v + 0] = __builtin_amdgcn_perm(a[2 * v], a[2 * v + 1], 0x05040100u);
+            out[4 * v + 1] = __builtin_amdgcn_perm(a[2 * v], a[2 * v + 1], 0x07060302u);
+            out[4 * v + 2] = __builtin_amdgcn_perm(b[2 * v], b[2 * v + 1], 0x05040100u);
+            out[4 * v + 3] = __builtin_amdgcn_perm(b[2 * v], b[2 * v + 1], 0x07060302u);
+        }
+    } else {
+        // m = 2l + h: (x[2l + 8 + h], x[2l + h])
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            out[2 * l] = __builtin_amdgcn_perm(a[l], b[l], 0x05040100u);
+            out[2 * l + 1] = __builtin_amdgcn_perm(a[l], b[l], 0x07060302u);
+        }
+    }
 }
 
 // The previous word for lane i of an 8-lane tile group: lane - 1, or lane + 7 for i == 0 (DPP within a 16-lane row).
@@ -76,7 +140,50 @@ __device__ __forceinline__ float bf16r(float x) {
 }
 __device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// fp16(a * b) with the product rounded to fp32 first, as the reference does (hipcc would otherwise fuse the multiply
+// and the conversion into one v_fma_mix rounding, which differs in rare double-rounding cases).
+__device__ __forceinline__ uint16_t f16_of_product(float a, float b) {
+    float p = a * b;
+    __asm__ volatile("" : "+v"(p));
+    return f32_to_f16(p);
+}
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+
+// The value of lane (lane ^ M) for M in {1, 2, 4, 8, 16, 32}, without LDS: DPP quad permutes and row shifts inside
+// 16-lane rows, the gfx950 permlane swaps across rows and halves.
+template <int M>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+    const int x = (int)v;
+    if constexpr (M == 1) {
+        return (uint32_t)__builtin_amdgcn_mov_dpp(x, 0xB1, 0xf, 0xf, false);   // quad_perm [1, 0, 3, 2]
+    } else if constexpr (M == 2) {
+        return (uint32_t)__builtin_amdgcn_mov_dpp(x, 0x4E, 0xf, 0xf, false);   // quad_perm [2, 3, 0, 1]
+    } else if constexpr (M == 4 || M == 8) {
+        const int up = __builtin_amdgcn_mov_dpp(x, 0x100 + M, 0xf, 0xf, false);  // row_shl: lane + M
+        const int dn = __builtin_amdgcn_mov_dpp(x, 0x110 + M, 0xf, 0xf, false);  // row_shr: lane - M
+        return (uint32_t)((__lane_id() & M) ? dn : up);
+    } else if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        return (uint32_t)((__lane_id() & 16) ? r[0] : r[1]);
+    } else {
+        static_assert(M == 32, "lane_xor: M in {1, 2, 4, 8, 16, 32}");
+        const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        return (uint32_t)((__lane_id() & 32) ? r[0] : r[1]);
+    }
+}
+template <int M>
+__device__ __forceinline__ float lane_xor_f(float v) {
+    return __builtin_bit_cast(float, lane_xor<M>(__builtin_bit_cast(uint32_t, v)));
+}
+
+template <int M>
+__device__ __forceinline__ void fwht_stage(float (&v)[2], int lane) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const float o = lane_xor_f<M>(v[j]);
+        v[j] = (lane & M) ? o - v[j] : v[j] + o;
+    }
+}
 
 // 128-point unnormalised Walsh-Hadamard transform of a wave64 row, two values a lane (v[j] = element 2 lane + j):
 // butterflies at strides 1, 2, ..., 64, each (lower + upper, lower - upper) -- experts.rs:25-42's order, so every
@@ -87,14 +194,30 @@ __device__ __forceinline__ void fwht128_w64(float (&v)[2], int lane) {
         v[0] = a + b;
         v[1] = a - b;
     }
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const float o = __shfl_xor(v[j], m, 64);
-            v[j] = (lane & m) ? o - v[j] : v[j] + o;
-        }
-    }
+    fwht_stage<1>(v, lane);
+    fwht_stage<2>(v, lane);
+    fwht_stage<4>(v, lane);
+    fwht_stage<8>(v, lane);
+    fwht_stage<16>(v, lane);
+    fwht_stage<32>(v, lane);
+}
+
+// Wave-wide reductions through lane_xor (every lane gets the result).
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, lane_xor_f<1>(v));
+    v = fmaxf(v, lane_xor_f<2>(v));
+    v = fmaxf(v, lane_xor_f<4>(v));
+    v = fmaxf(v, lane_xor_f<8>(v));
+    v = fmaxf(v, lane_xor_f<16>(v));
+    return fmaxf(v, lane_xor_f<32>(v));
+}
+__device__ __forceinline__ int wave_min(int v) {
+    v = min(v, (int)lane_xor<1>((uint32_t)v));
+    v = min(v, (int)lane_xor<2>((uint32_t)v));
+    v = min(v, (int)lane_xor<4>((uint32_t)v));
+    v = min(v, (int)lane_xor<8>((uint32_t)v));
+    v = min(v, (int)lane_xor<16>((uint32_t)v));
+    return min(v, (int)lane_xor<32>((uint32_t)v));
 }
 
 }  // namespace gfr

@@ -65,6 +65,7 @@ int check_shape(int hidden, int inter) {
         return fail(GFR_EINVAL, "hidden %d / inter %d must be positive multiples of 128", hidden, inter);
     if (hidden % 256 || inter % 256)
         return fail(GFR_EINVAL, "hidden %d / inter %d must be multiples of 256 (k split of the GEMV)", hidden, inter);
+    if (hidden / 128 > 4096 || inter / 128 > 4096) return fail(GFR_EINVAL, "hidden / inter too large");
     return 0;
 }
 
@@ -78,8 +79,8 @@ struct gfr_grouping {
 
 struct gfr_experts {
     int hidden, inter, slots, exl3_slots, max_rows;
-    uint16_t *xg, *xu, *xd;
-    float *z, *y;
+    uint16_t* xd;
+    float *zgu, *zd, *y;             // gate/up and down split partials, expert outputs
 };
 
 struct gfr_linear {
@@ -153,6 +154,32 @@ int gfr_grouping_destroy(gfr_grouping* g) {
 }
 
 // ---- decode / verify experts ------------------------------------------------------------------------------------
+namespace {
+// The decode launches: gate/up GEMV (+ rotation), down GEMV (+ gate/up epilogue), down epilogue (+ combine).
+int experts_run(gfr_experts* ex, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
+                int input_stride, const int32_t* picks, const int32_t* ids, const int32_t* count,
+                const int32_t* members, int rows, int maxm, const float* weights, float* out,
+                const gfr::RouteOne* route = nullptr) {
+    const int P = rows * ex->slots, D = ex->hidden, N = ex->inter;
+    const int maxu = P < w->experts ? P : w->experts;
+    hipError_t e;
+    if ((e = gfr::launch_expert_gateup(stream, input, input_stride, w->suh_g, w->suh_u, w->gt, w->ut, ids, count,
+                                       members, ex->zgu, D, N, P, rows, maxm, ex->slots, w->experts, w->bits, maxu,
+                                       route)) !=
+        hipSuccess)
+        return hip_fail(e, "gate/up gemv");
+    if ((e = gfr::launch_expert_down(stream, ex->zgu, D, w->svh_g, w->svh_u, w->suh_d, 10.f, ex->xd, w->dt, ids,
+                                     count, members, ex->zd, N, P, rows, maxm, ex->slots, w->experts, w->bits,
+                                     maxu)) !=
+        hipSuccess)
+        return hip_fail(e, "down gemv");
+    if ((e = gfr::launch_down_finish(stream, ex->zd, picks, w->svh_d, ex->y, rows, P, D, gfr::gemv_down_splits(N),
+                                     ex->slots, ex->exl3_slots, weights, out)) != hipSuccess)
+        return hip_fail(e, "down epilogue");
+    return 0;
+}
+}  // namespace
+
 int gfr_experts_create(gfr_experts** out, int hidden, int inter, int slots, int exl3_slots, int max_rows) {
     if (!out) return fail(GFR_EINVAL, "null out");
     *out = nullptr;
@@ -161,15 +188,13 @@ int gfr_experts_create(gfr_experts** out, int hidden, int inter, int slots, int 
     if (slots <= 0 || slots > 32 || exl3_slots < 0 || exl3_slots > slots)
         return fail(GFR_EINVAL, "slots %d / exl3_slots %d", slots, exl3_slots);
     if (max_rows <= 0 || max_rows > 64) return fail(GFR_EINVAL, "expert verifier scratch bound: max_rows %d", max_rows);
-    gfr_experts* ex = new gfr_experts{hidden, inter, slots, exl3_slots, max_rows, nullptr, nullptr, nullptr, nullptr,
+    gfr_experts* ex = new gfr_experts{hidden, inter, slots, exl3_slots, max_rows, nullptr, nullptr, nullptr,
                                       nullptr};
     const size_t P = (size_t)max_rows * slots;
-    const size_t SK = (size_t)(gfr::gemv_splits(hidden) > gfr::gemv_splits(inter) ? gfr::gemv_splits(hidden)
-                                                                                  : gfr::gemv_splits(inter));
-    const size_t zn = 2 * SK * P * (size_t)(hidden > inter ? hidden : inter);
-    if ((rc = alloc_zero(&ex->xg, P * hidden, "experts xg")) || (rc = alloc_zero(&ex->xu, P * hidden, "experts xu")) ||
-        (rc = alloc_zero(&ex->xd, P * inter, "experts xd")) || (rc = alloc_zero(&ex->z, zn, "experts z")) ||
-        (rc = alloc_zero(&ex->y, P * hidden, "experts y"))) {
+    const size_t zgu = 2 * (size_t)gfr::gemv_gateup_splits(hidden) * P * inter;
+    const size_t zd = (size_t)gfr::gemv_down_splits(inter) * P * hidden;
+    if ((rc = alloc_zero(&ex->xd, P * inter, "experts xd")) || (rc = alloc_zero(&ex->zgu, zgu, "experts zgu")) ||
+        (rc = alloc_zero(&ex->zd, zd, "experts zd")) || (rc = alloc_zero(&ex->y, P * hidden, "experts y"))) {
         gfr_experts_destroy(ex);
         return rc;
     }
@@ -188,25 +213,7 @@ int gfr_experts_run_rows(gfr_experts* ex, hipStream_t stream, const gfr_exl3_exp
                     ex->max_rows);
     if (!input || !picks || !ids || !count || !members) return fail(GFR_EINVAL, "null input");
     if (input_stride < ex->hidden) return fail(GFR_EINVAL, "input stride %d < hidden %d", input_stride, ex->hidden);
-    const int P = rows * ex->slots, D = ex->hidden, N = ex->inter;
-    const int maxu = P < w->experts ? P : w->experts;
-    hipError_t e;
-    if ((e = gfr::launch_rot_in(stream, input, input_stride, false, picks, w->suh_g, w->suh_u, ex->xg, ex->xu, D, P,
-                                ex->slots, ex->exl3_slots, 2)) != hipSuccess)
-        return hip_fail(e, "rot_in");
-    if ((e = gfr::launch_gemv(stream, ex->xg, ex->xu, w->gt, w->ut, ids, count, members, ex->z, D, N, P, maxm,
-                              ex->slots, w->experts, w->bits, 2, maxu)) != hipSuccess)
-        return hip_fail(e, "gate/up gemv");
-    if ((e = gfr::launch_gateup_epilogue(stream, ex->z, picks, w->svh_g, w->svh_u, w->suh_d, ex->xd, P, N,
-                                         gfr::gemv_splits(D), ex->slots, ex->exl3_slots, 10.f)) != hipSuccess)
-        return hip_fail(e, "gate/up epilogue");
-    if ((e = gfr::launch_gemv(stream, ex->xd, ex->xd, w->dt, w->dt, ids, count, members, ex->z, N, D, P, maxm,
-                              ex->slots, w->experts, w->bits, 1, maxu)) != hipSuccess)
-        return hip_fail(e, "down gemv");
-    if ((e = gfr::launch_down_epilogue(stream, ex->z, picks, w->svh_d, ex->y, P, D, gfr::gemv_splits(N), ex->slots,
-                                       ex->exl3_slots)) != hipSuccess)
-        return hip_fail(e, "down epilogue");
-    return 0;
+    return experts_run(ex, stream, w, input, input_stride, picks, ids, count, members, rows, maxm, nullptr, nullptr);
 }
 
 float* gfr_experts_y(const gfr_experts* ex) { return ex ? ex->y : nullptr; }
@@ -214,7 +221,7 @@ uint16_t* gfr_experts_xd(const gfr_experts* ex) { return ex ? ex->xd : nullptr; 
 
 int gfr_experts_destroy(gfr_experts* ex) {
     if (!ex) return 0;
-    free_all({ex->xg, ex->xu, ex->xd, ex->z, ex->y});
+    free_all({ex->xd, ex->zgu, ex->zd, ex->y});
     delete ex;
     return 0;
 }
@@ -286,6 +293,27 @@ int gfr_exl3_grouped_gemv(hipStream_t stream, const uint16_t* x0, const uint16_t
     hipError_t e = gfr::launch_gemv(stream, x0, x1 ? x1 : x0, t0, t1 ? t1 : t0, uids, ucount, members, z, kin, n,
                                     pairs, maxm, slots, experts, bits, mats, maxu);
     if (e != hipSuccess) return hip_fail(e, "grouped gemv");
+    return 0;
+}
+
+// ---- router alone -----------------------------------------------------------------------------------------------
+int gfr_route_topk(hipStream_t stream, const float* logits, int rows, int routed, int topk, int32_t* picks,
+                   float* weights) {
+    if (!logits || !picks || !weights) return fail(GFR_EINVAL, "null argument");
+    if (rows <= 0 || routed <= 0 || routed > 1024 || topk <= 0 || topk > 31 || topk > routed)
+        return fail(GFR_EINVAL, "rows %d routed %d topk %d", rows, routed, topk);
+    hipError_t e = gfr::launch_route(stream, logits, rows, routed, topk, routed, picks, weights);
+    if (e != hipSuccess) return hip_fail(e, "route");
+    return 0;
+}
+
+// ---- debug rotation ---------------------------------------------------------------------------------------------
+int gfr_exl3_rotate(hipStream_t stream, const uint16_t* x, int x_stride, int x_f16, const int32_t* expert,
+                    const uint16_t* suh, int k, int rows, uint16_t* out) {
+    if (!x || !expert || !suh || !out) return fail(GFR_EINVAL, "null argument");
+    if (k <= 0 || k % 128 || rows <= 0 || x_stride < k) return fail(GFR_EINVAL, "k %d rows %d stride %d", k, rows, x_stride);
+    hipError_t e = gfr::launch_rot_in(stream, x, x_stride, x_f16 != 0, expert, suh, suh, out, out, k, rows, 1, 1, 1);
+    if (e != hipSuccess) return hip_fail(e, "rotate");
     return 0;
 }
 
@@ -393,18 +421,27 @@ int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const
     if (rows <= 0 || rows > m->max_rows) return fail(GFR_EINVAL, "rows %d outside 1..%d", rows, m->max_rows);
     if (!input || !logits) return fail(GFR_EINVAL, "null input");
     hipError_t e;
-    if ((e = gfr::launch_route(stream, logits, rows, m->routed, m->topk, m->routed, m->picks, m->weights)) !=
-        hipSuccess)
+    if (rows > m->decode_rows &&
+        (e = gfr::launch_route(stream, logits, rows, m->routed, m->topk, m->routed, m->picks, m->weights)) !=
+            hipSuccess)
         return hip_fail(e, "route");
-    const float* y;
     if (rows <= m->decode_rows) {
         gfr_grouping* g = m->group_dec;
-        if ((rc = gfr_grouping_run(g, stream, m->picks, rows))) return rc;
-        if ((rc = gfr_experts_run_rows(m->dec, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members,
-                                       rows, g->max_rows)))
-            return rc;
-        y = m->dec->y;
-    } else {
+        if (rows == 1) {
+            // three launches: gate/up (+ route, rotation), down (+ gate/up epilogue), down epilogue (+ combine)
+            const gfr::RouteOne r{logits, m->routed, m->picks, m->weights, g->ids, g->count, g->members};
+            return experts_run(m->dec, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members, 1,
+                               g->max_rows, m->weights, m->out, &r);
+        }
+        // four launches: route + group, gate/up (+ rotation), down (+ gate/up epilogue), down epilogue (+ combine)
+        if ((e = gfr::launch_route_group(stream, logits, rows, m->routed, m->topk, m->picks, m->weights, g->ids,
+                                         g->count, g->members, g->max_rows)) != hipSuccess)
+            return hip_fail(e, "route + group");
+        return experts_run(m->dec, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members, rows,
+                           g->max_rows, m->weights, m->out);
+    }
+    const float* y;
+    {
         gfr_grouping* g = m->group_pre;
         if ((rc = gfr_grouping_run(g, stream, m->picks, rows))) return rc;
         if ((rc = gfr_fast_experts_run(m->pre, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members,

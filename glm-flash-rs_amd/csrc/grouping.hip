@@ -12,6 +12,7 @@
 // reference's 8192-row limit.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include "route.hpp"
 
 namespace gfr {
 
@@ -44,12 +45,11 @@ __device__ __forceinline__ int first_slot(const int* __restrict__ picks, int r, 
     return s;
 }
 
-// One workgroup of 1024 threads. LDS: E * ceil(rows / 32) bitmap words + E counts.
-__global__ void __launch_bounds__(1024) group_small_kernel(const int* __restrict__ picks, int rows, int slots,
-                                                           int E, int* __restrict__ ids, int* __restrict__ count,
-                                                           int* __restrict__ members, int maxm) {
-    extern __shared__ uint32_t lds[];
-    __shared__ int scan_scratch[16];
+// One workgroup (blockDim.x a multiple of 64, <= 1024). lds: E * ceil(rows / 32) bitmap words + 2 E ints.
+// picks may live in LDS or global memory.
+__device__ __forceinline__ void group_small_body(const int* picks, int rows, int slots, int E, int* __restrict__ ids,
+                                                 int* __restrict__ count, int* __restrict__ members, int maxm,
+                                                 uint32_t* lds, int* scan_scratch) {
     const int NWD = (rows + 31) >> 5;
     uint32_t* bits = lds;                                    // [E][NWD]
     int* ucnt = reinterpret_cast<int*>(lds + (size_t)E * NWD);  // [E]: count of the u-th used expert
@@ -101,6 +101,37 @@ __global__ void __launch_bounds__(1024) group_small_kernel(const int* __restrict
         const int u = (int)(i / maxm), j = (int)(i % maxm);
         if (u >= used || j >= ucnt[u]) members[i] = -1;
     }
+}
+
+__global__ void __launch_bounds__(1024) group_small_kernel(const int* __restrict__ picks, int rows, int slots,
+                                                           int E, int* __restrict__ ids, int* __restrict__ count,
+                                                           int* __restrict__ members, int maxm) {
+    extern __shared__ uint32_t lds[];
+    __shared__ int scan_scratch[16];
+    group_small_body(picks, rows, slots, E, ids, count, members, maxm, lds, scan_scratch);
+}
+
+// Decode windows in one launch: wave w routes tokens w, w + 16, ... (route.hpp) into LDS and global picks /
+// weights, then the workgroup groups them (group_small_body). rows <= GROUP_SMALL_ROWS.
+__global__ void __launch_bounds__(1024) route_group_kernel(const float* __restrict__ logits, int rows, int routed,
+                                                           int topk, int* __restrict__ picks,
+                                                           float* __restrict__ weights, int* __restrict__ ids,
+                                                           int* __restrict__ count, int* __restrict__ members,
+                                                           int maxm) {
+    extern __shared__ uint32_t lds[];
+    __shared__ int scan_scratch[16];
+    const int slots = topk + 1, E = routed + 1;
+    int* pk = reinterpret_cast<int*>(lds);                     // [rows][slots]
+    float* wt = reinterpret_cast<float*>(pk + rows * slots);   // [rows][slots]
+    uint32_t* rest = reinterpret_cast<uint32_t*>(wt + rows * slots);
+    for (int r = threadIdx.x >> 6; r < rows; r += blockDim.x >> 6)
+        route_token(logits + (size_t)r * routed, routed, topk, routed, pk + r * slots, wt + r * slots);
+    __syncthreads();
+    for (int i = threadIdx.x; i < rows * slots; i += blockDim.x) {
+        picks[i] = pk[i];
+        weights[i] = wt[i];
+    }
+    group_small_body(pk, rows, slots, E, ids, count, members, maxm, rest, scan_scratch);
 }
 
 // Large windows, launch 1: the 256 rows of this workgroup marked in an LDS bitmap [E][8], stored to
@@ -199,6 +230,14 @@ hipError_t launch_group_small(hipStream_t s, const int* picks, int rows, int slo
                               int* members, int maxm) {
     const size_t lds = ((size_t)E * ((rows + 31) / 32) + 2 * (size_t)E) * 4;
     group_small_kernel<<<1, 1024, lds, s>>>(picks, rows, slots, E, ids, count, members, maxm);
+    return hipGetLastError();
+}
+
+hipError_t launch_route_group(hipStream_t s, const float* logits, int rows, int routed, int topk, int* picks,
+                              float* weights, int* ids, int* count, int* members, int maxm) {
+    const int E = routed + 1, slots = topk + 1;
+    const size_t lds = (2 * (size_t)rows * slots + (size_t)E * ((rows + 31) / 32) + 2 * (size_t)E) * 4;
+    route_group_kernel<<<1, 1024, lds, s>>>(logits, rows, routed, topk, picks, weights, ids, count, members, maxm);
     return hipGetLastError();
 }
 

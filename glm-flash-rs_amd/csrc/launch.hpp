@@ -9,6 +9,9 @@ namespace gfr {
 constexpr int GROUP_SMALL_ROWS = 256;
 hipError_t launch_group_small(hipStream_t s, const int* picks, int rows, int slots, int E, int* ids, int* count,
                               int* members, int maxm);
+// route (route.hpp) + group_small in one launch; rows <= GROUP_SMALL_ROWS, routed + 1 <= 1024
+hipError_t launch_route_group(hipStream_t s, const float* logits, int rows, int routed, int topk, int* picks,
+                              float* weights, int* ids, int* count, int* members, int maxm);
 hipError_t launch_group_large(hipStream_t s, const int* picks, int rows, int slots, int E, uint32_t* bits,
                               int* prefix, int* counts, int* ids, int* count, int* members, int maxm);
 
@@ -22,6 +25,33 @@ int gemv_splits(int Kin);  // K splits of the decode GEMV (fixed by the shape, s
 hipError_t launch_gemv(hipStream_t s, const uint16_t* X0, const uint16_t* X1, const uint32_t* T0, const uint32_t* T1,
                        const int* uids, const int* ucount, const int* members, float* Z, int Kin, int N, int P,
                        int maxm, int slots, int E, int bits, int mats, int maxu);
+int gemv_gateup_splits(int D);  // K splits of the decode gate/up GEMV (one 128-block a wave, 4 waves)
+int gemv_down_splits(int N);    // K splits of the decode down GEMV (one 128-block a wave, 2 waves)
+// Decode path: gate/up GEMV with rot_in fused (-> gate/up split partials Zgu [2][SK][P][N]); down GEMV with the
+// gate/up epilogue fused as its activation source (-> Zd [SK][P][D], xd [P][N]); down epilogue + combine.
+// The gate/up GEMV needs gemv_gateup_splits(D) <= 4.
+// One-token windows can route inside the gate/up launch: the token's logits, and where to store its picks /
+// weights and the window's grouping (ids, count, members with stride maxm) for the later launches.
+struct RouteOne {
+    const float* logits;
+    int routed;
+    int* picks;
+    float* weights;
+    int* ids;
+    int* count;
+    int* members;
+};
+hipError_t launch_expert_gateup(hipStream_t s, const uint16_t* x, int x_stride, const uint16_t* suh_g,
+                                const uint16_t* suh_u, const uint32_t* gt, const uint32_t* ut, const int* uids,
+                                const int* ucount, const int* members, float* Zgu, int D, int N, int P, int rows,
+                                int maxm, int slots, int E, int bits, int maxu, const RouteOne* route);
+hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, const uint16_t* svh_g, const uint16_t* svh_u,
+                              const uint16_t* suh_d, float limit, uint16_t* xd, const uint32_t* dt, const int* uids,
+                              const int* ucount, const int* members, float* Zd, int N, int P, int rows, int maxm,
+                              int slots, int E, int bits, int maxu);
+hipError_t launch_down_finish(hipStream_t s, const float* Zd, const int* pick, const uint16_t* svh_d, float* y,
+                              int rows, int P, int D, int SK, int slots, int exl3_slots, const float* weights,
+                              float* out);
 hipError_t launch_gateup_epilogue(hipStream_t s, const float* Z, const int* pick, const uint16_t* svh_g,
                                   const uint16_t* svh_u, const uint16_t* suh_d, uint16_t* xd, int P, int N, int SK,
                                   int slots, int exl3_slots, float limit);

@@ -5,61 +5,14 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "route.hpp"
+
 namespace gfr {
 
-// One wave a row; E <= 64 * 16 logits.
 __global__ void __launch_bounds__(64) route_kernel(const float* __restrict__ logits, int E, int topk, int shared_id,
                                                    int* __restrict__ picks, float* __restrict__ weights) {
-    constexpr int PER = 16;
-    const int r = blockIdx.x, lane = threadIdx.x, slots = topk + 1;
-    const float* l = logits + (size_t)r * E;
-    float v[PER];
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-        const int e = j * 64 + lane;
-        v[j] = e < E ? l[e] : -__builtin_inff();
-    }
-    uint32_t taken = 0;                        // bit j: expert j * 64 + lane is picked
-    int* pk = picks + (size_t)r * slots;
-    float* wt = weights + (size_t)r * slots;
-    for (int s = 0; s < topk; ++s) {
-        float bv = -__builtin_inff();
-        int be = 0x7fffffff;
-#pragma unroll
-        for (int j = 0; j < PER; ++j) {
-            const int e = j * 64 + lane;
-            if (e < E && !((taken >> j) & 1u) && (v[j] > bv || be == 0x7fffffff)) {
-                bv = v[j];
-                be = e;
-            }
-        }
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) {
-            const float ov = __shfl_xor(bv, m, 64);
-            const int oe = __shfl_xor(be, m, 64);
-            if (ov > bv || (ov == bv && oe < be)) {
-                bv = ov;
-                be = oe;
-            }
-        }
-        if ((be & 63) == lane) taken |= 1u << (be >> 6);
-        if (lane == 0) {
-            pk[s] = be;
-            wt[s] = bv;                           // the logit, until the weights below
-        }
-    }
-    if (lane == 0) {
-        const float m = wt[0];
-        float sum = 0.f;
-        for (int s = 0; s < topk; ++s) {
-            const float ex = expf(wt[s] - m);
-            wt[s] = ex;
-            sum += ex;
-        }
-        for (int s = 0; s < topk; ++s) wt[s] = wt[s] / sum;
-        pk[topk] = shared_id;
-        wt[topk] = 1.f;
-    }
+    const int r = blockIdx.x, slots = topk + 1;
+    route_token(logits + (size_t)r * E, E, topk, shared_id, picks + (size_t)r * slots, weights + (size_t)r * slots);
 }
 
 // out[r][n] = sum over slots s (in order) of weights[r][s] * y[r * slots + s][n]

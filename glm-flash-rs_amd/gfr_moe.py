@@ -63,6 +63,8 @@ def _load() -> ctypes.CDLL:
         "gfr_linear_destroy": ([VP], I),
         "gfr_exl3_decode_tiles": ([P, P, I, I, I, P], I),
         "gfr_exl3_gemv_splits": ([I], I),
+        "gfr_exl3_rotate": ([P, P, I, I, P, P, I, I, P], I),
+        "gfr_route_topk": ([P, P, I, I, I, P, P], I),
         "gfr_exl3_grouped_gemv": ([P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I], I),
     }
     for name, (args, res) in sig.items():
@@ -284,6 +286,24 @@ class Linear(_Engine):
 
     def run(self, x, trellis, suh, svh, y, stream=None):
         _check(lib().gfr_linear_run(self._h, _stream(stream), _ptr(x), _ptr(trellis), _ptr(suh), _ptr(svh), _ptr(y)))
+
+
+def route(logits: torch.Tensor, topk: int, stream=None):
+    """The router alone: (picks [rows, topk + 1] int32, weights [rows, topk + 1] fp32), shared id = routed."""
+    rows, routed = logits.shape
+    picks = torch.empty((rows, topk + 1), dtype=torch.int32, device=logits.device)
+    weights = torch.empty((rows, topk + 1), dtype=torch.float32, device=logits.device)
+    _check(lib().gfr_route_topk(_stream(stream), _ptr(logits), rows, routed, topk, _ptr(picks), _ptr(weights)))
+    return picks, weights
+
+
+def rotate(x: torch.Tensor, expert: torch.Tensor, suh: torch.Tensor, stream=None) -> torch.Tensor:
+    """rot_in's formula (exl3.cu:224-241) on rows x [rows, k] (bf16 or fp16) with per-row experts: fp16 [rows, k]."""
+    rows, k = x.shape
+    out = torch.empty((rows, k), dtype=torch.float16, device=x.device)
+    _check(lib().gfr_exl3_rotate(_stream(stream), _ptr(x), x.stride(0), int(x.dtype == torch.float16), _ptr(expert),
+                                 _ptr(suh), k, rows, _ptr(out)))
+    return out
 
 
 def decode_tiles(trellis: torch.Tensor, kin: int, n: int, bits: int, stream=None) -> torch.Tensor:

@@ -111,6 +111,12 @@ float* gfr_moe_weights(const gfr_moe* m);        /* [rows][topk + 1] */
 int gfr_moe_set_decode_rows(gfr_moe* m, int decode_rows);  /* rows at or below run the decode path (default 64) */
 int gfr_moe_destroy(gfr_moe* m);
 
+/* ---- The router alone (the reference's Triton topk, moe.rs:89-100; source absent, semantics of the benchmark):
+ * logits [rows][routed] fp32 -> picks / weights [rows][topk + 1]: top-k by logit (ties: lower id), weights the
+ * softmax over the k picks (summed in slot order), then the shared expert id `routed` with weight 1. */
+int gfr_route_topk(hipStream_t stream, const float* logits, int rows, int routed, int topk, int32_t* picks,
+                   float* weights);
+
 /* ---- Single EXL3 linear (benchmark config 1; the decode path's GEMV with rot_in / down-epilogue formulas) ----
  * y [n] fp32 = svh * had(W^T xh) / sqrt(128), xh = fp16(had(x * suh) / sqrt(128)), x [kin] fp16. */
 typedef struct gfr_linear gfr_linear;
@@ -129,6 +135,12 @@ int gfr_exl3_grouped_gemv(hipStream_t stream, const uint16_t* x0, const uint16_t
                           const uint32_t* t1, const int32_t* uids, const int32_t* ucount, const int32_t* members,
                           float* z, int kin, int n, int pairs, int maxm, int slots, int experts, int bits, int mats,
                           int maxu);
+
+/* ---- Debug / parity: the input rotation alone (rot_in, exl3.cu:224-241), bit-exact to the CPU restatement:
+ * out[r][k] = fp16(had(x[r] * suh[expert[r]]) / sqrt(128)); x [rows][x_stride] bf16 (x_f16 = 0) or fp16;
+ * suh [experts][k] fp16; k a multiple of 128. */
+int gfr_exl3_rotate(hipStream_t stream, const uint16_t* x, int x_stride, int x_f16, const int32_t* expert,
+                    const uint16_t* suh, int k, int rows, uint16_t* out);
 
 /* ---- Debug / parity: decoded fp16 weights of one matrix [kin][n] (row = k), bit-exact to experts.rs:47-74 ---- */
 int gfr_exl3_decode_tiles(hipStream_t stream, const uint32_t* trellis, int kin, int n, int bits, uint16_t* out);
