@@ -146,6 +146,35 @@ def gemv_roofline(args, copies, stream):
             "us_per_launch": round(per * 1e6, 3)}
 
 
+def prefill_bench(args, copies, stream):
+    """Config 4: one MoE layer on an 8192-token prefill chunk, uniform top-4 routing (+ the shared expert)."""
+    import torch
+    import gfr_moe
+    import synth
+    rows = args.prefill_rows
+    moe = gfr_moe.Moe(D, N, E, TOPK, rows)
+    xs = synth.activations(rows, D, 21)
+    lgs = [synth.logits(rows, E, 22 + j) for j in range(2)]
+    ws = copies[:2]
+
+    def step(j):
+        return lambda: moe.run(ws[j % 2], xs, lgs[j % 2], rows, stream=stream)
+
+    g = graph_of([step(0), step(1)], stream)
+    time_graphs([g], stream)
+    n = max(args.prefill_steps // 2, 1)
+    secs = time_graphs([g] * n, stream) / (2 * n)
+    pairs_routed, pairs_shared = rows * TOPK, rows
+    flop = (pairs_routed + pairs_shared) * 2 * (2 * D * N + N * D)
+    tflops = flop / secs / 1e12
+    return {"config": f"config 4: {rows} tokens x top-4 uniform + shared, one MoE layer (route, group, rotate, "
+                      "gate/up + down MFMA grouped GEMMs, combine)",
+            "tok_per_s": round(rows / secs, 1), "ms_per_layer": round(secs * 1e3, 4),
+            "gflop": round(flop / 1e9, 1), "gflop_routed_only": round(pairs_routed * 2 * 3 * D * N / 1e9, 1),
+            "achieved_tflops": round(tflops, 1), "mfma_peak_tflops": MFMA_F16_PEAK_TFLOPS,
+            "mfma_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+
+
 def cpu_baseline(args, copies, xs, logits):
     import numpy as np
     import torch
@@ -183,6 +212,9 @@ def main():
     ap.add_argument("--kernel-launches", type=int, default=2048)
     ap.add_argument("--cpu-tokens", type=int, default=6)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--prefill-rows", type=int, default=8192)
+    ap.add_argument("--prefill-steps", type=int, default=20)
+    ap.add_argument("--no-prefill", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -193,6 +225,10 @@ def main():
     log(f"decode: {args.steps} steps in {secs * 1e3:.2f} ms")
     roof = gemv_roofline(args, copies, stream)
     log(f"gate/up gemv alone: {roof['us_per_launch']} us, {roof['achieved']} GB/s")
+    prefill = None
+    if not args.no_prefill:
+        prefill = prefill_bench(args, copies, stream)
+        log(f"prefill: {prefill['ms_per_layer']} ms/layer, {prefill['achieved_tflops']} TFLOP/s")
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(args, copies, xs, logits)
@@ -204,7 +240,7 @@ def main():
         "config": {"workload": "config 2: one MoE layer, bs=1 decode, hidden 2048, 64 routed + 1 shared EXL3 "
                                "experts, inter 1536, top-4, K=4", "global_batch": 1, "seq_len": 1,
                    "parallelism": "single-gpu", "weight_copies": args.copies, "routings": args.routings},
-        "roofline": roof, "cpu_baseline": cpu,
+        "roofline": roof, "cpu_baseline": cpu, "prefill": prefill,
     }
     print(json.dumps(out), flush=True)
 

@@ -1,14 +1,392 @@
-// Prefill-chunk experts on gfx950 (placeholder engine: scratch ownership; the MFMA kernels come next).
+// Prefill-chunk experts on gfx950: grouped trellis GEMMs on fp16 MFMA with the reference's fused epilogues.
+//
+// Same contract as glm-flash-rs FastExperts (src/fast_experts.rs:91-208) and its kernels (native/exl3_prefill.cu):
+//   gate/up  xd[p] = fp16(H(act * suh_d)), act = limited SwiGLU(H(Xg[p] @ Wg) * svh_g, H(Xu[p] @ Wu) * svh_u)
+//   down     y[p]  = H(xd[p] @ Wd) * svh_d                                                       (fp32)
+// for every routed pair p (H = the 128-block Hadamard / sqrt(128)), each output one full-K fp32 accumulation chain
+// (exl3_prefill.cu:14-23: no split-K partials), deterministic and row-independent.
+//
+// MI355X design:
+//   * Y^T = W^T X^T on v_mfma_f32_16x16x32_f16: the trellis-decoded weights are the A operand, decoded straight into
+//     MFMA registers. A lane that owns column c of a 16x16 tile and one pair of its words (4i + 2g, 4i + 2g + 1)
+//     holds exactly 8 values of that column -- rows {2l + 8 + h, 2l + h} -- which is one A-fragment lane
+//     (16 n x 8 k) once k is taken in the pair order of exl3_format.hpp (pair_row); the token rows (B operand) are
+//     staged in LDS in that same order, so no weight ever goes through LDS and none is decoded twice in a workgroup.
+//   * workgroup = 4 waves, a tile of BM = 128 member rows of one expert x 128 (gate/up: both matrices) or 256 (down)
+//     output columns; each wave owns 64 columns x 128 rows (32 MFMA 16x16 accumulators), K in steps of 32 with the
+//     next step's trellis words and token rows loaded while the current step multiplies (LDS double buffer).
+//   * the 128 columns of a gate/up item, and each 128 of a down item, are one Hadamard block, so the epilogue
+//     (transforms, scales, SwiGLU) runs in the workgroup: accumulators -> LDS (32 rows at a time) -> one wave a row.
+//   * work items (distinct expert u, pass of BM members) come from a plan kernel (member counts by parallel search,
+//     scan); grid = items x column groups, no empty launches past the plan.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include "exl3_format.hpp"
 #include "launch.hpp"
 #include "prefill.hpp"
 
+namespace gfr {
+
+constexpr int PF_BM = 128;          // member rows an item
+constexpr int PF_MAXU = 1024;       // distinct experts a window (grid / plan bound)
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+// ---- plan -----------------------------------------------------------------------------------------------------
+// ucnt[u] = members of distinct expert u (the first -1 of its members row, found by a parallel search: 64 probes a
+// round); items[k] = (u << 16) | pass for the passes of BM members, in u order; plan[0] = item count.
+__global__ void __launch_bounds__(1024) prefill_plan_kernel(const int* __restrict__ uids,
+                                                            const int* __restrict__ ucount,
+                                                            const int* __restrict__ members, int maxm, int E,
+                                                            int maxu, int* __restrict__ ucnt,
+                                                            int* __restrict__ items, int* __restrict__ plan) {
+    __shared__ int passes[PF_MAXU];
+    __shared__ int scan_w[16];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwv = blockDim.x >> 6;
+    const int count = ucount[0];
+    for (int u = wave; u < maxu; u += nwv) {
+        int n = 0;
+        if (u < count && uids[u] < E) {
+            const int* m = members + (size_t)u * maxm;
+            int lo = 0, hi = maxm;                       // the first -1 lies in [lo, hi]
+            while (hi - lo > 1) {
+                const int stride = (hi - lo + 63) / 64;
+                const int pos = lo + lane * stride;
+                const bool ok = pos < hi && m[pos] >= 0;
+                const uint64_t bal = __ballot(ok);
+                const int last = bal ? 63 - __builtin_clzll(bal) : -1;   // members come first
+                if (last < 0) { hi = lo; break; }        // m[lo] < 0
+                const int nlo = lo + last * stride;
+                hi = min(hi, nlo + stride);
+                lo = nlo + 1;
+                if (lo >= hi) break;
+            }
+            // lo = first unprobed position after the last member found, hi = bound; settle the last one
+            n = (lo < maxm && lo < hi && m[lo] >= 0) ? lo + 1 : lo;
+            if (hi == 0) n = 0;
+        }
+        if (lane == 0) {
+            ucnt[u] = n;
+            passes[u] = (n + PF_BM - 1) / PF_BM;
+        }
+    }
+    __syncthreads();
+    // exclusive scan of passes over u (blocks of blockDim.x)
+    int base = 0;
+    for (int u0 = 0; u0 < maxu; u0 += blockDim.x) {
+        const int u = u0 + threadIdx.x;
+        int x = u < maxu ? passes[u] : 0;
+        int v = x;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int o = __shfl_up(v, d, 64);
+            if (lane >= d) v += o;
+        }
+        if (lane == 63) scan_w[wave] = v;
+        __syncthreads();
+        int off = 0, all = 0;
+        for (int w = 0; w < nwv; ++w) {
+            const int s = scan_w[w];
+            if (w < wave) off += s;
+            all += s;
+        }
+        __syncthreads();
+        const int first = base + off + v - x;
+        for (int k = 0; k < x; ++k) items[first + k] = (u << 16) | k;
+        base += all;
+    }
+    if (threadIdx.x == 0) plan[0] = base;
+}
+
+// ---- rotation ----------------------------------------------------------------------------------------------
+// The pair order of a k tile (pair_row, K = 4): 16 values x[8], x[0], x[9], x[1], ... x[15], x[7]. A wave that holds
+// elements 2 lane, 2 lane + 1 of a 128-block stores them packed: lane j < 4 of each 8-lane group (rows 2j, 2j + 1, the
+// high halves of pairs 2j, 2j + 1) takes the low halves from lane j + 4 (rows 2j + 8, 2j + 9) and writes 8 bytes.
+__device__ __forceinline__ void store_pair_order(uint16_t* block, const float (&v)[2], int lane) {
+    const uint16_t h0 = f16_of_product(v[0], HAD_SCALE), h1 = f16_of_product(v[1], HAD_SCALE);
+    const uint32_t mine = (uint32_t)h0 | ((uint32_t)h1 << 16);
+    const uint32_t other = lane_xor<4>(mine);
+    if ((lane & 4) == 0) {
+        const int kt = lane >> 3, j = lane & 7;
+        const uint32_t d0 = (other & 0xffffu) | ((mine & 0xffffu) << 16);     // pair 2j: (x[2j + 8], x[2j])
+        const uint32_t d1 = (other >> 16) | (mine & 0xffff0000u);             // pair 2j + 1
+        *reinterpret_cast<uint2*>(block + kt * 16 + 4 * j) = make_uint2(d0, d1);
+    }
+}
+
+// rot_in for prefill chunks (exl3.cu:224-241, bit for bit): one wave a (token, 128-block), all its EXL3 slots and
+// both matrices; x read once, the rotated rows written in pair order (the MFMA B operand's k order).
+__global__ void __launch_bounds__(256) prefill_rot_kernel(const uint16_t* __restrict__ x, int x_stride,
+                                                          const int* __restrict__ pick,
+                                                          const uint16_t* __restrict__ suh0,
+                                                          const uint16_t* __restrict__ suh1, uint16_t* __restrict__ out0,
+                                                          uint16_t* __restrict__ out1, int K, int rows, int slots,
+                                                          int exl3_slots, int mats) {
+    const int lane = threadIdx.x & 63;
+    const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int KB = K / 128, row = task / KB, blk = task % KB;
+    if (row >= rows) return;
+    const int k = blk * 128 + 2 * lane;
+    const uint32_t xv = *reinterpret_cast<const uint32_t*>(x + (size_t)row * x_stride + k);
+    const float x0 = bf16_to_f32((uint16_t)xv), x1 = bf16_to_f32((uint16_t)(xv >> 16));
+    for (int s = 0; s < exl3_slots; ++s) {
+        const int p = row * slots + s, e = pick[p];
+        for (int m = 0; m < mats; ++m) {
+            const uint32_t sv = *reinterpret_cast<const uint32_t*>((m ? suh1 : suh0) + (size_t)e * K + k);
+            float v[2] = {x0 * f16_to_f32((uint16_t)sv), x1 * f16_to_f32((uint16_t)(sv >> 16))};
+            fwht128_w64(v, lane);
+            store_pair_order((m ? out1 : out0) + (size_t)p * K + blk * 128, v, lane);
+        }
+    }
+}
+
+// ---- GEMM --------------------------------------------------------------------------------------------------------
+struct PrefillArgs {
+    const uint16_t* x0;      // rows [P][Kin] fp16 in pair order, matrix 0 (gate, or the down input xd)
+    const uint16_t* x1;      // of matrix 1 (up); == x0 when the input rotations are shared
+    const uint32_t* t0;      // trellis [E][Kin/16][N/16][32]
+    const uint32_t* t1;
+    const int* uids;
+    const int* members;
+    const int* ucnt;
+    const int* items;
+    const int* plan;
+    int Kin, N, maxm, slots;
+    const uint16_t* sv0;     // gate/up: svh_g, svh_u, suh_d; down: svh_d
+    const uint16_t* sv1;
+    const uint16_t* sd;
+    uint16_t* xd;            // gate/up output [P][N] fp16 in pair order
+    float* y;                // down output [P][N]
+    float limit;
+};
+
+// The A fragment of one 16-column trellis tile over two k tiles (K = 4): lane l owns column c = l % 16 of the tile
+// (format lane i = c % 8, value half c / 8) for k tile q / 2 and word pair g = q % 2 (q = l / 16): words 4i + 2g and
+// 4i + 2g + 1 hold its 8 values, rows (2l + 8 + h, 2l + h) for l = 2g, 2g + 1 -- the pair order of pair_row, the order
+// the token rows are staged in. tw: the tile's words of the two k tiles in LDS, [2][32].
+__device__ __forceinline__ h8_t a_fragment4(const uint32_t* tw, int lane) {
+    const int c = lane & 15, i = c & 7, q = lane >> 4, kt = q >> 1, g = q & 1;
+    const uint32_t* w = tw + kt * 32;
+    const int w0i = 4 * i + 2 * g;
+    const uint32_t p0 = w[(w0i + 31) & 31];
+    const uint2 ww = *reinterpret_cast<const uint2*>(w + w0i);
+    const uint32_t w0 = ww.x, w1 = ww.y;
+    const uint32_t sel = (c >> 3) ? 0x02010100u : 0x04030302u;   // value half: (s6,s4)/(s7,s5) or (s2,s0)/(s3,s1)
+    uint32_t s[4];
+    {
+        const uint32_t a = __builtin_amdgcn_alignbit(p0, w0, 4), b = p0 >> 4;
+        s[0] = __builtin_amdgcn_perm(b, a, sel);
+        s[1] = __builtin_amdgcn_perm(p0, w0, sel);
+    }
+    {
+        const uint32_t a = __builtin_amdgcn_alignbit(w0, w1, 4), b = w0 >> 4;
+        s[2] = __builtin_amdgcn_perm(b, a, sel);
+        s[3] = __builtin_amdgcn_perm(w0, w1, sel);
+    }
+    h8_t f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const h2_t v = decode_pair(s[j]);
+        f[2 * j] = v[0];
+        f[2 * j + 1] = v[1];
+    }
+    return f;
+}
+
+// 16-byte direct-to-LDS load: lane i's 16 bytes land at lds_base + 16 i.
+__device__ __forceinline__ void load_lds16(const void* g, void* lds_base) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                     (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+}
+
+// Workgroup barrier for LDS-only hand-offs: this wave's LDS operations complete, then s_barrier. Unlike
+// __syncthreads() it does not wait for outstanding global loads (the staged direct-to-LDS loads of later steps).
+__device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// s_waitcnt vmcnt(n), other counters unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Item (u, pass) x column group cg. MATS = 2: gate + up, 128 columns of each (waves 0-1 gate, 2-3 up); MATS = 1:
+// down, 256 columns (wave w: columns 64 w ..). Rows: the pass's BM = 256 members of expert u (pairs). Each wave:
+// 64 columns (4 trellis tiles, A fragments decoded in registers) x 256 rows (16 B fragments from LDS), 64 MFMAs a
+// step of 32 k. Staging: NS LDS stages filled by direct-to-LDS loads NS - 1 steps ahead; a staged row keeps its four
+// 16-byte chunks XOR-swizzled by (row >> 1) & 3 to spread the B-fragment reads over the banks.
+template <int MATS>
+__global__ void __launch_bounds__(256, 2) prefill_gemm_kernel(const PrefillArgs a) {
+    constexpr int BM = PF_BM, NCOLS = MATS == 2 ? 128 : 256, NS = 3, RG = BM / 16;
+    constexpr int XBUF = BM * 64;                        // one matrix's rows of a step (2 k tiles)
+    constexpr int TBUF = 16 * 2 * 128;                   // the workgroup's 16 tiles x 2 k tiles of words
+    constexpr int STAGE = MATS * XBUF + TBUF;
+    constexpr int EPITCH = MATS == 2 ? 2 * 128 + 4 : 256 + 4;
+    constexpr int LDS_EPI = 32 * EPITCH * 4;
+    constexpr int LDS_BYTES = NS * STAGE > LDS_EPI ? NS * STAGE : LDS_EPI;
+    constexpr int XLOADS = MATS * XBUF / 1024 / 4;       // direct loads of rows a wave a step
+    constexpr int RB16 = BM / 16;                        // 16-row blocks a matrix
+    __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
+    __shared__ int rows_sh[BM];
+
+    const int ncg = a.N / NCOLS;
+    // XCD-aware order: the hardware deals consecutive workgroups to the 8 XCDs in turn; renumber so that each XCD gets
+    // a contiguous range of (item, column group) -- an item's column groups then share one L2 (its token rows) and an
+    // expert's passes follow each other there (its trellis words).
+    const int nblk = gridDim.x, per = (nblk + 7) >> 3;
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    const int full = nblk & 7 ? nblk & 7 : 8;            // XCDs holding `per` workgroups (the rest hold per - 1)
+    const int logical = (xcd < full ? xcd * per : full * per + (xcd - full) * (per - 1)) + slot;
+    const int item = logical / ncg, cg = logical % ncg;
+    if (item >= a.plan[0]) return;
+    const int it = a.items[item];
+    const int u = it >> 16, pass = it & 0xffff;
+    const int e = a.uids[u];
+    const int nrows = min(BM, a.ucnt[u] - pass * BM);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    {
+        const int* mrow = a.members + (size_t)u * a.maxm + pass * BM;
+        const int c0 = mrow[0];
+        const int p0 = (c0 >> 5) * a.slots + (c0 & 31);
+        const int code = tid < nrows ? mrow[tid] : -1;
+        if (tid < BM) rows_sh[tid] = code >= 0 ? (code >> 5) * a.slots + (code & 31) : p0;   // padding: member 0
+    }
+    __syncthreads();
+
+    const int KT = a.Kin >> 4, NT = a.N >> 4, S = KT / 2;
+    const int col0 = cg * NCOLS;
+    const int mat = MATS == 2 ? wave >> 1 : 0;
+    const int wtile0 = MATS == 2 ? (wave & 1) * 4 : wave * 4;   // the wave's first tile within its matrix's columns
+    const int stile0 = MATS == 2 ? mat * 8 + wtile0 : wtile0;    // ... within the staged tiles
+
+    // the lane's direct loads: rows (XLOADS of them, 16 rows a load) and one trellis chunk
+    const uint16_t* xsrc[XLOADS];
+#pragma unroll
+    for (int j = 0; j < XLOADS; ++j) {
+        const int t = wave * XLOADS + j;                  // 16-row block of the stage (MATS * 16 of them)
+        const int m = t / RB16, row = (t % RB16) * 16 + lane / 4, pos = lane & 3;
+        const int c = pos ^ ((row >> 1) & 3);              // the global chunk this LDS position holds
+        xsrc[j] = (m ? a.x1 : a.x0) + (size_t)rows_sh[row] * a.Kin + (c >> 1) * 16 + (c & 1) * 8;
+    }
+    const uint32_t* tsrc;
+    {
+        const int blk = wave * 8 + lane / 8, ch = lane & 7;   // (tile, k tile) block of 128 B, 16-byte chunk
+        const int tile = blk >> 1, kt = blk & 1;
+        const int tmat = MATS == 2 ? tile >> 3 : 0;
+        const int ntile = col0 / 16 + (MATS == 2 ? (tile & 7) : tile);
+        tsrc = (tmat ? a.t1 : a.t0) + (((size_t)e * KT + kt) * NT + ntile) * 32 + ch * 4;
+    }
+    auto issue = [&](int s) {
+        unsigned char* st = lds + (s % NS) * STAGE;
+#pragma unroll
+        for (int j = 0; j < XLOADS; ++j) load_lds16(xsrc[j] + (size_t)s * 32, st + (wave * XLOADS + j) * 1024);
+        load_lds16(tsrc + (size_t)s * 2 * NT * 32, st + MATS * XBUF + wave * 1024);
+    };
+
+    f4_t acc[4][RG];
+#pragma unroll
+    for (int t4 = 0; t4 < 4; ++t4)
+#pragma unroll
+        for (int b = 0; b < RG; ++b) acc[t4][b] = (f4_t){0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s)
+        if (s < S) issue(s);
+    // two workgroups a CU (two waves a SIMD): one wave's trellis decode (VALU) overlaps the other's MFMAs
+    const int q = lane >> 4, cq = 2 * (q >> 1) + (q & 1);
+    for (int s = 0; s < S; ++s) {
+        // stage s has landed once at most NS - 2 later stages' loads are outstanding
+        if (s + NS - 2 < S) wait_vmcnt<(NS - 2) * (XLOADS + 1)>();
+        else wait_vmcnt<0>();
+        lds_barrier();
+        if (s + NS - 1 < S) issue(s + NS - 1);
+        const unsigned char* st = lds + (s % NS) * STAGE;
+        const unsigned char* xb = st + mat * XBUF;
+        const uint32_t* tw = reinterpret_cast<const uint32_t*>(st + MATS * XBUF);
+        h8_t bfr[RG];
+#pragma unroll
+        for (int b = 0; b < RG; ++b) {
+            const int row = 16 * b + (lane & 15);
+            bfr[b] = *reinterpret_cast<const h8_t*>(xb + row * 64 + ((cq ^ ((row >> 1) & 3)) << 4));
+        }
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
+            const h8_t af = a_fragment4(tw + (stile0 + t4) * 64, lane);
+#pragma unroll
+            for (int b = 0; b < RG; ++b)
+                acc[t4][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bfr[b], acc[t4][b], 0, 0, 0);
+        }
+    }
+    __syncthreads();
+
+    // ---- epilogue: 32 rows at a time through LDS, one wave a row
+    float* ep = reinterpret_cast<float*>(lds);
+#pragma unroll
+    for (int c = 0; c < BM / 32; ++c) {
+        if (c * 32 >= nrows) break;
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int n = (wtile0 + t4) * 16 + 4 * (lane >> 4) + r;
+                    const int row = 16 * bb + (lane & 15);
+                    ep[row * EPITCH + (MATS == 2 ? mat * 128 : 0) + n] = acc[t4][2 * c + bb][r];
+                }
+        __syncthreads();
+        for (int rr = wave; rr < 32; rr += 4) {
+            const int row = c * 32 + rr;
+            if (row >= nrows) break;
+            const int p = rows_sh[row];
+            if constexpr (MATS == 2) {
+                float gv[2] = {ep[rr * EPITCH + 2 * lane], ep[rr * EPITCH + 2 * lane + 1]};
+                float uv[2] = {ep[rr * EPITCH + 128 + 2 * lane], ep[rr * EPITCH + 128 + 2 * lane + 1]};
+                fwht128_w64(gv, lane);
+                fwht128_w64(uv, lane);
+                const size_t o = (size_t)e * a.N + col0 + 2 * lane;
+                const uint32_t sg = *reinterpret_cast<const uint32_t*>(a.sv0 + o);
+                const uint32_t su = *reinterpret_cast<const uint32_t*>(a.sv1 + o);
+                const uint32_t sd = *reinterpret_cast<const uint32_t*>(a.sd + o);
+                const float svg[2] = {f16_to_f32((uint16_t)sg), f16_to_f32((uint16_t)(sg >> 16))};
+                const float svu[2] = {f16_to_f32((uint16_t)su), f16_to_f32((uint16_t)(su >> 16))};
+                const float sdd[2] = {f16_to_f32((uint16_t)sd), f16_to_f32((uint16_t)(sd >> 16))};
+                float v[2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const float gg = fminf(bf16r(gv[j] * HAD_SCALE * svg[j]), a.limit);
+                    const float uu = fminf(fmaxf(bf16r(uv[j] * HAD_SCALE * svu[j]), -a.limit), a.limit);
+                    const float act = bf16r(bf16r(gg / (1.f + expf(-gg))) * uu);
+                    v[j] = act * sdd[j];
+                }
+                fwht128_w64(v, lane);
+                store_pair_order(a.xd + (size_t)p * a.N + col0, v, lane);
+            } else {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    float v[2] = {ep[rr * EPITCH + h * 128 + 2 * lane], ep[rr * EPITCH + h * 128 + 2 * lane + 1]};
+                    fwht128_w64(v, lane);
+                    const size_t o = (size_t)e * a.N + col0 + h * 128 + 2 * lane;
+                    const uint32_t sv = *reinterpret_cast<const uint32_t*>(a.sv0 + o);
+                    float2 yv;
+                    yv.x = v[0] * HAD_SCALE * f16_to_f32((uint16_t)sv);
+                    yv.y = v[1] * HAD_SCALE * f16_to_f32((uint16_t)(sv >> 16));
+                    *reinterpret_cast<float2*>(a.y + (size_t)p * a.N + col0 + h * 128 + 2 * lane) = yv;
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace gfr
+
 struct gfr_fast_experts {
     gfr::PrefillDims d;
     uint16_t *xg, *xu, *xd;
     float* out;
+    int *ucnt, *items, *plan;
 };
 
 namespace gfr {
@@ -16,11 +394,14 @@ namespace gfr {
 hipError_t prefill_create(gfr_fast_experts** out, int hidden, int inter, int slots, int exl3_slots, int experts,
                           int max_rows) {
     gfr_fast_experts* fx = new gfr_fast_experts{{hidden, inter, slots, exl3_slots, experts, max_rows},
-                                                nullptr, nullptr, nullptr, nullptr};
+                                                nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
     const size_t P = (size_t)max_rows * slots;
+    const size_t max_items = P / PF_BM + PF_MAXU + 1;
     hipError_t e;
     if ((e = hipMalloc(&fx->xg, P * hidden * 2)) != hipSuccess || (e = hipMalloc(&fx->xu, P * hidden * 2)) != hipSuccess ||
-        (e = hipMalloc(&fx->xd, P * inter * 2)) != hipSuccess || (e = hipMalloc(&fx->out, P * hidden * 4)) != hipSuccess) {
+        (e = hipMalloc(&fx->xd, P * inter * 2)) != hipSuccess || (e = hipMalloc(&fx->out, P * hidden * 4)) != hipSuccess ||
+        (e = hipMalloc(&fx->ucnt, PF_MAXU * 4)) != hipSuccess || (e = hipMalloc(&fx->items, max_items * 4)) != hipSuccess ||
+        (e = hipMalloc(&fx->plan, 16)) != hipSuccess) {
         prefill_destroy(fx);
         return e;
     }
@@ -30,9 +411,39 @@ hipError_t prefill_create(gfr_fast_experts** out, int hidden, int inter, int slo
 
 PrefillDims prefill_dims(const gfr_fast_experts* fx) { return fx->d; }
 
-hipError_t prefill_run(gfr_fast_experts*, hipStream_t, const gfr_exl3_experts*, const uint16_t*, int, const int*,
-                       const int*, const int*, const int*, int, int, bool) {
-    return hipErrorNotSupported;
+hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_experts* w, const uint16_t* input,
+                       int input_stride, const int* picks, const int* ids, const int* count, const int* members,
+                       int rows, int maxm, bool shared_x) {
+    const PrefillDims& d = fx->d;
+    if (w->bits != 4) return hipErrorNotSupported;        // the MFMA path decodes K = 4 tiles
+    const int P = rows * d.slots;
+    const int maxu = P < w->experts ? P : w->experts;
+    if (maxu > PF_MAXU) return hipErrorInvalidValue;
+    hipError_t e;
+    // rotated rows of every EXL3 pair (one copy when the two input rotations are the same)
+    {
+        const int tasks = rows * (d.hidden / 128);
+        prefill_rot_kernel<<<(tasks + 3) / 4, 256, 0, s>>>(input, input_stride, picks, w->suh_g, w->suh_u, fx->xg,
+                                                           fx->xu, d.hidden, rows, d.slots, d.exl3_slots,
+                                                           shared_x ? 1 : 2);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    prefill_plan_kernel<<<1, 1024, 0, s>>>(ids, count, members, maxm, w->experts, maxu, fx->ucnt, fx->items, fx->plan);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    const int max_items = P / PF_BM + maxu;
+    PrefillArgs a{};
+    a.uids = ids; a.members = members; a.ucnt = fx->ucnt; a.items = fx->items; a.plan = fx->plan;
+    a.maxm = maxm; a.slots = d.slots; a.limit = 10.f;
+    // gate / up -> xd
+    a.x0 = fx->xg; a.x1 = shared_x ? fx->xg : fx->xu; a.t0 = w->gt; a.t1 = w->ut; a.Kin = d.hidden; a.N = d.inter;
+    a.sv0 = w->svh_g; a.sv1 = w->svh_u; a.sd = w->suh_d; a.xd = fx->xd;
+    prefill_gemm_kernel<2><<<max_items * (d.inter / 128), 256, 0, s>>>(a);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    // down -> output
+    a.x0 = fx->xd; a.x1 = fx->xd; a.t0 = w->dt; a.t1 = w->dt; a.Kin = d.inter; a.N = d.hidden;
+    a.sv0 = w->svh_d; a.sv1 = nullptr; a.sd = nullptr; a.xd = nullptr; a.y = fx->out;
+    prefill_gemm_kernel<1><<<max_items * (d.hidden / 256), 256, 0, s>>>(a);
+    return hipGetLastError();
 }
 
 float* prefill_output(const gfr_fast_experts* fx) { return fx->out; }
@@ -40,7 +451,8 @@ uint16_t* prefill_xd(const gfr_fast_experts* fx) { return fx->xd; }
 
 void prefill_destroy(gfr_fast_experts* fx) {
     if (!fx) return;
-    for (void* p : {(void*)fx->xg, (void*)fx->xu, (void*)fx->xd, (void*)fx->out})
+    for (void* p : {(void*)fx->xg, (void*)fx->xu, (void*)fx->xd, (void*)fx->out, (void*)fx->ucnt, (void*)fx->items,
+                    (void*)fx->plan})
         if (p) (void)hipFree(p);
     delete fx;
 }

@@ -1,0 +1,115 @@
+"""Prefill path (FastExperts) on the GPU: MFMA grouped GEMMs against the CPU oracle (one full-K chain a row,
+exl3_prefill.cu:14-23), the reference probe's row cases (fast_experts.rs:247-286), shared-X == separate-X,
+graph replays byte-identical, and the MoE layer at the 8K-token prefill shape."""
+import numpy as np
+import pytest
+import torch
+
+from refs import DecodedExperts, assert_close, np_u16
+
+pytestmark = pytest.mark.gpu
+
+D, N, BITS = 2048, 1536, 4
+
+
+def _probe_picks(rows, E, slots):
+    # fast_experts.rs:247-286: (r * 7 + slot) % 16 for the routed slots, the shared expert last
+    return np.array([[(E if s == slots - 1 else (r * 7 + s) % 16) for s in range(slots)] for r in range(rows)],
+                    np.int32)
+
+
+@pytest.fixture(scope="module")
+def weights():
+    import synth
+    return synth.experts(17, D, N, BITS, seed=77)
+
+
+@pytest.mark.parametrize("rows,maxm", [(1, 129), (63, 129), (64, 129), (65, 129), (129, 129)])
+def test_fast_experts_reference_cases(gfr, oracle, weights, rows, maxm):
+    import synth
+    slots = 5
+    w = weights
+    picks_np = _probe_picks(rows, 16, slots)
+    picks = torch.from_numpy(picks_np).cuda()
+    x = synth.activations(rows, D, 3 + rows)
+    g = gfr.Grouping(17, slots, maxm)
+    g.run(picks, rows)
+    fx = gfr.FastExperts(D, N, slots, slots, 17, maxm)
+    fx.run(w, x, picks, g.ids, g.count, g.members, rows, maxm, shared_x=False)
+    torch.cuda.synchronize()
+    y = fx.output[:rows * slots].cpu().numpy()
+    assert np.all(np.isfinite(y))
+    dec = DecodedExperts(oracle, w)
+    xb = np_u16(x)
+    check = [(r, s) for r in range(rows) for s in range(slots)]
+    if len(check) > 24:
+        rng = np.random.default_rng(rows)
+        check = [check[i] for i in rng.choice(len(check), 24, replace=False)] + [check[-1]]
+    for r, s in check:
+        want, _ = dec.row(xb[r], int(picks_np[r, s]), sk_gu=1, sk_d=1, warps=1)
+        assert_close(y[r * slots + s], want, what=f"rows {rows} row {r} slot {s}")
+
+
+def test_shared_x_equals_separate_x(gfr, weights):
+    """With suh_g == suh_u, the shared-rotation launch is byte-identical to the separate one (fast_experts.rs:369-381)."""
+    import synth
+    import dataclasses
+    w = dataclasses.replace(weights, suh_u=weights.suh_g)
+    rows, slots, maxm = 70, 5, 70
+    picks = torch.from_numpy(_probe_picks(rows, 16, slots)).cuda()
+    x = synth.activations(rows, D, 9)
+    g = gfr.Grouping(17, slots, maxm)
+    g.run(picks, rows)
+    fx = gfr.FastExperts(D, N, slots, slots, 17, maxm)
+    fx.run(w, x, picks, g.ids, g.count, g.members, rows, maxm, shared_x=True)
+    a = fx.output[:rows * slots].clone()
+    fx.run(w, x, picks, g.ids, g.count, g.members, rows, maxm, shared_x=False)
+    assert torch.equal(a, fx.output[:rows * slots])
+
+
+def test_prefill_graph_replays(gfr, weights):
+    import synth
+    rows, slots, maxm = 200, 5, 256
+    picks = torch.from_numpy(_probe_picks(rows, 16, slots)).cuda()
+    x = synth.activations(rows, D, 10)
+    g = gfr.Grouping(17, slots, maxm)
+    fx = gfr.FastExperts(D, N, slots, slots, 17, maxm)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        g.run(picks, rows, stream=s)
+        fx.run(weights, x, picks, g.ids, g.count, g.members, rows, maxm, False, stream=s)
+        s.synchronize()
+        eager = fx.output[:rows * slots].clone()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            g.run(picks, rows, stream=s)
+            fx.run(weights, x, picks, g.ids, g.count, g.members, rows, maxm, False, stream=s)
+    for _ in range(3):
+        fx.output.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(fx.output[:rows * slots], eager)
+
+
+def test_moe_prefill_config4_tokens(gfr, oracle):
+    """Config 4 shape: 8192 tokens, 64 routed + 1 shared, top-4, uniform routing; sampled tokens vs the oracle."""
+    import synth
+    E, topk, rows = 64, 4, 8192
+    w = synth.experts(E + 1, D, N, BITS, seed=5)
+    x = synth.activations(rows, D, 6)
+    lg = synth.logits(rows, E, 7)
+    m = gfr.Moe(D, N, E, topk, rows)
+    m.run(w, x, lg, rows)
+    torch.cuda.synchronize()
+    out = m.output[:rows].cpu().numpy()
+    assert np.all(np.isfinite(out))
+    p, wt = oracle.route(lg.cpu().numpy(), topk, E)
+    assert np.array_equal(m.picks[:rows].cpu().numpy(), p)
+    dec = DecodedExperts(oracle, w)
+    xb = np_u16(x)
+    for r in (0, 4097, rows - 1):
+        ys = np.stack([dec.row(xb[r], int(e), sk_gu=1, sk_d=1, warps=1)[0] for e in p[r]])
+        want = oracle.combine(ys, wt[r:r + 1], 1, topk + 1)
+        assert_close(out[r], want[0], what=f"token {r}")
