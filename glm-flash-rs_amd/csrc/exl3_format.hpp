@@ -158,7 +158,9 @@ __device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
         return (uint32_t)__builtin_amdgcn_mov_dpp(x, 0xB1, 0xf, 0xf, false);   // quad_perm [1, 0, 3, 2]
     } else if constexpr (M == 2) {
         return (uint32_t)__builtin_amdgcn_mov_dpp(x, 0x4E, 0xf, 0xf, false);   // quad_perm [2, 3, 0, 1]
-    } else if constexpr (M == 4 || M == 8) {
+    } else if constexpr (M == 8) {
+        return (uint32_t)__builtin_amdgcn_mov_dpp(x, 0x128, 0xf, 0xf, false);  // row_ror:8 (inside a 16-lane row)
+    } else if constexpr (M == 4) {
         const int up = __builtin_amdgcn_mov_dpp(x, 0x100 + M, 0xf, 0xf, false);  // row_shl: lane + M
         const int dn = __builtin_amdgcn_mov_dpp(x, 0x110 + M, 0xf, 0xf, false);  // row_shr: lane - M
         return (uint32_t)((__lane_id() & M) ? dn : up);

@@ -13,21 +13,28 @@
 //     (16 n x 8 k) once k is taken in the pair order of exl3_format.hpp (pair_row); the token rows (B operand) are
 //     staged in LDS in that same order, so no weight ever goes through LDS and none is decoded twice in a workgroup.
 //   * workgroup = 4 waves, a tile of BM = 128 member rows of one expert x 128 (gate/up: both matrices) or 256 (down)
-//     output columns; each wave owns 64 columns x 128 rows (32 MFMA 16x16 accumulators), K in steps of 32 with the
-//     next step's trellis words and token rows loaded while the current step multiplies (LDS double buffer).
+//     output columns, two workgroups a CU; each wave owns 64 columns x 128 rows (32 MFMA 16x16 accumulators), K in
+//     steps of 32, multi-stage direct-to-LDS staging and a register pipeline (next step's decode during this step's
+//     MFMAs).
 //   * the 128 columns of a gate/up item, and each 128 of a down item, are one Hadamard block, so the epilogue
-//     (transforms, scales, SwiGLU) runs in the workgroup: accumulators -> LDS (32 rows at a time) -> one wave a row.
+//     (transforms, scales, SwiGLU) runs in the workgroup: accumulators -> LDS (32 rows at a time) -> registers with
+//     8 consecutive values a lane and four rows a wave, so that three of the seven butterfly stages stay in registers.
 //   * work items (distinct expert u, pass of BM members) come from a plan kernel (member counts by parallel search,
 //     scan); grid = items x column groups, no empty launches past the plan.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <type_traits>
 #include "exl3_format.hpp"
 #include "launch.hpp"
 #include "prefill.hpp"
 
 namespace gfr {
 
-constexpr int PF_BM = 128;          // member rows an item
+#ifndef PF_BM_ROWS
+#define PF_BM_ROWS 128
+#endif
+constexpr int PF_BM = PF_BM_ROWS;   // member rows an item (256: one workgroup a CU; 128: two)
+constexpr int PF_OCC = PF_BM == 256 ? 1 : 2;
 constexpr int PF_MAXU = 1024;       // distinct experts a window (grid / plan bound)
 
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
@@ -211,29 +218,86 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// ---- epilogue helpers: rows of 128 columns held 8 contiguous values a lane ----------------------------------------
+// Lane l holds elements 8 j .. 8 j + 7 of a row, j = (l & 3) | ((l >> 3) & 3) << 2; lane bits 2 and 5 pick one of
+// four rows, so a wave transforms four rows at once. Element bits 0-2 are in registers, bits 3, 4, 5, 6 are lane
+// bits 0, 1, 3, 4 (lane xor 1, 2, 8, 16: DPP quad permutes, row_ror:8 and a permlane16 swap).
+__device__ __forceinline__ int l8_j(int lane) { return (lane & 3) | ((lane >> 3) & 3) << 2; }
+__device__ __forceinline__ int l8_row(int lane) { return ((lane >> 2) & 1) | ((lane >> 5) & 1) << 1; }
+
+template <int M>
+__device__ __forceinline__ void fwht_l8_cross(float (&v)[8], int lane) {
+    const float sgn = (lane & M) ? -1.f : 1.f;            // lower: v + other, upper: other - v
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(sgn, v[i], lane_xor_f<M>(v[i]));
+}
+
+// 128-point unnormalised Walsh-Hadamard transform of four rows a wave (butterflies at strides 1, 2, ..., 64, each
+// (lower + upper, lower - upper) in fp32, as experts.rs:25-42).
+__device__ __forceinline__ void fwht128_l8(float (&v)[8], int lane) {
+#pragma unroll
+    for (int st = 1; st < 8; st <<= 1)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (!(i & st)) {
+                const float a = v[i], b = v[i + st];
+                v[i] = a + b;
+                v[i + st] = a - b;
+            }
+    fwht_l8_cross<1>(v, lane);
+    fwht_l8_cross<2>(v, lane);
+    fwht_l8_cross<8>(v, lane);
+    fwht_l8_cross<16>(v, lane);
+}
+
+// fp16(v / sqrt(128)) of a row held as above, stored in the pair order of pair_row (K != 2) into a 128-value block:
+// pair m of k tile kt = (x[m + 8] low, x[m] high), so the lane of the tile's first half (j even) pairs with its
+// neighbour (lane xor 1) that holds the second; the even lane stores pairs 0-3, the odd lane pairs 4-7.
+__device__ __forceinline__ void store_pairs_l8(uint16_t* block, const float (&v)[8], int lane) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        w[i] = (uint32_t)f16_of_product(v[2 * i], HAD_SCALE) | ((uint32_t)f16_of_product(v[2 * i + 1], HAD_SCALE) << 16);
+    const int j = l8_j(lane);
+    const bool odd = j & 1;
+    const uint32_t r0 = lane_xor<1>(odd ? w[0] : w[2]), r1 = lane_xor<1>(odd ? w[1] : w[3]);
+    const uint32_t L0 = odd ? w[2] : r0, L1 = odd ? w[3] : r1;   // the x[m + 8] (low halves)
+    const uint32_t H0 = odd ? r0 : w[0], H1 = odd ? r1 : w[1];   // the x[m] (high halves)
+    uint4 o;
+    o.x = __builtin_amdgcn_perm(H0, L0, 0x05040100u);
+    o.y = __builtin_amdgcn_perm(H0, L0, 0x07060302u);
+    o.z = __builtin_amdgcn_perm(H1, L1, 0x05040100u);
+    o.w = __builtin_amdgcn_perm(H1, L1, 0x07060302u);
+    *reinterpret_cast<uint4*>(block + (j >> 1) * 16 + (j & 1) * 8) = o;
+}
+
 // Item (u, pass) x column group cg. MATS = 2: gate + up, 128 columns of each (waves 0-1 gate, 2-3 up); MATS = 1:
-// down, 256 columns (wave w: columns 64 w ..). Rows: the pass's BM = 256 members of expert u (pairs). Each wave:
-// 64 columns (4 trellis tiles, A fragments decoded in registers) x 256 rows (16 B fragments from LDS), 64 MFMAs a
-// step of 32 k. Staging: NS LDS stages filled by direct-to-LDS loads NS - 1 steps ahead; a staged row keeps its four
-// 16-byte chunks XOR-swizzled by (row >> 1) & 3 to spread the B-fragment reads over the banks.
+// down, 256 columns (wave w: columns 64 w ..). Rows: the pass's BM members of expert u (pairs). Each wave owns 64
+// columns (4 trellis tiles) x BM rows: a step of 32 k is 4 A fragments decoded in registers against BM / 16 B
+// fragments, so every decoded fragment feeds BM / 16 MFMAs. Software pipeline: while step s multiplies, the wave
+// decodes step s + 1's A fragments into a second register set and keeps a ring of B fragments D reads ahead of the
+// MFMAs; direct-to-LDS loads run NS - 1 steps ahead of the step that reads them. With BM = 128 two workgroups share
+// a CU, so one wave's decode (VALU) overlaps the other's MFMAs on each SIMD. A staged row keeps its four 16-byte
+// chunks XOR-swizzled by (row >> 1) & 3 to spread the B-fragment reads over the banks.
 template <int MATS>
-__global__ void __launch_bounds__(256, 2) prefill_gemm_kernel(const PrefillArgs a) {
-    constexpr int BM = PF_BM, NCOLS = MATS == 2 ? 128 : 256, NS = 3, RG = BM / 16;
-    constexpr int XBUF = BM * 64;                        // one matrix's rows of a step (2 k tiles)
+__global__ void __launch_bounds__(256, PF_OCC) prefill_gemm_kernel(const PrefillArgs a) {
+    constexpr int BM = PF_BM, NCOLS = MATS == 2 ? 128 : 256, RB = BM / 16;
+    constexpr int NS = PF_OCC == 1 ? (MATS == 2 ? 4 : 6) : (MATS == 2 ? 3 : 4);
+    constexpr int XBUF = BM * 64;                        // one matrix's rows of a step (2 k tiles, pair order)
     constexpr int TBUF = 16 * 2 * 128;                   // the workgroup's 16 tiles x 2 k tiles of words
     constexpr int STAGE = MATS * XBUF + TBUF;
-    constexpr int EPITCH = MATS == 2 ? 2 * 128 + 4 : 256 + 4;
-    constexpr int LDS_EPI = 32 * EPITCH * 4;
+    constexpr int ER = BM / 4, EPITCH = 256 + 8;         // epilogue: BM / 4 rows of 256 fp32 columns at a time
+    constexpr int LDS_EPI = ER * EPITCH * 4;
     constexpr int LDS_BYTES = NS * STAGE > LDS_EPI ? NS * STAGE : LDS_EPI;
     constexpr int XLOADS = MATS * XBUF / 1024 / 4;       // direct loads of rows a wave a step
-    constexpr int RB16 = BM / 16;                        // 16-row blocks a matrix
+    constexpr int LOADS = XLOADS + 1;                    // ... plus one of trellis words
+    static_assert((BM == 256 || BM == 128) && NS <= 6, "tile shape");
     __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
     __shared__ int rows_sh[BM];
 
     const int ncg = a.N / NCOLS;
     // XCD-aware order: the hardware deals consecutive workgroups to the 8 XCDs in turn; renumber so that each XCD gets
-    // a contiguous range of (item, column group) -- an item's column groups then share one L2 (its token rows) and an
-    // expert's passes follow each other there (its trellis words).
+    // a contiguous range of (item, column group) -- an item's column groups then share one L2 (its token rows).
     const int nblk = gridDim.x, per = (nblk + 7) >> 3;
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
     const int full = nblk & 7 ? nblk & 7 : 8;            // XCDs holding `per` workgroups (the rest hold per - 1)
@@ -264,8 +328,8 @@ __global__ void __launch_bounds__(256, 2) prefill_gemm_kernel(const PrefillArgs 
     const uint16_t* xsrc[XLOADS];
 #pragma unroll
     for (int j = 0; j < XLOADS; ++j) {
-        const int t = wave * XLOADS + j;                  // 16-row block of the stage (MATS * 16 of them)
-        const int m = t / RB16, row = (t % RB16) * 16 + lane / 4, pos = lane & 3;
+        const int t = wave * XLOADS + j;                  // 16-row block of the stage (MATS * RB of them)
+        const int m = t / RB, row = (t % RB) * 16 + lane / 4, pos = lane & 3;
         const int c = pos ^ ((row >> 1) & 3);              // the global chunk this LDS position holds
         xsrc[j] = (m ? a.x1 : a.x0) + (size_t)rows_sh[row] * a.Kin + (c >> 1) * 16 + (c & 1) * 8;
     }
@@ -283,101 +347,159 @@ __global__ void __launch_bounds__(256, 2) prefill_gemm_kernel(const PrefillArgs 
         for (int j = 0; j < XLOADS; ++j) load_lds16(xsrc[j] + (size_t)s * 32, st + (wave * XLOADS + j) * 1024);
         load_lds16(tsrc + (size_t)s * 2 * NT * 32, st + MATS * XBUF + wave * 1024);
     };
+    // wait until at most n stages' loads of this wave are outstanding
+    auto wait_stages = [&](int n) {
+        if (n >= 5) wait_vmcnt<5 * LOADS>();
+        else if (n == 4) wait_vmcnt<4 * LOADS>();
+        else if (n == 3) wait_vmcnt<3 * LOADS>();
+        else if (n == 2) wait_vmcnt<2 * LOADS>();
+        else if (n == 1) wait_vmcnt<LOADS>();
+        else wait_vmcnt<0>();
+    };
+    const int q = lane >> 4;
+    // B fragment b of step s from LDS; the 4 decoded A fragments of step s
+    auto read_b = [&](int s, int b) {
+        const unsigned char* xb = lds + (s % NS) * STAGE + mat * XBUF;
+        const int row = 16 * b + (lane & 15);
+        return *reinterpret_cast<const h8_t*>(xb + row * 64 + ((q ^ ((row >> 1) & 3)) << 4));
+    };
+    auto decode_a = [&](int s, h8_t (&af)[4]) {
+        const uint32_t* tw = reinterpret_cast<const uint32_t*>(lds + (s % NS) * STAGE + MATS * XBUF);
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
+            af[t4] = a_fragment4(tw + (stile0 + t4) * 64, lane);
+        }
+    };
 
-    f4_t acc[4][RG];
+    f4_t acc[4][RB];
 #pragma unroll
     for (int t4 = 0; t4 < 4; ++t4)
 #pragma unroll
-        for (int b = 0; b < RG; ++b) acc[t4][b] = (f4_t){0.f, 0.f, 0.f, 0.f};
+        for (int b = 0; b < RB; ++b) acc[t4][b] = (f4_t){0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s)
         if (s < S) issue(s);
-    // two workgroups a CU (two waves a SIMD): one wave's trellis decode (VALU) overlaps the other's MFMAs
-    const int q = lane >> 4, cq = 2 * (q >> 1) + (q & 1);
-    for (int s = 0; s < S; ++s) {
-        // stage s has landed once at most NS - 2 later stages' loads are outstanding
-        if (s + NS - 2 < S) wait_vmcnt<(NS - 2) * (XLOADS + 1)>();
-        else wait_vmcnt<0>();
+    wait_stages(min(S, NS - 1) - 1);                      // stage 0 landed
+    lds_barrier();
+    constexpr int D = 4;                                  // B fragments read ahead (a ring of registers)
+    h8_t ring[D], a0[4], a1[4];
+#pragma unroll
+    for (int b = 0; b < D; ++b) ring[b] = read_b(0, b);
+    decode_a(0, a0);
+    // one step: multiply (ac, B fragments of the ring) while an is decoded for step s + 1 and the ring is refilled
+    // D fragments ahead (the last D of them from step s + 1's stage)
+    auto step = [&](int s, const h8_t (&ac)[4], h8_t (&an)[4]) {
+        // stage s + 1 landed (at most the stages after it in flight) and every wave is done with stage s - 1
+        wait_stages(min(S - 1, s + NS - 2) - (s + 1));
         lds_barrier();
-        if (s + NS - 1 < S) issue(s + NS - 1);
-        const unsigned char* st = lds + (s % NS) * STAGE;
-        const unsigned char* xb = st + mat * XBUF;
-        const uint32_t* tw = reinterpret_cast<const uint32_t*>(st + MATS * XBUF);
-        h8_t bfr[RG];
+        if (s + NS - 1 < S) issue(s + NS - 1);           // into stage s - 1's buffer, now free
+        const int sn = s + 1 < S ? s + 1 : s;             // the last step re-reads its own stage (unused)
+        decode_a(sn, an);
 #pragma unroll
-        for (int b = 0; b < RG; ++b) {
-            const int row = 16 * b + (lane & 15);
-            bfr[b] = *reinterpret_cast<const h8_t*>(xb + row * 64 + ((cq ^ ((row >> 1) & 3)) << 4));
+        for (int b = 0; b < RB; ++b) {
+            const h8_t bc = ring[b % D];
+            ring[b % D] = b + D < RB ? read_b(s, b + D) : read_b(sn, b + D - RB);
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4)
+                acc[t4][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac[t4], bc, acc[t4][b], 0, 0, 0);
         }
+        // keep the decode inside this step (the compiler would otherwise sink it next to its use)
 #pragma unroll
-        for (int t4 = 0; t4 < 4; ++t4) {
-            const h8_t af = a_fragment4(tw + (stile0 + t4) * 64, lane);
+        for (int t4 = 0; t4 < 4; ++t4) __asm__ volatile("" : "+v"(an[t4]));
+    };
+    for (int s = 0; s < S; ++s) {
+        step(s, a0, a1);
 #pragma unroll
-            for (int b = 0; b < RG; ++b)
-                acc[t4][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bfr[b], acc[t4][b], 0, 0, 0);
-        }
+        for (int t4 = 0; t4 < 4; ++t4) a0[t4] = a1[t4];
     }
     __syncthreads();
 
-    // ---- epilogue: 32 rows at a time through LDS, one wave a row
+    // ---- epilogue: ER rows at a time through LDS; each wave takes ER / 4 rows, four at a time (lane layout of
+    // fwht128_l8). The column scales are the same for every row: loaded once.
     float* ep = reinterpret_cast<float*>(lds);
+    const int j8 = l8_j(lane), r4 = l8_row(lane);
+    float sc[3][8];   // MATS = 2: svh gate, svh up, suh down of columns 8 j8 ..; MATS = 1: svh of both halves
+    {
+        const size_t o = (size_t)e * a.N + col0 + 8 * j8;
+        const uint16_t* src[3] = {a.sv0 + o, MATS == 2 ? a.sv1 + o : a.sv0 + o + 128, MATS == 2 ? a.sd + o : nullptr};
 #pragma unroll
-    for (int c = 0; c < BM / 32; ++c) {
-        if (c * 32 >= nrows) break;
+        for (int m = 0; m < (MATS == 2 ? 3 : 2); ++m) {
+            const uint4 v = *reinterpret_cast<const uint4*>(src[m]);
+            const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int bb = 0; bb < 2; ++bb)
+            for (int i = 0; i < 4; ++i) {
+                sc[m][2 * i] = f16_to_f32((uint16_t)vv[i]);
+                sc[m][2 * i + 1] = f16_to_f32((uint16_t)(vv[i] >> 16));
+            }
+        }
+    }
+    const int ncol = (MATS == 2 ? mat * 128 : 0) + wtile0 * 16 + 4 * (lane >> 4);
+    auto ld8 = [&](int row, int col, float (&v)[8]) {
+        const float4 x = *reinterpret_cast<const float4*>(ep + row * EPITCH + col);
+        const float4 y = *reinterpret_cast<const float4*>(ep + row * EPITCH + col + 4);
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w; v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+    };
+    // one chunk of ER rows; c is a compile-time constant so that acc stays in registers
+    auto chunk = [&](auto cc) {
+        constexpr int c = decltype(cc)::value;
+        if (c * ER >= nrows) return;
 #pragma unroll
-            for (int t4 = 0; t4 < 4; ++t4)
+        for (int bb = 0; bb < ER / 16; ++bb)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int n = (wtile0 + t4) * 16 + 4 * (lane >> 4) + r;
-                    const int row = 16 * bb + (lane & 15);
-                    ep[row * EPITCH + (MATS == 2 ? mat * 128 : 0) + n] = acc[t4][2 * c + bb][r];
-                }
+            for (int t4 = 0; t4 < 4; ++t4) {
+                const int row = 16 * bb + (lane & 15);
+                *reinterpret_cast<f4_t*>(ep + row * EPITCH + ncol + t4 * 16) = acc[t4][c * (ER / 16) + bb];
+            }
         __syncthreads();
-        for (int rr = wave; rr < 32; rr += 4) {
-            const int row = c * 32 + rr;
-            if (row >= nrows) break;
-            const int p = rows_sh[row];
+#pragma unroll
+        for (int g = 0; g < ER / 16; ++g) {
+            const int rr = wave * (ER / 4) + 4 * g + r4;        // this lane's row of the chunk
+            if (c * ER + wave * (ER / 4) + 4 * g >= nrows) break;
+            const int row = c * ER + rr;
             if constexpr (MATS == 2) {
-                float gv[2] = {ep[rr * EPITCH + 2 * lane], ep[rr * EPITCH + 2 * lane + 1]};
-                float uv[2] = {ep[rr * EPITCH + 128 + 2 * lane], ep[rr * EPITCH + 128 + 2 * lane + 1]};
-                fwht128_w64(gv, lane);
-                fwht128_w64(uv, lane);
-                const size_t o = (size_t)e * a.N + col0 + 2 * lane;
-                const uint32_t sg = *reinterpret_cast<const uint32_t*>(a.sv0 + o);
-                const uint32_t su = *reinterpret_cast<const uint32_t*>(a.sv1 + o);
-                const uint32_t sd = *reinterpret_cast<const uint32_t*>(a.sd + o);
-                const float svg[2] = {f16_to_f32((uint16_t)sg), f16_to_f32((uint16_t)(sg >> 16))};
-                const float svu[2] = {f16_to_f32((uint16_t)su), f16_to_f32((uint16_t)(su >> 16))};
-                const float sdd[2] = {f16_to_f32((uint16_t)sd), f16_to_f32((uint16_t)(sd >> 16))};
-                float v[2];
+                float gv[8], uv[8];
+                ld8(rr, 8 * j8, gv);
+                ld8(rr, 128 + 8 * j8, uv);
+                fwht128_l8(gv, lane);
+                fwht128_l8(uv, lane);
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const float gg = fminf(bf16r(gv[j] * HAD_SCALE * svg[j]), a.limit);
-                    const float uu = fminf(fmaxf(bf16r(uv[j] * HAD_SCALE * svu[j]), -a.limit), a.limit);
-                    const float act = bf16r(bf16r(gg / (1.f + expf(-gg))) * uu);
-                    v[j] = act * sdd[j];
+                for (int i = 0; i < 8; ++i) {
+                    const float gg = fminf(bf16r(gv[i] * HAD_SCALE * sc[0][i]), a.limit);
+                    const float uu = fminf(fmaxf(bf16r(uv[i] * HAD_SCALE * sc[1][i]), -a.limit), a.limit);
+                    // silu through the hardware exp2 / reciprocal (within an ulp or two of expf and the IEEE divide;
+                    // the bf16 rounding that follows absorbs the difference)
+                    const float ex = __builtin_amdgcn_exp2f(gg * -1.4426950408889634f);
+                    const float act = bf16r(bf16r(gg * __builtin_amdgcn_rcpf(1.f + ex)) * uu);
+                    gv[i] = act * sc[2][i];
                 }
-                fwht128_w64(v, lane);
-                store_pair_order(a.xd + (size_t)p * a.N + col0, v, lane);
+                fwht128_l8(gv, lane);
+                if (row < nrows) store_pairs_l8(a.xd + (size_t)rows_sh[row] * a.N + col0, gv, lane);
             } else {
+                float v[2][8];
+                ld8(rr, 8 * j8, v[0]);
+                ld8(rr, 128 + 8 * j8, v[1]);
+                fwht128_l8(v[0], lane);
+                fwht128_l8(v[1], lane);
+                if (row < nrows) {
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    float v[2] = {ep[rr * EPITCH + h * 128 + 2 * lane], ep[rr * EPITCH + h * 128 + 2 * lane + 1]};
-                    fwht128_w64(v, lane);
-                    const size_t o = (size_t)e * a.N + col0 + h * 128 + 2 * lane;
-                    const uint32_t sv = *reinterpret_cast<const uint32_t*>(a.sv0 + o);
-                    float2 yv;
-                    yv.x = v[0] * HAD_SCALE * f16_to_f32((uint16_t)sv);
-                    yv.y = v[1] * HAD_SCALE * f16_to_f32((uint16_t)(sv >> 16));
-                    *reinterpret_cast<float2*>(a.y + (size_t)p * a.N + col0 + h * 128 + 2 * lane) = yv;
+                    for (int h = 0; h < 2; ++h) {
+                        float4* dst = reinterpret_cast<float4*>(a.y + (size_t)rows_sh[row] * a.N + col0 + h * 128 + 8 * j8);
+                        dst[0] = make_float4(v[h][0] * HAD_SCALE * sc[h][0], v[h][1] * HAD_SCALE * sc[h][1],
+                                             v[h][2] * HAD_SCALE * sc[h][2], v[h][3] * HAD_SCALE * sc[h][3]);
+                        dst[1] = make_float4(v[h][4] * HAD_SCALE * sc[h][4], v[h][5] * HAD_SCALE * sc[h][5],
+                                             v[h][6] * HAD_SCALE * sc[h][6], v[h][7] * HAD_SCALE * sc[h][7]);
+                    }
                 }
             }
         }
         __syncthreads();
-    }
+    };
+    static_assert(BM / ER == 4, "four epilogue chunks");
+    chunk(std::integral_constant<int, 0>{});
+    chunk(std::integral_constant<int, 1>{});
+    chunk(std::integral_constant<int, 2>{});
+    chunk(std::integral_constant<int, 3>{});
 }
 
 }  // namespace gfr
@@ -436,7 +558,7 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
     a.maxm = maxm; a.slots = d.slots; a.limit = 10.f;
     // gate / up -> xd
     a.x0 = fx->xg; a.x1 = shared_x ? fx->xg : fx->xu; a.t0 = w->gt; a.t1 = w->ut; a.Kin = d.hidden; a.N = d.inter;
-    a.sv0 = w->svh_g; a.sv1 = w->svh_u; a.sd = w->suh_d; a.xd = fx->xd;
+    a.sv0 = w->svh_g; a.sv1 = w->svh_u; a.sd = w->suh_d; a.xd = fx->xd; a.y = fx->out;
     prefill_gemm_kernel<2><<<max_items * (d.inter / 128), 256, 0, s>>>(a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     // down -> output
