@@ -141,9 +141,32 @@ def gemv_roofline(args, copies, stream):
     algo = weight_bytes + act_bytes
     achieved = algo / per / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "gemv_kernel<4,4,4,8,2> (gate/up grouped trellis GEMV)", "bytes_per_launch": algo,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+            "kernel": "expert_gemv_kernel<4,4,4,2,0,1,false> (gate/up grouped trellis GEMV)", "bytes_per_launch": algo,
             "us_per_launch": round(per * 1e6, 3)}
+
+
+def measured_traffic():
+    """HBM bytes per launch of the roofline kernel from the committed rocprofv3 --pmc summary (FETCH_SIZE and
+    WRITE_SIZE per dispatch, each scaled by the same counter's reading on a plain copy of known size)."""
+    path = os.path.join(ROOT, "profiles", "gemv_c2_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    return t.get("hbm_bytes_per_launch")
+
+
+def calibrate_copy():
+    """A plain 256 MiB device copy, three times: the reference reading for the FETCH_SIZE / WRITE_SIZE counters
+    (run under rocprofv3 --pmc with --calibrate-copy)."""
+    import torch
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
 
 
 def prefill_bench(args, copies, stream):
@@ -215,12 +238,14 @@ def main():
     ap.add_argument("--prefill-rows", type=int, default=8192)
     ap.add_argument("--prefill-steps", type=int, default=20)
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true", help="first run a 256 MiB copy (counter reference)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
-    import torch
+    if args.calibrate_copy:
+        calibrate_copy()
     secs, copies, xs, logits, stream = decode_bench(args)
     log(f"decode: {args.steps} steps in {secs * 1e3:.2f} ms")
     roof = gemv_roofline(args, copies, stream)
