@@ -13,6 +13,7 @@
 #include <stdint.h>
 #include "exl3_format.hpp"
 #include "route.hpp"
+#include "launch.hpp"
 
 namespace gfr {
 
@@ -486,6 +487,296 @@ __global__ void __launch_bounds__(64) down_epilogue_kernel(const float* __restri
     *reinterpret_cast<float2*>(y + (size_t)p * D + n) = o;
 }
 
+
+// ---- one-token MoE layer in one persistent launch ----------------------------------------------------------------
+// The bs = 1 layer (Moe::run_prefetched, moe.rs:66-182, for the benchmark's router) as one launch instead of three:
+// route -> gate/up GEMV (rot_in fused) -> gate/up epilogue -> down GEMV -> down epilogue -> combine. Workgroup b takes
+// units b, b + grid, b + 2 grid, ... in order, every gate/up unit before any down unit; the grid is at most the
+// number of workgroups the GPU holds at once, so a workgroup that waits (a down unit waiting for gate/up partials)
+// only waits for gate/up units of resident workgroups that never wait themselves. The down units' trellis words
+// stream in while gate/up units still run; a bounded wait sets an error word instead of hanging.
+//   gate/up unit (slot s, 128-column block cb, K split, matrix): 4 waves, one 128-k block each, added in wave order
+//     -> Zgu partial row, then one count on the (s, cb) arrival counter.
+//   down unit (slot s, split pair q, 128-column block hb of the hidden size): waves 0-1 split 2q, waves 2-3 split
+//     2q + 1, 2 waves a split, one 128-k block cb each. Once the (s, cb) counters show all 2 SKgu gate/up partials,
+//     each wave runs the gate/up epilogue of its own block (exl3.cu:260-296) into its activations, as the
+//     three-launch path's down GEMV does; the two waves of a split are added in order -> Zd partial rows.
+//   finish: the last down unit of column block hb (counted over every slot and split) runs the down epilogue
+//     (exl3.cu:300-321) of every slot and the slot-ordered weighted combine -> out[hb].
+// Every sum has the order of the three-launch path (same wave, split and slot order), so the output is bit for bit
+// that path's. Data that other workgroups read goes through agent-scope (L2-coherent) stores and loads; a hand-off
+// is: stores, s_waitcnt (the stores are complete), then the counter's atomic add. The gate/up counters only grow
+// (ready = 2 SKgu arrivals past the launch's generation); the finish counters are cleared by their last arriver, and
+// the very last one advances the generation, so nothing needs clearing between launches (graph replays included).
+__device__ __forceinline__ uint32_t ld_agent(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t add_agent(uint32_t* p, uint32_t v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// this wave's agent-scope stores are complete (visible to every workgroup's agent-scope loads)
+__device__ __forceinline__ void stores_done() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+#ifdef GFR_TOKEN_TRACE
+#define TOKEN_MARK(k) do { if (threadIdx.x == 0) a.trace[blockIdx.x * 16 + (k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define TOKEN_MARK(k) do { } while (0)
+#endif
+constexpr int TOKEN_SPIN_LIMIT = 1 << 22;     // polls of a counter before the launch gives up (error word)
+constexpr int TOKEN_MAX_SLOTS = 16;
+constexpr int TOKEN_MAX_SPLITS = 16;           // K splits of either GEMV (hidden <= 8192, inter <= 4096)
+
+// this wave's 128 k x 16 columns of one trellis block row against its staged activations xs (pair order)
+template <int K>
+__device__ __forceinline__ void token_dot(const uint32_t (&wr)[8][K], const uint16_t* xs, int i, float& acc0,
+                                          float& acc1) {
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+        const uint32_t prev = prev_word(wr[kk][K - 1], i);
+        h2_t d[2][8];
+        decode_lane<K>(wr[kk], prev, d);
+        const uint4 xa = *reinterpret_cast<const uint4*>(xs + kk * 16);
+        const uint4 xb = *reinterpret_cast<const uint4*>(xs + kk * 16 + 8);
+        const uint32_t xp[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            acc0 = __builtin_amdgcn_fdot2(d[0][q], bits_h2(xp[q]), acc0, false);
+            acc1 = __builtin_amdgcn_fdot2(d[1][q], bits_h2(xp[q]), acc1, false);
+        }
+    }
+}
+
+__device__ __forceinline__ void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int K>
+__global__ void __launch_bounds__(256) moe_token_kernel(const TokenArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t xs[4][128];
+    __shared__ float red[4][128];
+    __shared__ float2 ys[TOKEN_MAX_SLOTS][64];
+    __shared__ uint32_t sh[2];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, t8 = lane >> 3, i = lane & 7;
+    const int S = a.slots, NCB = a.N >> 7, NHB = a.D >> 7, SKgu = a.D >> 9, SKd = a.N >> 8, QD = (SKd + 1) >> 1;
+    const uint32_t Tgu = (uint32_t)(S * NCB * SKgu * 2), T = Tgu + (uint32_t)(S * QD * NHB);
+    uint32_t* const genp = a.sync + 1;
+    uint32_t* const fcnt = a.sync + 2;
+    uint32_t* const err = a.sync + 3;
+    uint32_t* const gcnt = a.sync + 4;               // [S][NCB], grows by 2 SKgu a launch
+    uint32_t* const hcnt = gcnt + S * NCB;           // [NHB], cleared by its last arriver
+    TOKEN_MARK(0);
+
+    int pick;                                        // lane s < S: slot s's expert and weight
+    float weight;
+    route_token_regs(a.logits, a.routed, S - 1, a.routed, pick, weight);
+    int rank = 0;                                    // ascending order of the slots' experts
+    for (int j = 0; j < S; ++j) rank += __builtin_amdgcn_readlane(pick, j) < pick;
+    const uint32_t gen = ld_agent(genp);
+    const uint32_t gu_ready = (gen + 1) * (uint32_t)(2 * SKgu);
+    TOKEN_MARK(1);
+
+    for (uint32_t t = blockIdx.x; t < T; t += (uint32_t)a.grid) {
+        if (t == 0 && wave == 0 && lane < S) {       // the window's routing and grouping for the caller
+            a.pick_out[lane] = pick;
+            a.weight_out[lane] = weight;
+            a.ids_out[rank] = pick;
+            a.members_out[(size_t)rank * a.maxm] = lane;
+            for (int j = 1; j < a.maxm; ++j) a.members_out[(size_t)rank * a.maxm + j] = -1;
+            if (lane == 0) a.count_out[0] = S;
+        }
+        if (t < Tgu) {
+            // ---- gate/up unit
+            const int g = t / (2 * SKgu), r = t % (2 * SKgu);
+            const int s = g / NCB, cb = g % NCB, split = r >> 1, mat = r & 1;
+            const int e = __builtin_amdgcn_readlane(pick, s);
+            const int KT = a.D >> 4, NT = a.N >> 4, kblk = split * 4 + wave;
+            uint32_t wr[8][K];
+            {
+                const uint32_t* src = (mat ? a.ut : a.gt) + (((size_t)e * KT + kblk * 8) * NT + cb * 8 + t8) * (8 * K) + i * K;
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk) load_words<K>(src + (size_t)kk * NT * (8 * K), wr[kk]);
+            }
+            const uint32_t xv = *reinterpret_cast<const uint32_t*>(a.x + kblk * 128 + 2 * lane);
+            const uint32_t sv =
+                *reinterpret_cast<const uint32_t*>((mat ? a.suh_u : a.suh_g) + (size_t)e * a.D + kblk * 128 + 2 * lane);
+            {
+                float v[2] = {bf16_to_f32((uint16_t)xv) * f16_to_f32((uint16_t)sv),
+                              bf16_to_f32((uint16_t)(xv >> 16)) * f16_to_f32((uint16_t)(sv >> 16))};
+                fwht128_w64(v, lane);
+                store_block<K>(xs[wave], v, lane);
+                wave_sync_lds();
+            }
+            float acc0 = 0.f, acc1 = 0.f;
+            token_dot<K>(wr, xs[wave], i, acc0, acc1);
+            red[wave][16 * t8 + i] = acc0;
+            red[wave][16 * t8 + i + 8] = acc1;
+            __syncthreads();
+            if (tid < 128) {
+                const float sum = red[0][tid] + red[1][tid] + red[2][tid] + red[3][tid];
+                st_agent(a.zgu + ((size_t)(mat * SKgu + split) * S + s) * a.N + cb * 128 + tid, sum);
+            }
+            stores_done();
+            __syncthreads();
+            if (tid == 0) add_agent(gcnt + s * NCB + cb, 1);
+            TOKEN_MARK(2);
+        } else {
+            // ---- down unit
+            const uint32_t td = t - Tgu;
+            const int s = td / (QD * NHB), r = td % (QD * NHB), q = r / NHB, hb = r % NHB;
+            const int e = __builtin_amdgcn_readlane(pick, s);
+            const int sp = 2 * q + (wave >> 1), nsp = SKd - 2 * q < 2 ? SKd - 2 * q : 2;
+            const bool active = sp < SKd;
+            const int cb = 2 * sp + (wave & 1);          // this wave's 128-k block of the intermediate size
+            const int KT = a.N >> 4, NT = a.D >> 4;
+            float acc0 = 0.f, acc1 = 0.f;
+            uint32_t wr[8][K];
+            uint32_t sg = 0, su = 0, sd = 0;
+            if (active) {
+                const uint32_t* src = a.dt + (((size_t)e * KT + cb * 8) * NT + hb * 8 + t8) * (8 * K) + i * K;
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk) load_words<K>(src + (size_t)kk * NT * (8 * K), wr[kk]);
+                const size_t o = (size_t)e * a.N + cb * 128 + 2 * lane;
+                sg = *reinterpret_cast<const uint32_t*>(a.svh_g + o);
+                su = *reinterpret_cast<const uint32_t*>(a.svh_u + o);
+                sd = *reinterpret_cast<const uint32_t*>(a.suh_d + o);
+                // wait for the 2 SKgu gate/up partials of (s, cb), then the gate/up epilogue of the block
+                int spins = 0;
+                while (__builtin_amdgcn_readfirstlane(ld_agent(gcnt + s * NCB + cb)) != gu_ready) {
+                    if (++spins > TOKEN_SPIN_LIMIT) {
+                        if (lane == 0) __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(4);
+                }
+                TOKEN_MARK(5);
+                const int n = cb * 128 + 2 * lane;
+                float gv[2] = {0.f, 0.f}, uv[2] = {0.f, 0.f};
+                {
+                    float zz[TOKEN_MAX_SPLITS][4];      // every partial in flight at once, then added in order
+#pragma unroll
+                    for (int k = 0; k < TOKEN_MAX_SPLITS; ++k)
+                        if (k < SKgu) {
+                            const float* zg = a.zgu + ((size_t)k * S + s) * a.N + n;
+                            const float* zu = a.zgu + ((size_t)(SKgu + k) * S + s) * a.N + n;
+                            zz[k][0] = ld_agent(zg);
+                            zz[k][1] = ld_agent(zg + 1);
+                            zz[k][2] = ld_agent(zu);
+                            zz[k][3] = ld_agent(zu + 1);
+                        }
+#pragma unroll
+                    for (int k = 0; k < TOKEN_MAX_SPLITS; ++k)
+                        if (k < SKgu) {
+                            gv[0] += zz[k][0];
+                            gv[1] += zz[k][1];
+                            uv[0] += zz[k][2];
+                            uv[1] += zz[k][3];
+                        }
+                }
+                const float svg[2] = {f16_to_f32((uint16_t)sg), f16_to_f32((uint16_t)(sg >> 16))};
+                const float svu[2] = {f16_to_f32((uint16_t)su), f16_to_f32((uint16_t)(su >> 16))};
+                const float sdd[2] = {f16_to_f32((uint16_t)sd), f16_to_f32((uint16_t)(sd >> 16))};
+                fwht128_w64(gv, lane);
+                fwht128_w64(uv, lane);
+                float v[2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const float gg = fminf(bf16r(gv[j] * HAD_SCALE * svg[j]), a.limit);
+                    const float uu = fminf(fmaxf(bf16r(uv[j] * HAD_SCALE * svu[j]), -a.limit), a.limit);
+                    const float act = bf16r(bf16r(gg / (1.f + expf(-gg))) * uu);
+                    v[j] = act * sdd[j];
+                }
+                fwht128_w64(v, lane);
+                store_block<K>(xs[wave], v, lane);
+                if (hb == 0)                              // the down input, for the caller (engine xd)
+                    *reinterpret_cast<uint32_t*>(a.xd + (size_t)s * a.N + n) =
+                        (uint32_t)f16_of_product(v[0], HAD_SCALE) | ((uint32_t)f16_of_product(v[1], HAD_SCALE) << 16);
+                wave_sync_lds();
+                token_dot<K>(wr, xs[wave], i, acc0, acc1);
+            }
+            red[wave][16 * t8 + i] = acc0;
+            red[wave][16 * t8 + i + 8] = acc1;
+            __syncthreads();
+            TOKEN_MARK(6);
+            {
+                const int h = tid >> 7, col = tid & 127;     // the split pair's half h = split 2q + h
+                if (h < nsp) {
+                    const float sum = red[2 * h][col] + red[2 * h + 1][col];
+                    st_agent(a.zd + ((size_t)(2 * q + h) * S + s) * a.D + hb * 128 + col, sum);
+                }
+            }
+            stores_done();
+            __syncthreads();
+            if (tid == 0) {
+                const uint32_t total = (uint32_t)(S * SKd);
+                const bool last = add_agent(hcnt + hb, (uint32_t)nsp) + nsp == total;
+                if (last) st_agent(hcnt + hb, 0u);
+                sh[1] = last;
+            }
+            __syncthreads();
+            if (sh[1]) {
+                TOKEN_MARK(8);
+                // finish of hb: every slot's down epilogue (split partials in order, transform, svh_d), then the
+                // slots in order, weighted
+                const int n = hb * 128 + 2 * lane;
+                for (int s2 = wave; s2 < S; s2 += 4) {
+                    const int e2 = __builtin_amdgcn_readlane(pick, s2);
+                    float v[2] = {0.f, 0.f};
+                    float zz[TOKEN_MAX_SPLITS][2];
+#pragma unroll
+                    for (int k = 0; k < TOKEN_MAX_SPLITS; ++k)
+                        if (k < SKd) {
+                            const float* z = a.zd + ((size_t)k * S + s2) * a.D + n;
+                            zz[k][0] = ld_agent(z);
+                            zz[k][1] = ld_agent(z + 1);
+                        }
+#pragma unroll
+                    for (int k = 0; k < TOKEN_MAX_SPLITS; ++k)
+                        if (k < SKd) {
+                            v[0] += zz[k][0];
+                            v[1] += zz[k][1];
+                        }
+                    const uint32_t sv = *reinterpret_cast<const uint32_t*>(a.svh_d + (size_t)e2 * a.D + n);
+                    fwht128_w64(v, lane);
+                    const float2 yv = make_float2(v[0] * HAD_SCALE * f16_to_f32((uint16_t)sv),
+                                                  v[1] * HAD_SCALE * f16_to_f32((uint16_t)(sv >> 16)));
+                    ys[s2][lane] = yv;
+                    *reinterpret_cast<float2*>(a.y + (size_t)s2 * a.D + n) = yv;
+                }
+                __syncthreads();
+                if (wave == 0) {
+                    float o0 = 0.f, o1 = 0.f;
+                    for (int s2 = 0; s2 < S; ++s2) {
+                        const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, weight), s2));
+                        o0 += w * ys[s2][lane].x;
+                        o1 += w * ys[s2][lane].y;
+                    }
+                    *reinterpret_cast<float2*>(a.out + n) = make_float2(o0, o1);
+                    TOKEN_MARK(9);
+                    if (lane == 0 && add_agent(fcnt, 1) == (uint32_t)(NHB - 1)) {
+                        st_agent(fcnt, 0u);
+                        st_agent(genp, gen + 1);            // the layer is done: the next launch's generation
+                    }
+                }
+            }
+        }
+    }
+}
+
 }  // namespace gfr
 
 #include "launch.hpp"
@@ -612,6 +903,41 @@ hipError_t launch_gateup_epilogue(hipStream_t s, const float* Z, const int* pick
                                   int slots, int exl3_slots, float limit) {
     gateup_epilogue_kernel<<<dim3(P, N / 128), 64, 0, s>>>(Z, pick, svh_g, svh_u, suh_d, xd, P, N, SK, slots,
                                                            exl3_slots, limit);
+    return hipGetLastError();
+}
+
+int token_sync_words(int slots, int D, int N) { return 4 + slots * (N / 128) + D / 128; }
+
+int token_units(int slots, int D, int N) {
+    const int SKd = N / 256;
+    return slots * (N / 128) * (D / 512) * 2 + slots * ((SKd + 1) / 2) * (D / 128);
+}
+
+bool token_shape_ok(int D, int N) {
+    return D % 512 == 0 && N % 256 == 0 && D / 512 <= TOKEN_MAX_SPLITS && N / 256 <= TOKEN_MAX_SPLITS;
+}
+int token_max_slots() { return TOKEN_MAX_SLOTS; }
+
+int token_blocks_per_cu(int bits) {
+    int nb = 0;
+    hipError_t e = hipErrorInvalidValue;
+    switch (bits) {
+        case 2: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, moe_token_kernel<2>, 256, 0); break;
+        case 3: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, moe_token_kernel<3>, 256, 0); break;
+        case 4: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, moe_token_kernel<4>, 256, 0); break;
+        case 5: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, moe_token_kernel<5>, 256, 0); break;
+    }
+    return e == hipSuccess ? nb : 0;
+}
+
+hipError_t launch_moe_token(hipStream_t s, const TokenArgs& a, int bits) {
+    switch (bits) {
+        case 2: moe_token_kernel<2><<<a.grid, 256, 0, s>>>(a); break;
+        case 3: moe_token_kernel<3><<<a.grid, 256, 0, s>>>(a); break;
+        case 4: moe_token_kernel<4><<<a.grid, 256, 0, s>>>(a); break;
+        case 5: moe_token_kernel<5><<<a.grid, 256, 0, s>>>(a); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

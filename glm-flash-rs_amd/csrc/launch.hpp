@@ -58,6 +58,38 @@ hipError_t launch_gateup_epilogue(hipStream_t s, const float* Z, const int* pick
 hipError_t launch_down_epilogue(hipStream_t s, const float* Z, const int* pick, const uint16_t* svh_d, float* y,
                                 int P, int D, int SK, int slots, int exl3_slots);
 
+// One-token MoE layer in one persistent launch (moe_token_kernel): the arguments, the sync words it needs (zero at
+// creation, never cleared by the host), its work units, the shapes it takes (hidden % 512, inter % 256) and its
+// residency (its grid must fit on the GPU at once: a workgroup may wait for another's results).
+struct TokenArgs {
+    const uint16_t* x;        // the token, bf16 [D]
+    const float* logits;      // [routed]
+    int routed, slots, D, N, E;
+    float limit;
+    const uint32_t *gt, *ut, *dt;
+    const uint16_t *suh_g, *suh_u, *suh_d, *svh_g, *svh_u, *svh_d;
+    float* zgu;               // [2][SKgu][slots][N]
+    uint16_t* xd;             // [slots][N]
+    float* zd;                // [SKd][slots][D]
+    float* y;                 // [slots][D]
+    float* out;               // [D]
+    int* pick_out;            // picks / weights [slots]; the window's ids / count / members (stride maxm)
+    float* weight_out;
+    int* ids_out;
+    int* count_out;
+    int* members_out;
+    int maxm;
+    uint32_t* sync;           // token_sync_words(slots, D, N) words, zero at creation
+    int grid;                 // at most the workgroups the GPU holds at once (token_blocks_per_cu * CUs)
+    uint64_t* trace;          // GFR_TOKEN_TRACE builds only: per-workgroup timestamps [grid][16]
+};
+int token_sync_words(int slots, int D, int N);
+int token_units(int slots, int D, int N);
+bool token_shape_ok(int D, int N);
+int token_max_slots();
+int token_blocks_per_cu(int bits);   // resident 256-thread workgroups a CU (0: unknown width)
+hipError_t launch_moe_token(hipStream_t s, const TokenArgs& a, int bits);
+
 // router.hip
 hipError_t launch_route(hipStream_t s, const float* logits, int rows, int E, int topk, int shared_id, int* picks,
                         float* weights);

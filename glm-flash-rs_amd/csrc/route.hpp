@@ -11,31 +11,31 @@ namespace gfr {
 constexpr int ROUTE_MAX_E = 64 * 16;
 
 // One wave (64 lanes) routes one token into registers: lane s < topk holds the s-th pick and its weight, lane topk
-// the shared expert (weight 1). k rounds of a wave-wide max (DPP / permlane, no LDS), ties to the lower id.
-__device__ __forceinline__ void route_token_regs(const float* __restrict__ l, int E, int topk, int shared_id,
-                                                 int& pick, float& weight) {
-    constexpr int PER = ROUTE_MAX_E / 64;
+// the shared expert (weight 1). Lane l holds logits l, l + 64, ... (PER of them); k rounds of a wave-wide max (DPP /
+// permlane, no LDS) whose winner is the lowest id holding it (a ballot per register, lowest set lane).
+template <int PER>
+__device__ __forceinline__ void route_token_per(const float* __restrict__ l, int E, int topk, int shared_id,
+                                                int& pick, float& weight) {
     const int lane = threadIdx.x & 63;
-    const int per = (E + 63) >> 6;                     // values a lane actually holds
     float v[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
         const int e = j * 64 + lane;
-        v[j] = (j < per && e < E) ? l[e] : -__builtin_inff();
+        v[j] = e < E ? l[e] : -__builtin_inff();
     }
     float my_v = 0.f;                                  // lane s < topk: the s-th pick's logit and id
     int my_e = 0;
     for (int s = 0; s < topk; ++s) {
-        float lm = -__builtin_inff();
+        float lm = v[0];
 #pragma unroll
-        for (int j = 0; j < PER; ++j)
-            if (j < per) lm = fmaxf(lm, v[j]);
+        for (int j = 1; j < PER; ++j) lm = fmaxf(lm, v[j]);
         const float best = wave_max(lm);
-        int le = 0x7fffffff;                           // this lane's lowest id holding the best value
+        int be = 0;
 #pragma unroll
-        for (int j = PER - 1; j >= 0; --j)
-            if (j < per && v[j] == best && j * 64 + lane < E) le = j * 64 + lane;
-        const int be = wave_min(le);
+        for (int j = PER - 1; j >= 0; --j) {           // the lowest register (id block) holding it wins
+            const uint64_t b = __ballot(v[j] == best && j * 64 + lane < E);
+            if (b) be = j * 64 + __builtin_ctzll(b);
+        }
         if ((be & 63) == lane) {
 #pragma unroll
             for (int j = 0; j < PER; ++j)
@@ -52,6 +52,14 @@ __device__ __forceinline__ void route_token_regs(const float* __restrict__ l, in
     for (int s = 0; s < topk; ++s) sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), s));
     pick = lane < topk ? my_e : shared_id;
     weight = lane < topk ? ex / sum : 1.f;
+}
+
+__device__ __forceinline__ void route_token_regs(const float* __restrict__ l, int E, int topk, int shared_id,
+                                                 int& pick, float& weight) {
+    if (E <= 64) route_token_per<1>(l, E, topk, shared_id, pick, weight);
+    else if (E <= 128) route_token_per<2>(l, E, topk, shared_id, pick, weight);
+    else if (E <= 256) route_token_per<4>(l, E, topk, shared_id, pick, weight);
+    else route_token_per<ROUTE_MAX_E / 64>(l, E, topk, shared_id, pick, weight);
 }
 
 // One wave routes one token; pk / wt (LDS or global) receive topk + 1 entries.
