@@ -66,6 +66,18 @@ __host__ __device__ constexpr int pair_row(int K, int m, int half) {
                   : (2 * (m >> 1) + (m & 1) + (half ? 0 : 8));
 }
 
+// The lane's 32 values, each from its own funnel-shifted window, in the K != 2 pairing (pair_row with K != 2).
+template <int K>
+__device__ __forceinline__ void decode_lane_windows(const uint32_t (&w)[K], uint32_t prev, h2_t (&d)[2][8]) {
+#define GFR_PAIR(L, J)                                                                                       \
+    d[(J) >> 2][2 * (L) + ((J) & 1)] = decode_pair(__builtin_amdgcn_perm(                                     \
+        lane_window<K, 8 * (L) + (J)>(w, prev), lane_window<K, 8 * (L) + (J) + 2>(w, prev), 0x05040100u));
+#define GFR_WORDS(L) GFR_PAIR(L, 0) GFR_PAIR(L, 1) GFR_PAIR(L, 4) GFR_PAIR(L, 5)
+    GFR_WORDS(0) GFR_WORDS(1) GFR_WORDS(2) GFR_WORDS(3)
+#undef GFR_WORDS
+#undef GFR_PAIR
+}
+
 // Decode the lane's 32 values into d[c][m] (see pair_row).
 template <int K>
 __device__ __forceinline__ void decode_lane(const uint32_t (&w)[K], uint32_t prev, h2_t (&d)[2][8]) {
@@ -92,14 +104,15 @@ __device__ __forceinline__ void decode_lane(const uint32_t (&w)[K], uint32_t pre
                 d[j >> 2][4 * v + (j & 3)] = decode_pair(__builtin_amdgcn_alignbit(p, w[v], 14 - 2 * j));
         }
     } else {
-#define GFR_PAIR(L, J)                                                                                       \
-        d[(J) >> 2][2 * (L) + ((J) & 1)] = decode_pair(__builtin_amdgcn_perm(                                 \
-            lane_window<K, 8 * (L) + (J)>(w, prev), lane_window<K, 8 * (L) + (J) + 2>(w, prev), 0x05040100u));
-#define GFR_WORDS(L) GFR_PAIR(L, 0) GFR_PAIR(L, 1) GFR_PAIR(L, 4) GFR_PAIR(L, 5)
-        GFR_WORDS(0) GFR_WORDS(1) GFR_WORDS(2) GFR_WORDS(3)
-#undef GFR_WORDS
-#undef GFR_PAIR
+        decode_lane_windows<K>(w, prev, d);
     }
+}
+
+// decode_lane with the K != 2 pairing for every K (pairs (8l + j + 2, 8l + j)): the prefill path's k order.
+template <int K>
+__device__ __forceinline__ void decode_lane_std(const uint32_t (&w)[K], uint32_t prev, h2_t (&d)[2][8]) {
+    if constexpr (K == 2) decode_lane_windows<K>(w, prev, d);
+    else decode_lane<K>(w, prev, d);
 }
 
 // The 16 activations of one k tile, natural order in (a = halves 0..7, b = halves 8..15), rearranged into the 8

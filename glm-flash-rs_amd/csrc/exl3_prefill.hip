@@ -279,21 +279,24 @@ __device__ __forceinline__ void store_pairs_l8(uint16_t* block, const float (&v)
 // MFMAs; direct-to-LDS loads run NS - 1 steps ahead of the step that reads them. With BM = 128 two workgroups share
 // a CU, so one wave's decode (VALU) overlaps the other's MFMAs on each SIMD. A staged row keeps its four 16-byte
 // chunks XOR-swizzled by (row >> 1) & 3 to spread the B-fragment reads over the banks.
-template <int MATS>
+template <int MATS, int K>
 __global__ void __launch_bounds__(256, PF_OCC) prefill_gemm_kernel(const PrefillArgs a) {
     constexpr int BM = PF_BM, NCOLS = MATS == 2 ? 128 : 256, RB = BM / 16;
     constexpr int NS = PF_OCC == 1 ? (MATS == 2 ? 4 : 6) : (MATS == 2 ? 3 : 4);
     constexpr int XBUF = BM * 64;                        // one matrix's rows of a step (2 k tiles, pair order)
-    constexpr int TBUF = 16 * 2 * 128;                   // the workgroup's 16 tiles x 2 k tiles of words
+    constexpr int TBUF = 16 * 2 * 32 * K;                // the workgroup's 16 tiles x 2 k tiles of words
     constexpr int STAGE = MATS * XBUF + TBUF;
     constexpr int ER = BM / 4, EPITCH = 256 + 8;         // epilogue: BM / 4 rows of 256 fp32 columns at a time
     constexpr int LDS_EPI = ER * EPITCH * 4;
     constexpr int LDS_BYTES = NS * STAGE > LDS_EPI ? NS * STAGE : LDS_EPI;
     constexpr int XLOADS = MATS * XBUF / 1024 / 4;       // direct loads of rows a wave a step
-    constexpr int LOADS = XLOADS + 1;                    // ... plus one of trellis words
+    constexpr int TL = (K + 3) / 4;                      // direct loads of trellis words a wave a step
+    constexpr int LOADS = XLOADS + TL;
     static_assert((BM == 256 || BM == 128) && NS <= 6, "tile shape");
     __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
     __shared__ int rows_sh[BM];
+    // K != 4: each lane decodes one trellis lane's 32 values of one tile and the fragments are exchanged here
+    __shared__ __attribute__((aligned(16))) uint4 afrag[K == 4 ? 1 : 4][4][64];
 
     const int ncg = a.N / NCOLS;
     // XCD-aware order: the hardware deals consecutive workgroups to the 8 XCDs in turn; renumber so that each XCD gets
@@ -333,19 +336,26 @@ __global__ void __launch_bounds__(256, PF_OCC) prefill_gemm_kernel(const Prefill
         const int c = pos ^ ((row >> 1) & 3);              // the global chunk this LDS position holds
         xsrc[j] = (m ? a.x1 : a.x0) + (size_t)rows_sh[row] * a.Kin + (c >> 1) * 16 + (c & 1) * 8;
     }
-    const uint32_t* tsrc;
-    {
-        const int blk = wave * 8 + lane / 8, ch = lane & 7;   // (tile, k tile) block of 128 B, 16-byte chunk
+    // trellis words: 32 blocks (tile, k tile) of 32 K bytes, K loads of 64 16-byte chunks; wave w issues loads
+    // w, w + 4, ... (the last one repeated where K is not a multiple of 4: the same bytes to the same place)
+    const uint32_t* tsrc[TL];
+    int tdst[TL];
+#pragma unroll
+    for (int j = 0; j < TL; ++j) {
+        const int li = wave + 4 * j < K ? wave + 4 * j : K - 1;
+        const int c = li * 64 + lane, blk = c / (2 * K), ch = c % (2 * K);
         const int tile = blk >> 1, kt = blk & 1;
         const int tmat = MATS == 2 ? tile >> 3 : 0;
         const int ntile = col0 / 16 + (MATS == 2 ? (tile & 7) : tile);
-        tsrc = (tmat ? a.t1 : a.t0) + (((size_t)e * KT + kt) * NT + ntile) * 32 + ch * 4;
+        tsrc[j] = (tmat ? a.t1 : a.t0) + (((size_t)e * KT + kt) * NT + ntile) * (8 * K) + ch * 4;
+        tdst[j] = MATS * XBUF + li * 1024;
     }
     auto issue = [&](int s) {
         unsigned char* st = lds + (s % NS) * STAGE;
 #pragma unroll
         for (int j = 0; j < XLOADS; ++j) load_lds16(xsrc[j] + (size_t)s * 32, st + (wave * XLOADS + j) * 1024);
-        load_lds16(tsrc + (size_t)s * 2 * NT * 32, st + MATS * XBUF + wave * 1024);
+#pragma unroll
+        for (int j = 0; j < TL; ++j) load_lds16(tsrc[j] + (size_t)s * 2 * NT * (8 * K), st + tdst[j]);
     };
     // wait until at most n stages' loads of this wave are outstanding
     auto wait_stages = [&](int n) {
@@ -365,9 +375,36 @@ __global__ void __launch_bounds__(256, PF_OCC) prefill_gemm_kernel(const Prefill
     };
     auto decode_a = [&](int s, h8_t (&af)[4]) {
         const uint32_t* tw = reinterpret_cast<const uint32_t*>(lds + (s % NS) * STAGE + MATS * XBUF);
+        if constexpr (K == 4) {
 #pragma unroll
-        for (int t4 = 0; t4 < 4; ++t4) {
-            af[t4] = a_fragment4(tw + (stile0 + t4) * 64, lane);
+            for (int t4 = 0; t4 < 4; ++t4) af[t4] = a_fragment4(tw + (stile0 + t4) * 64, lane);
+        } else {
+            // lane (t4, kt, i) decodes trellis lane i of k tile kt of tile t4 (32 values: columns i and i + 8 of
+            // 16 rows), then hands each of its four 8-value pieces (column half, word pair g) to the MFMA lane
+            // that owns it: column i + 8 half, k chunk 2 kt + g
+            const int t4 = lane >> 4, kt = (lane >> 3) & 1, i = lane & 7;
+            const uint32_t* tl = tw + (stile0 + t4) * (16 * K) + kt * (8 * K);
+            uint32_t w[K];
+#pragma unroll
+            for (int k = 0; k < K; ++k) w[k] = tl[i * K + k];
+            const uint32_t prev = tl[(i * K + 8 * K - 1) % (8 * K)];
+            h2_t d[2][8];
+            decode_lane_std<K>(w, prev, d);
+#pragma unroll
+            for (int half = 0; half < 2; ++half)
+#pragma unroll
+                for (int g = 0; g < 2; ++g)
+                    afrag[wave][t4][i + 8 * half + 16 * (2 * kt + g)] =
+                        make_uint4(h2_bits(d[half][4 * g]), h2_bits(d[half][4 * g + 1]), h2_bits(d[half][4 * g + 2]),
+                                   h2_bits(d[half][4 * g + 3]));
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int t = 0; t < 4; ++t) af[t] = __builtin_bit_cast(h8_t, afrag[wave][t][lane]);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");   // the reads complete before the next writes
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
     };
 
@@ -533,11 +570,23 @@ hipError_t prefill_create(gfr_fast_experts** out, int hidden, int inter, int slo
 
 PrefillDims prefill_dims(const gfr_fast_experts* fx) { return fx->d; }
 
+template <int MATS>
+static hipError_t launch_gemm(int bits, dim3 grid, hipStream_t s, const PrefillArgs& a) {
+    switch (bits) {
+        case 2: prefill_gemm_kernel<MATS, 2><<<grid, 256, 0, s>>>(a); break;
+        case 3: prefill_gemm_kernel<MATS, 3><<<grid, 256, 0, s>>>(a); break;
+        case 4: prefill_gemm_kernel<MATS, 4><<<grid, 256, 0, s>>>(a); break;
+        case 5: prefill_gemm_kernel<MATS, 5><<<grid, 256, 0, s>>>(a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_experts* w, const uint16_t* input,
                        int input_stride, const int* picks, const int* ids, const int* count, const int* members,
                        int rows, int maxm, bool shared_x) {
     const PrefillDims& d = fx->d;
-    if (w->bits != 4) return hipErrorNotSupported;        // the MFMA path decodes K = 4 tiles
+    if (w->bits < 2 || w->bits > 5) return hipErrorInvalidValue;
     const int P = rows * d.slots;
     const int maxu = P < w->experts ? P : w->experts;
     if (maxu > PF_MAXU) return hipErrorInvalidValue;
@@ -559,13 +608,11 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
     // gate / up -> xd
     a.x0 = fx->xg; a.x1 = shared_x ? fx->xg : fx->xu; a.t0 = w->gt; a.t1 = w->ut; a.Kin = d.hidden; a.N = d.inter;
     a.sv0 = w->svh_g; a.sv1 = w->svh_u; a.sd = w->suh_d; a.xd = fx->xd; a.y = fx->out;
-    prefill_gemm_kernel<2><<<max_items * (d.inter / 128), 256, 0, s>>>(a);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = launch_gemm<2>(w->bits, dim3(max_items * (d.inter / 128)), s, a)) != hipSuccess) return e;
     // down -> output
     a.x0 = fx->xd; a.x1 = fx->xd; a.t0 = w->dt; a.t1 = w->dt; a.Kin = d.inter; a.N = d.hidden;
     a.sv0 = w->svh_d; a.sv1 = nullptr; a.sd = nullptr; a.xd = nullptr; a.y = fx->out;
-    prefill_gemm_kernel<1><<<max_items * (d.hidden / 256), 256, 0, s>>>(a);
-    return hipGetLastError();
+    return launch_gemm<1>(w->bits, dim3(max_items * (d.hidden / 256)), s, a);
 }
 
 float* prefill_output(const gfr_fast_experts* fx) { return fx->out; }

@@ -113,3 +113,29 @@ def test_moe_prefill_config4_tokens(gfr, oracle):
         ys = np.stack([dec.row(xb[r], int(e), sk_gu=1, sk_d=1, warps=1)[0] for e in p[r]])
         want = oracle.combine(ys, wt[r:r + 1], 1, topk + 1)
         assert_close(out[r], want[0], what=f"token {r}")
+
+
+@pytest.mark.parametrize("bits", [2, 3, 5])
+def test_fast_experts_bit_widths(gfr, oracle, bits):
+    """K = 2, 3, 5 (config 5's mixed bit rates): the MFMA path's generic decode (one trellis lane a thread, pieces
+    handed to their MFMA lanes through LDS) against the oracle, at C5's hidden size."""
+    import synth
+    Dk, Nk, E, slots, rows, maxm = 5120, 1536, 9, 9, 40, 40
+    w = synth.experts(E, Dk, Nk, bits, seed=90 + bits)
+    picks_np = np.array([[(r * 3 + s) % (E - 1) if s < slots - 1 else E - 1 for s in range(slots)]
+                         for r in range(rows)], np.int32)
+    picks_np[:, :slots - 1] = np.sort(picks_np[:, :slots - 1], axis=1)
+    picks = torch.from_numpy(picks_np).cuda()
+    x = synth.activations(rows, Dk, 5 + bits)
+    g = gfr.Grouping(E, slots, maxm)
+    g.run(picks, rows)
+    fx = gfr.FastExperts(Dk, Nk, slots, slots, E, maxm)
+    fx.run(w, x, picks, g.ids, g.count, g.members, rows, maxm, shared_x=False)
+    torch.cuda.synchronize()
+    y = fx.output[:rows * slots].cpu().numpy()
+    assert np.all(np.isfinite(y))
+    dec = DecodedExperts(oracle, w)
+    xb = np_u16(x)
+    for r, s in [(0, 0), (7, 3), (19, slots - 1), (rows - 1, 5)]:
+        want, _ = dec.row(xb[r], int(picks_np[r, s]), sk_gu=1, sk_d=1, warps=1)
+        assert_close(y[r * slots + s], want, what=f"K={bits} row {r} slot {s}")
