@@ -162,8 +162,8 @@ __device__ __forceinline__ uint16_t f16_of_product(float a, float b) {
 }
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
 
-// The value of lane (lane ^ M) for M in {1, 2, 4, 8, 16, 32}, without LDS: DPP quad permutes and row shifts inside
-// 16-lane rows, the gfx950 permlane swaps across rows and halves.
+// The value of lane (lane ^ M) for M in {1, 2, 4, 8, 16, 32}, without LDS memory: DPP quad permutes, row shifts and
+// rotations inside 16-lane rows, a ds_swizzle across rows of a 32-lane half, the gfx950 permlane32 swap across halves.
 template <int M>
 __device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
     const int x = (int)v;
@@ -178,8 +178,8 @@ __device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
         const int dn = __builtin_amdgcn_mov_dpp(x, 0x110 + M, 0xf, 0xf, false);  // row_shr: lane - M
         return (uint32_t)((__lane_id() & M) ? dn : up);
     } else if constexpr (M == 16) {
-        const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
-        return (uint32_t)((__lane_id() & 16) ? r[0] : r[1]);
+        // ds_swizzle bit mode (and 0x1f, or 0, xor 0x10): the LDS crossbar, no memory and no VALU slot
+        return (uint32_t)__builtin_amdgcn_ds_swizzle(x, 0x1f | (0x10 << 10));
     } else {
         static_assert(M == 32, "lane_xor: M in {1, 2, 4, 8, 16, 32}");
         const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);

@@ -106,119 +106,7 @@ __global__ void __launch_bounds__(1024) prefill_plan_kernel(const int* __restric
     if (threadIdx.x == 0) plan[0] = base;
 }
 
-// ---- rotation ----------------------------------------------------------------------------------------------
-// The pair order of a k tile (pair_row, K = 4): 16 values x[8], x[0], x[9], x[1], ... x[15], x[7]. A wave that holds
-// elements 2 lane, 2 lane + 1 of a 128-block stores them packed: lane j < 4 of each 8-lane group (rows 2j, 2j + 1, the
-// high halves of pairs 2j, 2j + 1) takes the low halves from lane j + 4 (rows 2j + 8, 2j + 9) and writes 8 bytes.
-__device__ __forceinline__ void store_pair_order(uint16_t* block, const float (&v)[2], int lane) {
-    const uint16_t h0 = f16_of_product(v[0], HAD_SCALE), h1 = f16_of_product(v[1], HAD_SCALE);
-    const uint32_t mine = (uint32_t)h0 | ((uint32_t)h1 << 16);
-    const uint32_t other = lane_xor<4>(mine);
-    if ((lane & 4) == 0) {
-        const int kt = lane >> 3, j = lane & 7;
-        const uint32_t d0 = (other & 0xffffu) | ((mine & 0xffffu) << 16);     // pair 2j: (x[2j + 8], x[2j])
-        const uint32_t d1 = (other >> 16) | (mine & 0xffff0000u);             // pair 2j + 1
-        *reinterpret_cast<uint2*>(block + kt * 16 + 4 * j) = make_uint2(d0, d1);
-    }
-}
-
-// rot_in for prefill chunks (exl3.cu:224-241, bit for bit): one wave a (token, 128-block), all its EXL3 slots and
-// both matrices; x read once, the rotated rows written in pair order (the MFMA B operand's k order).
-__global__ void __launch_bounds__(256) prefill_rot_kernel(const uint16_t* __restrict__ x, int x_stride,
-                                                          const int* __restrict__ pick,
-                                                          const uint16_t* __restrict__ suh0,
-                                                          const uint16_t* __restrict__ suh1, uint16_t* __restrict__ out0,
-                                                          uint16_t* __restrict__ out1, int K, int rows, int slots,
-                                                          int exl3_slots, int mats) {
-    const int lane = threadIdx.x & 63;
-    const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int KB = K / 128, row = task / KB, blk = task % KB;
-    if (row >= rows) return;
-    const int k = blk * 128 + 2 * lane;
-    const uint32_t xv = *reinterpret_cast<const uint32_t*>(x + (size_t)row * x_stride + k);
-    const float x0 = bf16_to_f32((uint16_t)xv), x1 = bf16_to_f32((uint16_t)(xv >> 16));
-    for (int s = 0; s < exl3_slots; ++s) {
-        const int p = row * slots + s, e = pick[p];
-        for (int m = 0; m < mats; ++m) {
-            const uint32_t sv = *reinterpret_cast<const uint32_t*>((m ? suh1 : suh0) + (size_t)e * K + k);
-            float v[2] = {x0 * f16_to_f32((uint16_t)sv), x1 * f16_to_f32((uint16_t)(sv >> 16))};
-            fwht128_w64(v, lane);
-            store_pair_order((m ? out1 : out0) + (size_t)p * K + blk * 128, v, lane);
-        }
-    }
-}
-
-// ---- GEMM --------------------------------------------------------------------------------------------------------
-struct PrefillArgs {
-    const uint16_t* x0;      // rows [P][Kin] fp16 in pair order, matrix 0 (gate, or the down input xd)
-    const uint16_t* x1;      // of matrix 1 (up); == x0 when the input rotations are shared
-    const uint32_t* t0;      // trellis [E][Kin/16][N/16][32]
-    const uint32_t* t1;
-    const int* uids;
-    const int* members;
-    const int* ucnt;
-    const int* items;
-    const int* plan;
-    int Kin, N, maxm, slots;
-    const uint16_t* sv0;     // gate/up: svh_g, svh_u, suh_d; down: svh_d
-    const uint16_t* sv1;
-    const uint16_t* sd;
-    uint16_t* xd;            // gate/up output [P][N] fp16 in pair order
-    float* y;                // down output [P][N]
-    float limit;
-};
-
-// The A fragment of one 16-column trellis tile over two k tiles (K = 4): lane l owns column c = l % 16 of the tile
-// (format lane i = c % 8, value half c / 8) for k tile q / 2 and word pair g = q % 2 (q = l / 16): words 4i + 2g and
-// 4i + 2g + 1 hold its 8 values, rows (2l + 8 + h, 2l + h) for l = 2g, 2g + 1 -- the pair order of pair_row, the order
-// the token rows are staged in. tw: the tile's words of the two k tiles in LDS, [2][32].
-__device__ __forceinline__ h8_t a_fragment4(const uint32_t* tw, int lane) {
-    const int c = lane & 15, i = c & 7, q = lane >> 4, kt = q >> 1, g = q & 1;
-    const uint32_t* w = tw + kt * 32;
-    const int w0i = 4 * i + 2 * g;
-    const uint32_t p0 = w[(w0i + 31) & 31];
-    const uint2 ww = *reinterpret_cast<const uint2*>(w + w0i);
-    const uint32_t w0 = ww.x, w1 = ww.y;
-    const uint32_t sel = (c >> 3) ? 0x02010100u : 0x04030302u;   // value half: (s6,s4)/(s7,s5) or (s2,s0)/(s3,s1)
-    uint32_t s[4];
-    {
-        const uint32_t a = __builtin_amdgcn_alignbit(p0, w0, 4), b = p0 >> 4;
-        s[0] = __builtin_amdgcn_perm(b, a, sel);
-        s[1] = __builtin_amdgcn_perm(p0, w0, sel);
-    }
-    {
-        const uint32_t a = __builtin_amdgcn_alignbit(w0, w1, 4), b = w0 >> 4;
-        s[2] = __builtin_amdgcn_perm(b, a, sel);
-        s[3] = __builtin_amdgcn_perm(w0, w1, sel);
-    }
-    h8_t f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const h2_t v = decode_pair(s[j]);
-        f[2 * j] = v[0];
-        f[2 * j + 1] = v[1];
-    }
-    return f;
-}
-
-// 16-byte direct-to-LDS load: lane i's 16 bytes land at lds_base + 16 i.
-__device__ __forceinline__ void load_lds16(const void* g, void* lds_base) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
-                                     (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
-}
-
-// Workgroup barrier for LDS-only hand-offs: this wave's LDS operations complete, then s_barrier. Unlike
-// __syncthreads() it does not wait for outstanding global loads (the staged direct-to-LDS loads of later steps).
-__device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-// s_waitcnt vmcnt(n), other counters unconstrained (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// ---- epilogue helpers: rows of 128 columns held 8 contiguous values a lane ----------------------------------------
+// ---- rows of 128 values, 8 contiguous values a lane (the rotation and the GEMM epilogues) -----------------------
 // Lane l holds elements 8 j .. 8 j + 7 of a row, j = (l & 3) | ((l >> 3) & 3) << 2; lane bits 2 and 5 pick one of
 // four rows, so a wave transforms four rows at once. Element bits 0-2 are in registers, bits 3, 4, 5, 6 are lane
 // bits 0, 1, 3, 4 (lane xor 1, 2, 8, 16: DPP quad permutes, row_ror:8 and a permlane16 swap).
@@ -271,6 +159,143 @@ __device__ __forceinline__ void store_pairs_l8(uint16_t* block, const float (&v)
     *reinterpret_cast<uint4*>(block + (j >> 1) * 16 + (j & 1) * 8) = o;
 }
 
+
+// rot_in for prefill chunks (exl3.cu:224-241, bit for bit): one wave a (token, 128-block), every (EXL3 slot, matrix)
+// row of it four at a time in the 8-values-a-lane layout of fwht128_l8 (the reference's butterfly order, so the
+// bits are rot_in's); x read once, the rotated rows written in pair order (the MFMA B operand's k order).
+__global__ void __launch_bounds__(256) prefill_rot_kernel(const uint16_t* __restrict__ x, int x_stride,
+                                                          const int* __restrict__ pick,
+                                                          const uint16_t* __restrict__ suh0,
+                                                          const uint16_t* __restrict__ suh1, uint16_t* __restrict__ out0,
+                                                          uint16_t* __restrict__ out1, int K, int rows, int slots,
+                                                          int exl3_slots, int mats) {
+    const int lane = threadIdx.x & 63;
+    const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int KB = K / 128, row = task / KB, blk = task % KB;
+    if (row >= rows) return;
+    const int j8 = l8_j(lane), r4 = l8_row(lane);
+    const int k = blk * 128 + 8 * j8;
+    float xf[8];
+    {
+        const uint4 xv = *reinterpret_cast<const uint4*>(x + (size_t)row * x_stride + k);
+        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xf[2 * i] = bf16_to_f32((uint16_t)xw[i]);
+            xf[2 * i + 1] = bf16_to_f32((uint16_t)(xw[i] >> 16));
+        }
+    }
+    // every round's expert and scales in flight before the first transform (rows = (slot, matrix), four a round)
+    constexpr int MAXR = 16;                             // rounds: exl3_slots * mats <= 64
+    const int nrow = exl3_slots * mats;
+    const int pk = lane < exl3_slots ? pick[row * slots + lane] : 0;
+    uint4 sv[MAXR];
+#pragma unroll
+    for (int rd = 0; rd < MAXR; ++rd) {
+        const int ri = rd * 4 + r4;
+        const int sl = ri < nrow ? (mats == 2 ? ri >> 1 : ri) : 0, m = ri < nrow ? (mats == 2 ? ri & 1 : 0) : 0;
+        const int e = __shfl(pk, sl, 64);
+        if (rd * 4 < nrow) sv[rd] = *reinterpret_cast<const uint4*>((m ? suh1 : suh0) + (size_t)e * K + k);
+    }
+#pragma unroll
+    for (int rd = 0; rd < MAXR; ++rd) {
+        if (rd * 4 >= nrow) break;
+        const int ri = rd * 4 + r4;
+        const bool valid = ri < nrow;
+        const int sl = valid ? (mats == 2 ? ri >> 1 : ri) : 0, m = valid ? (mats == 2 ? ri & 1 : 0) : 0;
+        const int p = row * slots + sl;
+        const uint32_t sw[4] = {sv[rd].x, sv[rd].y, sv[rd].z, sv[rd].w};
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = xf[2 * i] * f16_to_f32((uint16_t)sw[i]);
+            v[2 * i + 1] = xf[2 * i + 1] * f16_to_f32((uint16_t)(sw[i] >> 16));
+        }
+        fwht128_l8(v, lane);
+        if (valid) store_pairs_l8((m ? out1 : out0) + (size_t)p * K + blk * 128, v, lane);
+    }
+}
+
+// ---- GEMM --------------------------------------------------------------------------------------------------------
+struct PrefillArgs {
+    const uint16_t* x0;      // rows [P][Kin] fp16 in pair order, matrix 0 (gate, or the down input xd)
+    const uint16_t* x1;      // of matrix 1 (up); == x0 when the input rotations are shared
+    const uint32_t* t0;      // trellis [E][Kin/16][N/16][32]
+    const uint32_t* t1;
+    const int* uids;
+    const int* members;
+    const int* ucnt;
+    const int* items;
+    const int* plan;
+    int Kin, N, maxm, slots;
+    const uint16_t* sv0;     // gate/up: svh_g, svh_u, suh_d; down: svh_d
+    const uint16_t* sv1;
+    const uint16_t* sd;
+    uint16_t* xd;            // gate/up output [P][N] fp16 in pair order
+    float* y;                // down output [P][N]
+    float limit;
+    uint64_t* trace;         // GFR_PF_TRACE builds only: per-workgroup timestamps [grid][8]
+};
+
+// The A fragment of one 16-column trellis tile over two k tiles (K = 4): lane l owns column c = l % 16 of the tile
+// (format lane i = c % 8, value half c / 8) for k tile q / 2 and word pair g = q % 2 (q = l / 16): words 4i + 2g and
+// 4i + 2g + 1 hold its 8 values, rows (2l + 8 + h, 2l + h) for l = 2g, 2g + 1 -- the pair order of pair_row, the order
+// the token rows are staged in. tw: the tile's words of the two k tiles in LDS, [2][32].
+// The words of that fragment: the previous word and the lane's word pair of its k tile.
+__device__ __forceinline__ void frag4_words(const uint32_t* tw, int lane, uint32_t& p0, uint32_t& w0, uint32_t& w1) {
+    const int c = lane & 15, i = c & 7, q = lane >> 4, kt = q >> 1, g = q & 1;
+    const uint32_t* w = tw + kt * 32;
+    const int w0i = 4 * i + 2 * g;
+    p0 = w[(w0i + 31) & 31];
+    const uint2 ww = *reinterpret_cast<const uint2*>(w + w0i);
+    w0 = ww.x;
+    w1 = ww.y;
+}
+// Its four packed state pairs (each two 16-bit windows of one column, pair order).
+__device__ __forceinline__ void frag4_states(uint32_t p0, uint32_t w0, uint32_t w1, int lane, uint32_t (&s)[4]) {
+    const uint32_t sel = ((lane & 15) >> 3) ? 0x02010100u : 0x04030302u;   // value half: (s6,s4)/(s7,s5) or (s2,s0)/(s3,s1)
+    {
+        const uint32_t a = __builtin_amdgcn_alignbit(p0, w0, 4), b = p0 >> 4;
+        s[0] = __builtin_amdgcn_perm(b, a, sel);
+        s[1] = __builtin_amdgcn_perm(p0, w0, sel);
+    }
+    {
+        const uint32_t a = __builtin_amdgcn_alignbit(w0, w1, 4), b = w0 >> 4;
+        s[2] = __builtin_amdgcn_perm(b, a, sel);
+        s[3] = __builtin_amdgcn_perm(w0, w1, sel);
+    }
+}
+__device__ __forceinline__ h8_t a_fragment4(const uint32_t* tw, int lane) {
+    uint32_t p0, w0, w1, s[4];
+    frag4_words(tw, lane, p0, w0, w1);
+    frag4_states(p0, w0, w1, lane, s);
+    h8_t f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const h2_t v = decode_pair(s[j]);
+        f[2 * j] = v[0];
+        f[2 * j + 1] = v[1];
+    }
+    return f;
+}
+
+// 16-byte direct-to-LDS load: lane i's 16 bytes land at lds_base + 16 i.
+__device__ __forceinline__ void load_lds16(const void* g, void* lds_base) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                     (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+}
+
+// Workgroup barrier for LDS-only hand-offs: this wave's LDS operations complete, then s_barrier. Unlike
+// __syncthreads() it does not wait for outstanding global loads (the staged direct-to-LDS loads of later steps).
+__device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// s_waitcnt vmcnt(n), other counters unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // Item (u, pass) x column group cg. MATS = 2: gate + up, 128 columns of each (waves 0-1 gate, 2-3 up); MATS = 1:
 // down, 256 columns (wave w: columns 64 w ..). Rows: the pass's BM members of expert u (pairs). Each wave owns 64
 // columns (4 trellis tiles) x BM rows: a step of 32 k is 4 A fragments decoded in registers against BM / 16 B
@@ -296,7 +321,7 @@ __global__ void __launch_bounds__(256, PF_OCC) prefill_gemm_kernel(const Prefill
     __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
     __shared__ int rows_sh[BM];
     // K != 4: each lane decodes one trellis lane's 32 values of one tile and the fragments are exchanged here
-    __shared__ __attribute__((aligned(16))) uint4 afrag[K == 4 ? 1 : 4][4][64];
+    __shared__ __attribute__((aligned(16))) uint4 afrag[(K == 4 || PF_BM == 256) ? 1 : 4][4][64];
 
     const int ncg = a.N / NCOLS;
     // XCD-aware order: the hardware deals consecutive workgroups to the 8 XCDs in turn; renumber so that each XCD gets
@@ -426,20 +451,57 @@ __global__ void __launch_bounds__(256, PF_OCC) prefill_gemm_kernel(const Prefill
     decode_a(0, a0);
     // one step: multiply (ac, B fragments of the ring) while an is decoded for step s + 1 and the ring is refilled
     // D fragments ahead (the last D of them from step s + 1's stage)
+#ifdef GFR_PF_TRACE
+    uint64_t tw = 0;
+    const uint64_t tl0 = __builtin_amdgcn_s_memtime();
+#endif
     auto step = [&](int s, const h8_t (&ac)[4], h8_t (&an)[4]) {
         // stage s + 1 landed (at most the stages after it in flight) and every wave is done with stage s - 1
+#ifdef GFR_PF_TRACE
+        const uint64_t w0 = __builtin_amdgcn_s_memtime();
+#endif
         wait_stages(min(S - 1, s + NS - 2) - (s + 1));
         lds_barrier();
+#ifdef GFR_PF_TRACE
+        tw += __builtin_amdgcn_s_memtime() - w0;
+#endif
         if (s + NS - 1 < S) issue(s + NS - 1);           // into stage s - 1's buffer, now free
         const int sn = s + 1 < S ? s + 1 : s;             // the last step re-reads its own stage (unused)
-        decode_a(sn, an);
+        if constexpr (K == 4) {
+            // the next step's decode spread over this step's MFMA groups (sched_barrier keeps each group together,
+            // so the VALU of the decode issues while the matrix core works)
+            constexpr int PPB = 16 / RB;                  // decoded pairs a B fragment
+            const uint32_t* twn = reinterpret_cast<const uint32_t*>(lds + (sn % NS) * STAGE + MATS * XBUF);
+            uint32_t wp[4], w0[4], w1[4], st[4];
 #pragma unroll
-        for (int b = 0; b < RB; ++b) {
-            const h8_t bc = ring[b % D];
-            ring[b % D] = b + D < RB ? read_b(s, b + D) : read_b(sn, b + D - RB);
+            for (int t4 = 0; t4 < 4; ++t4) frag4_words(twn + (stile0 + t4) * 64, lane, wp[t4], w0[t4], w1[t4]);
 #pragma unroll
-            for (int t4 = 0; t4 < 4; ++t4)
-                acc[t4][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac[t4], bc, acc[t4][b], 0, 0, 0);
+            for (int b = 0; b < RB; ++b) {
+                const h8_t bc = ring[b % D];
+                ring[b % D] = b + D < RB ? read_b(s, b + D) : read_b(sn, b + D - RB);
+#pragma unroll
+                for (int t4 = 0; t4 < 4; ++t4)
+                    acc[t4][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac[t4], bc, acc[t4][b], 0, 0, 0);
+#pragma unroll
+                for (int pp = 0; pp < PPB; ++pp) {
+                    const int pr = b * PPB + pp, t = pr >> 2, j = pr & 3;
+                    if (j == 0) frag4_states(wp[t], w0[t], w1[t], lane, st);
+                    const h2_t v = decode_pair(st[j]);
+                    an[t][2 * j] = v[0];
+                    an[t][2 * j + 1] = v[1];
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+            decode_a(sn, an);
+#pragma unroll
+            for (int b = 0; b < RB; ++b) {
+                const h8_t bc = ring[b % D];
+                ring[b % D] = b + D < RB ? read_b(s, b + D) : read_b(sn, b + D - RB);
+#pragma unroll
+                for (int t4 = 0; t4 < 4; ++t4)
+                    acc[t4][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac[t4], bc, acc[t4][b], 0, 0, 0);
+            }
         }
         // keep the decode inside this step (the compiler would otherwise sink it next to its use)
 #pragma unroll
@@ -451,6 +513,9 @@ __global__ void __launch_bounds__(256, PF_OCC) prefill_gemm_kernel(const Prefill
         for (int t4 = 0; t4 < 4; ++t4) a0[t4] = a1[t4];
     }
     __syncthreads();
+#ifdef GFR_PF_TRACE
+    const uint64_t tl1 = __builtin_amdgcn_s_memtime();
+#endif
 
     // ---- epilogue: ER rows at a time through LDS; each wave takes ER / 4 rows, four at a time (lane layout of
     // fwht128_l8). The column scales are the same for every row: loaded once.
@@ -537,6 +602,13 @@ __global__ void __launch_bounds__(256, PF_OCC) prefill_gemm_kernel(const Prefill
     chunk(std::integral_constant<int, 1>{});
     chunk(std::integral_constant<int, 2>{});
     chunk(std::integral_constant<int, 3>{});
+#ifdef GFR_PF_TRACE
+    if (tid == 0) {
+        uint64_t* o = a.trace + (size_t)(MATS == 2 ? 0 : 16384) * 8 + (size_t)blockIdx.x * 8;
+        o[0] = tl0; o[1] = tl1; o[2] = __builtin_amdgcn_s_memtime(); o[3] = tw; o[4] = __builtin_amdgcn_s_memrealtime();
+        o[5] = MATS;
+    }
+#endif
 }
 
 }  // namespace gfr
@@ -546,6 +618,9 @@ struct gfr_fast_experts {
     uint16_t *xg, *xu, *xd;
     float* out;
     int *ucnt, *items, *plan;
+#ifdef GFR_PF_TRACE
+    uint64_t* trace;
+#endif
 };
 
 namespace gfr {
@@ -560,7 +635,11 @@ hipError_t prefill_create(gfr_fast_experts** out, int hidden, int inter, int slo
     if ((e = hipMalloc(&fx->xg, P * hidden * 2)) != hipSuccess || (e = hipMalloc(&fx->xu, P * hidden * 2)) != hipSuccess ||
         (e = hipMalloc(&fx->xd, P * inter * 2)) != hipSuccess || (e = hipMalloc(&fx->out, P * hidden * 4)) != hipSuccess ||
         (e = hipMalloc(&fx->ucnt, PF_MAXU * 4)) != hipSuccess || (e = hipMalloc(&fx->items, max_items * 4)) != hipSuccess ||
-        (e = hipMalloc(&fx->plan, 16)) != hipSuccess) {
+        (e = hipMalloc(&fx->plan, 16)) != hipSuccess
+#ifdef GFR_PF_TRACE
+        || (e = hipMalloc(&fx->trace, 32768 * 8 * 8)) != hipSuccess
+#endif
+    ) {
         prefill_destroy(fx);
         return e;
     }
@@ -603,6 +682,9 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const int max_items = P / PF_BM + maxu;
     PrefillArgs a{};
+#ifdef GFR_PF_TRACE
+    a.trace = fx->trace;
+#endif
     a.uids = ids; a.members = members; a.ucnt = fx->ucnt; a.items = fx->items; a.plan = fx->plan;
     a.maxm = maxm; a.slots = d.slots; a.limit = 10.f;
     // gate / up -> xd
@@ -616,6 +698,9 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
 }
 
 float* prefill_output(const gfr_fast_experts* fx) { return fx->out; }
+#ifdef GFR_PF_TRACE
+extern "C" uint64_t* gfr_fast_experts_trace(const gfr_fast_experts* fx) { return fx->trace; }
+#endif
 uint16_t* prefill_xd(const gfr_fast_experts* fx) { return fx->xd; }
 
 void prefill_destroy(gfr_fast_experts* fx) {
