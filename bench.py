@@ -213,16 +213,29 @@ def cpu_baseline(args, copies, xs, logits):
     vec = {n: np.ascontiguousarray(np_u16(getattr(w, n)[need])) for n in ("suh_g", "suh_u", "suh_d", "svh_g", "svh_u",
                                                                         "svh_d")}
     xb = np_u16(xs[:args.cpu_tokens])
-    total = 0.0
-    for t in range(args.cpu_tokens):
-        ex = [remap[int(e)] for e in picks[t]]
-        secs, _ = oracle.baseline_decode(xb[t], D, N, BITS, ex, sub["gt"], sub["ut"], sub["dt"], vec["suh_g"],
-                                         vec["suh_u"], vec["suh_d"], vec["svh_g"], vec["svh_u"], vec["svh_d"])
-        total += secs
-    return {"value": round(args.cpu_tokens / total, 4), "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": f"{args.cpu_tokens} tokens of config 2: per token the 5 experts' gate/up/down trellis decode "
-                      f"+ fixed-order fp32 matvec + epilogues (oracle/gfr_oracle.c, scalar, 1 thread)",
-            "seconds": round(total, 2)}
+
+    def token(t):
+        ex = [remap[int(e)] for e in picks[t % args.cpu_tokens]]
+        secs, _ = oracle.baseline_decode(xb[t % args.cpu_tokens], D, N, BITS, ex, sub["gt"], sub["ut"], sub["dt"],
+                                         vec["suh_g"], vec["suh_u"], vec["suh_d"], vec["svh_g"], vec["svh_u"],
+                                         vec["svh_d"])
+        return secs
+
+    total = sum(token(t) for t in range(args.cpu_tokens))
+    one = {"value": round(args.cpu_tokens / total, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+           "sample": f"{args.cpu_tokens} tokens of config 2: per token the 5 experts' gate/up/down trellis decode "
+                     f"+ fixed-order fp32 matvec + epilogues (oracle/gfr_oracle.c, scalar, 1 thread)",
+           "seconds": round(total, 2)}
+    # the same work on every host core the box gives this job: one token a thread (the C call drops the GIL)
+    from concurrent.futures import ThreadPoolExecutor
+    threads = max(1, min(args.cpu_threads, len(os.sched_getaffinity(0))))
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        list(ex.map(token, range(threads)))
+    wall = time.perf_counter() - t0
+    many = {"value": round(threads / wall, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{threads} tokens of config 2 at once, one a thread, same scalar C path", "seconds": round(wall, 2)}
+    return one, many
 
 
 def main():
@@ -234,6 +247,8 @@ def main():
     ap.add_argument("--routings", type=int, default=64)
     ap.add_argument("--kernel-launches", type=int, default=2048)
     ap.add_argument("--cpu-tokens", type=int, default=6)
+    ap.add_argument("--cpu-threads", type=int, default=16, help="threads of the all-cores CPU baseline (capped "
+                    "at the cores this process may use)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-rows", type=int, default=8192)
     ap.add_argument("--prefill-steps", type=int, default=20)
@@ -254,10 +269,11 @@ def main():
     if not args.no_prefill:
         prefill = prefill_bench(args, copies, stream)
         log(f"prefill: {prefill['ms_per_layer']} ms/layer, {prefill['achieved_tflops']} TFLOP/s")
-    cpu = None
+    cpu = cpu_all = None
     if not args.no_cpu:
-        cpu = cpu_baseline(args, copies, xs, logits)
-        log(f"cpu baseline: {cpu['value']} tok/s over {cpu['seconds']} s")
+        cpu, cpu_all = cpu_baseline(args, copies, xs, logits)
+        log(f"cpu baseline: {cpu['value']} tok/s over {cpu['seconds']} s; {cpu_all['cores']} threads "
+            f"{cpu_all['value']} tok/s")
     out = {
         "metric": METRIC, "value": round(args.steps / secs, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(secs * 1e3 / args.steps, 5), "higher_is_better": True,
@@ -265,7 +281,7 @@ def main():
         "config": {"workload": "config 2: one MoE layer, bs=1 decode, hidden 2048, 64 routed + 1 shared EXL3 "
                                "experts, inter 1536, top-4, K=4", "global_batch": 1, "seq_len": 1,
                    "parallelism": "single-gpu", "weight_copies": args.copies, "routings": args.routings},
-        "roofline": roof, "cpu_baseline": cpu, "prefill": prefill,
+        "roofline": roof, "cpu_baseline": cpu, "cpu_baseline_all_cores": cpu_all, "prefill": prefill,
     }
     print(json.dumps(out), flush=True)
 
