@@ -369,3 +369,23 @@ def test_single_launch_graph_replays(gfr):
             torch.cuda.synchronize()
             assert torch.equal(m.output, eager[0]), rep
     m.status()
+
+
+@pytest.mark.parametrize("bits", [2, 5])
+def test_moe_layer_config5_decode_vs_oracle(gfr, oracle, bits):
+    """Config 5's layer shape at bs = 1 (hidden 5120, 160 routed + 1 shared, top-8, inter 1536), K = 2 and 5, through
+    the Moe entry point against the oracle (routing exact, output within tolerance)."""
+    import synth
+    E, D, N, topk = 160, 5120, 1536, 8
+    w = synth.experts(E + 1, D, N, bits, seed=60 + bits)
+    x = synth.activations(1, D, 61)
+    lg = synth.zipf_logits(1, E, topk, 1.1, 62)
+    m = gfr.Moe(D, N, E, topk, 1)
+    m.run(w, x, lg, 1)
+    torch.cuda.synchronize()
+    p, wt = oracle.route(lg.cpu().numpy(), topk, E)
+    assert np.array_equal(m.picks.cpu().numpy(), p)
+    dec = DecodedExperts(oracle, w)
+    xb = np_u16(x)
+    ys = np.stack([dec.row(xb[0], int(e))[0] for e in p[0]])
+    assert_close(m.output.cpu().numpy(), oracle.combine(ys, wt, 1, topk + 1), what=f"config 5 K={bits}")

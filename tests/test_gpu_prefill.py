@@ -139,3 +139,26 @@ def test_fast_experts_bit_widths(gfr, oracle, bits):
     for r, s in [(0, 0), (7, 3), (19, slots - 1), (rows - 1, 5)]:
         want, _ = dec.row(xb[r], int(picks_np[r, s]), sk_gu=1, sk_d=1, warps=1)
         assert_close(y[r * slots + s], want, what=f"K={bits} row {r} slot {s}")
+
+
+def test_moe_prefill_config5_chunk(gfr, oracle):
+    """Config 5's prefill chunk: 16384 tokens, hidden 5120, 160 routed + 1 shared, top-8, Zipf(1.1) routing, K = 3;
+    routing exact, sampled tokens against the oracle."""
+    import synth
+    E, Dk, Nk, topk, rows, bits = 160, 5120, 1536, 8, 16384, 3
+    w = synth.experts(E + 1, Dk, Nk, bits, seed=71)
+    x = synth.activations(rows, Dk, 72)
+    lg = synth.zipf_logits(rows, E, topk, 1.1, 73)
+    m = gfr.Moe(Dk, Nk, E, topk, rows)
+    m.run(w, x, lg, rows)
+    torch.cuda.synchronize()
+    out = m.output[:rows].cpu().numpy()
+    assert np.all(np.isfinite(out))
+    p, wt = oracle.route(lg.cpu().numpy(), topk, E)
+    assert np.array_equal(m.picks[:rows].cpu().numpy(), p)
+    dec = DecodedExperts(oracle, w)
+    xb = np_u16(x)
+    for r in (0, rows - 1):
+        ys = np.stack([dec.row(xb[r], int(e), sk_gu=1, sk_d=1, warps=1)[0] for e in p[r]])
+        want = oracle.combine(ys, wt[r:r + 1], 1, topk + 1)
+        assert_close(out[r], want[0], what=f"config 5 token {r}")
