@@ -279,10 +279,14 @@ __device__ __forceinline__ h8_t a_fragment4(const uint32_t* tw, int lane) {
     return f;
 }
 
-// 16-byte direct-to-LDS load: lane i's 16 bytes land at lds_base + 16 i.
+// 16-byte direct-to-LDS load: lane i's 16 bytes land at lds_base + 16 i (lds_base uniform). Written as inline asm:
+// the compiler treats its builtin as an LDS store of unknown address and puts s_waitcnt vmcnt(0) before every later
+// LDS read, which drains the whole load pipeline each step; here the kernels wait for their stages themselves
+// (wait_vmcnt), and loads complete in order, so any wait the compiler adds for its own loads only waits longer.
 __device__ __forceinline__ void load_lds16(const void* g, void* lds_base) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
-                                     (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_base);
+    __asm__ volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(g), "{m0}"(m0) : "memory");
 }
 
 // Workgroup barrier for LDS-only hand-offs: this wave's LDS operations complete, then s_barrier. Unlike
