@@ -146,10 +146,9 @@ __device__ __forceinline__ uint32_t prev_word(uint32_t last, int i) {
 }
 
 __device__ __forceinline__ float bf16r(float x) {
-    // round to nearest even to bf16 (experts.rs:19-21 bit form; finite inputs)
-    uint32_t b = __builtin_bit_cast(uint32_t, x);
-    b = (b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u;
-    return __builtin_bit_cast(float, b);
+    // round to nearest even to bf16 (experts.rs:19-21 bit form; the same value for finite inputs): gfx950's
+    // v_cvt_pk_bf16_f32 and a shift back
+    return (float)(__bf16)x;
 }
 __device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }

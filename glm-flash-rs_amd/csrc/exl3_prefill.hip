@@ -12,10 +12,11 @@
 //     holds exactly 8 values of that column -- rows {2l + 8 + h, 2l + h} -- which is one A-fragment lane
 //     (16 n x 8 k) once k is taken in the pair order of exl3_format.hpp (pair_row); the token rows (B operand) are
 //     staged in LDS in that same order, so no weight ever goes through LDS and none is decoded twice in a workgroup.
-//   * workgroup = 4 waves, a tile of BM = 128 member rows of one expert x 128 (gate/up: both matrices) or 256 (down)
-//     output columns, two workgroups a CU; each wave owns 64 columns x 128 rows (32 MFMA 16x16 accumulators), K in
-//     steps of 32, multi-stage direct-to-LDS staging and a register pipeline (next step's decode during this step's
-//     MFMAs).
+//   * workgroup = 4 waves, a tile of BM member rows of one expert x 128 (gate/up: both matrices) or 256 (down)
+//     output columns, two workgroups a CU; each wave owns 64 columns x BM rows (4 BM / 16 MFMA 16x16 accumulators),
+//     K in steps of 32, multi-stage direct-to-LDS staging and a register pipeline (next step's decode during this
+//     step's MFMAs). BM = 160 for K = 4 (the trellis decode, VALU, is amortised over more rows; 256 VGPRs and
+//     two workgroups' stages still fit), 128 for the other widths (their fragment exchange needs more LDS).
 //   * the 128 columns of a gate/up item, and each 128 of a down item, are one Hadamard block, so the epilogue
 //     (transforms, scales, SwiGLU) runs in the workgroup: accumulators -> LDS (32 rows at a time) -> registers with
 //     8 consecutive values a lane and four rows a wave, so that three of the seven butterfly stages stay in registers.
@@ -34,7 +35,11 @@ namespace gfr {
 #define PF_BM_ROWS 128
 #endif
 constexpr int PF_BM = PF_BM_ROWS;   // member rows an item (256: one workgroup a CU; 128: two)
-constexpr int PF_OCC = PF_BM == 256 ? 1 : 2;
+#ifndef PF_BM4_ROWS
+#define PF_BM4_ROWS 160
+#endif
+constexpr int PF_BM4 = PF_BM4_ROWS;  // member rows an item for K = 4 (fits two workgroups a CU in LDS)
+static_assert(PF_BM4 >= PF_BM, "allocation bound");
 constexpr int PF_MAXU = 1024;       // distinct experts a window (grid / plan bound)
 
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
@@ -46,7 +51,7 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 __global__ void __launch_bounds__(1024) prefill_plan_kernel(const int* __restrict__ uids,
                                                             const int* __restrict__ ucount,
                                                             const int* __restrict__ members, int maxm, int E,
-                                                            int maxu, int* __restrict__ ucnt,
+                                                            int maxu, int bm, int* __restrict__ ucnt,
                                                             int* __restrict__ items, int* __restrict__ plan) {
     __shared__ int passes[PF_MAXU];
     __shared__ int scan_w[16];
@@ -75,7 +80,7 @@ __global__ void __launch_bounds__(1024) prefill_plan_kernel(const int* __restric
         }
         if (lane == 0) {
             ucnt[u] = n;
-            passes[u] = (n + PF_BM - 1) / PF_BM;
+            passes[u] = (n + bm - 1) / bm;
         }
     }
     __syncthreads();
@@ -308,24 +313,25 @@ __device__ __forceinline__ void wait_vmcnt() {
 // MFMAs; direct-to-LDS loads run NS - 1 steps ahead of the step that reads them. With BM = 128 two workgroups share
 // a CU, so one wave's decode (VALU) overlaps the other's MFMAs on each SIMD. A staged row keeps its four 16-byte
 // chunks XOR-swizzled by (row >> 1) & 3 to spread the B-fragment reads over the banks.
-template <int MATS, int K>
-__global__ void __launch_bounds__(256, PF_OCC) prefill_gemm_kernel(const PrefillArgs a) {
-    constexpr int BM = PF_BM, NCOLS = MATS == 2 ? 128 : 256, RB = BM / 16;
-    constexpr int NS = PF_OCC == 1 ? (MATS == 2 ? 4 : 6) : (MATS == 2 ? 3 : 4);
+template <int MATS, int K, int BM>
+__global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(const PrefillArgs a) {
+    constexpr int NCOLS = MATS == 2 ? 128 : 256, RB = BM / 16;
+    constexpr int OCC = BM == 256 ? 1 : 2;
+    constexpr int NS = OCC == 1 ? (MATS == 2 ? 4 : 6) : (MATS == 2 ? 3 : 4);
     constexpr int XBUF = BM * 64;                        // one matrix's rows of a step (2 k tiles, pair order)
     constexpr int TBUF = 16 * 2 * 32 * K;                // the workgroup's 16 tiles x 2 k tiles of words
     constexpr int STAGE = MATS * XBUF + TBUF;
-    constexpr int ER = BM / 4, EPITCH = 256 + 8;         // epilogue: BM / 4 rows of 256 fp32 columns at a time
+    constexpr int ER = BM % 64 ? 32 : BM / 4, EPITCH = 256 + 8;   // epilogue: ER rows of 256 fp32 columns at a time
     constexpr int LDS_EPI = ER * EPITCH * 4;
     constexpr int LDS_BYTES = NS * STAGE > LDS_EPI ? NS * STAGE : LDS_EPI;
-    constexpr int XLOADS = MATS * XBUF / 1024 / 4;       // direct loads of rows a wave a step
+    constexpr int XLOADS = (MATS * RB + 3) / 4;          // direct loads of rows a wave a step (the last repeated)
     constexpr int TL = (K + 3) / 4;                      // direct loads of trellis words a wave a step
     constexpr int LOADS = XLOADS + TL;
-    static_assert((BM == 256 || BM == 128) && NS <= 6, "tile shape");
+    static_assert((BM == 256 || BM == 160 || BM == 128) && NS <= 6, "tile shape");
     __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
     __shared__ int rows_sh[BM];
     // K != 4: each lane decodes one trellis lane's 32 values of one tile and the fragments are exchanged here
-    __shared__ __attribute__((aligned(16))) uint4 afrag[(K == 4 || PF_BM == 256) ? 1 : 4][4][64];
+    __shared__ __attribute__((aligned(16))) uint4 afrag[(K == 4 || BM == 256) ? 1 : 4][4][64];
 
     const int ncg = a.N / NCOLS;
     // XCD-aware order: the hardware deals consecutive workgroups to the 8 XCDs in turn; renumber so that each XCD gets
@@ -360,7 +366,7 @@ __global__ void __launch_bounds__(256, PF_OCC) prefill_gemm_kernel(const Prefill
     const uint16_t* xsrc[XLOADS];
 #pragma unroll
     for (int j = 0; j < XLOADS; ++j) {
-        const int t = wave * XLOADS + j;                  // 16-row block of the stage (MATS * RB of them)
+        const int t = min(wave * XLOADS + j, MATS * RB - 1);   // 16-row block of the stage (MATS * RB of them)
         const int m = t / RB, row = (t % RB) * 16 + lane / 4, pos = lane & 3;
         const int c = pos ^ ((row >> 1) & 3);              // the global chunk this LDS position holds
         xsrc[j] = (m ? a.x1 : a.x0) + (size_t)rows_sh[row] * a.Kin + (c >> 1) * 16 + (c & 1) * 8;
@@ -382,7 +388,8 @@ __global__ void __launch_bounds__(256, PF_OCC) prefill_gemm_kernel(const Prefill
     auto issue = [&](int s) {
         unsigned char* st = lds + (s % NS) * STAGE;
 #pragma unroll
-        for (int j = 0; j < XLOADS; ++j) load_lds16(xsrc[j] + (size_t)s * 32, st + (wave * XLOADS + j) * 1024);
+        for (int j = 0; j < XLOADS; ++j)
+            load_lds16(xsrc[j] + (size_t)s * 32, st + min(wave * XLOADS + j, MATS * RB - 1) * 1024);
 #pragma unroll
         for (int j = 0; j < TL; ++j) load_lds16(tsrc[j] + (size_t)s * 2 * NT * (8 * K), st + tdst[j]);
     };
@@ -448,7 +455,8 @@ __global__ void __launch_bounds__(256, PF_OCC) prefill_gemm_kernel(const Prefill
         if (s < S) issue(s);
     wait_stages(min(S, NS - 1) - 1);                      // stage 0 landed
     lds_barrier();
-    constexpr int D = 4;                                  // B fragments read ahead (a ring of registers)
+    constexpr int D = RB % 4 == 0 ? 4 : 2;                // B fragments read ahead (a ring of registers; RB % D == 0
+    static_assert(RB % D == 0, "ring");                   // so that step s + 1's first fragments land in ring[0 ..])
     h8_t ring[D], a0[4], a1[4];
 #pragma unroll
     for (int b = 0; b < D; ++b) ring[b] = read_b(0, b);
@@ -474,7 +482,6 @@ __global__ void __launch_bounds__(256, PF_OCC) prefill_gemm_kernel(const Prefill
         if constexpr (K == 4) {
             // the next step's decode spread over this step's MFMA groups (sched_barrier keeps each group together,
             // so the VALU of the decode issues while the matrix core works)
-            constexpr int PPB = 16 / RB;                  // decoded pairs a B fragment
             const uint32_t* twn = reinterpret_cast<const uint32_t*>(lds + (sn % NS) * STAGE + MATS * XBUF);
             uint32_t wp[4], w0[4], w1[4], st[4];
 #pragma unroll
@@ -487,8 +494,8 @@ __global__ void __launch_bounds__(256, PF_OCC) prefill_gemm_kernel(const Prefill
                 for (int t4 = 0; t4 < 4; ++t4)
                     acc[t4][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac[t4], bc, acc[t4][b], 0, 0, 0);
 #pragma unroll
-                for (int pp = 0; pp < PPB; ++pp) {
-                    const int pr = b * PPB + pp, t = pr >> 2, j = pr & 3;
+                for (int pr = b * 16 / RB; pr < (b + 1) * 16 / RB; ++pr) {   // the 16 decoded pairs spread evenly
+                    const int t = pr >> 2, j = pr & 3;
                     if (j == 0) frag4_states(wp[t], w0[t], w1[t], lane, st);
                     const h2_t v = decode_pair(st[j]);
                     an[t][2 * j] = v[0];
@@ -549,6 +556,7 @@ __global__ void __launch_bounds__(256, PF_OCC) prefill_gemm_kernel(const Prefill
     // one chunk of ER rows; c is a compile-time constant so that acc stays in registers
     auto chunk = [&](auto cc) {
         constexpr int c = decltype(cc)::value;
+        if constexpr (c * ER >= BM) return;
         if (c * ER >= nrows) return;
 #pragma unroll
         for (int bb = 0; bb < ER / 16; ++bb)
@@ -601,11 +609,12 @@ __global__ void __launch_bounds__(256, PF_OCC) prefill_gemm_kernel(const Prefill
         }
         __syncthreads();
     };
-    static_assert(BM / ER == 4, "four epilogue chunks");
+    static_assert(BM % ER == 0 && ER % 16 == 0 && BM / ER <= 5, "epilogue chunks");
     chunk(std::integral_constant<int, 0>{});
     chunk(std::integral_constant<int, 1>{});
     chunk(std::integral_constant<int, 2>{});
     chunk(std::integral_constant<int, 3>{});
+    chunk(std::integral_constant<int, 4>{});
 #ifdef GFR_PF_TRACE
     if (tid == 0) {
         uint64_t* o = a.trace + (size_t)(MATS == 2 ? 0 : 16384) * 8 + (size_t)blockIdx.x * 8;
@@ -656,10 +665,10 @@ PrefillDims prefill_dims(const gfr_fast_experts* fx) { return fx->d; }
 template <int MATS>
 static hipError_t launch_gemm(int bits, dim3 grid, hipStream_t s, const PrefillArgs& a) {
     switch (bits) {
-        case 2: prefill_gemm_kernel<MATS, 2><<<grid, 256, 0, s>>>(a); break;
-        case 3: prefill_gemm_kernel<MATS, 3><<<grid, 256, 0, s>>>(a); break;
-        case 4: prefill_gemm_kernel<MATS, 4><<<grid, 256, 0, s>>>(a); break;
-        case 5: prefill_gemm_kernel<MATS, 5><<<grid, 256, 0, s>>>(a); break;
+        case 2: prefill_gemm_kernel<MATS, 2, PF_BM><<<grid, 256, 0, s>>>(a); break;
+        case 3: prefill_gemm_kernel<MATS, 3, PF_BM><<<grid, 256, 0, s>>>(a); break;
+        case 4: prefill_gemm_kernel<MATS, 4, PF_BM4><<<grid, 256, 0, s>>>(a); break;
+        case 5: prefill_gemm_kernel<MATS, 5, PF_BM><<<grid, 256, 0, s>>>(a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -682,9 +691,11 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
                                                            shared_x ? 1 : 2);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    prefill_plan_kernel<<<1, 1024, 0, s>>>(ids, count, members, maxm, w->experts, maxu, fx->ucnt, fx->items, fx->plan);
+    const int bm = w->bits == 4 ? PF_BM4 : PF_BM;
+    prefill_plan_kernel<<<1, 1024, 0, s>>>(ids, count, members, maxm, w->experts, maxu, bm, fx->ucnt, fx->items,
+                                           fx->plan);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    const int max_items = P / PF_BM + maxu;
+    const int max_items = P / bm + maxu;
     PrefillArgs a{};
 #ifdef GFR_PF_TRACE
     a.trace = fx->trace;
