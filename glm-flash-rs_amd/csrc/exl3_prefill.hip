@@ -168,6 +168,7 @@ __device__ __forceinline__ void store_pairs_l8(uint16_t* block, const float (&v)
 // rot_in for prefill chunks (exl3.cu:224-241, bit for bit): one wave a (token, 128-block), every (EXL3 slot, matrix)
 // row of it four at a time in the 8-values-a-lane layout of fwht128_l8 (the reference's butterfly order, so the
 // bits are rot_in's); x read once, the rotated rows written in pair order (the MFMA B operand's k order).
+template <int MAXR>   // rounds of four (slot, matrix) rows: exl3_slots * mats <= 4 MAXR
 __global__ void __launch_bounds__(256) prefill_rot_kernel(const uint16_t* __restrict__ x, int x_stride,
                                                           const int* __restrict__ pick,
                                                           const uint16_t* __restrict__ suh0,
@@ -191,7 +192,6 @@ __global__ void __launch_bounds__(256) prefill_rot_kernel(const uint16_t* __rest
         }
     }
     // every round's expert and scales in flight before the first transform (rows = (slot, matrix), four a round)
-    constexpr int MAXR = 16;                             // rounds: exl3_slots * mats <= 64
     const int nrow = exl3_slots * mats;
     const int pk = lane < exl3_slots ? pick[row * slots + lane] : 0;
     uint4 sv[MAXR];
@@ -686,9 +686,19 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
     // rotated rows of every EXL3 pair (one copy when the two input rotations are the same)
     {
         const int tasks = rows * (d.hidden / 128);
-        prefill_rot_kernel<<<(tasks + 3) / 4, 256, 0, s>>>(input, input_stride, picks, w->suh_g, w->suh_u, fx->xg,
-                                                           fx->xu, d.hidden, rows, d.slots, d.exl3_slots,
-                                                           shared_x ? 1 : 2);
+        const int mats = shared_x ? 1 : 2;
+        if (d.exl3_slots * mats <= 16)   // fewer scale registers: more resident waves
+            prefill_rot_kernel<4><<<(tasks + 3) / 4, 256, 0, s>>>(input, input_stride, picks, w->suh_g, w->suh_u,
+                                                                  fx->xg, fx->xu, d.hidden, rows, d.slots,
+                                                                  d.exl3_slots, mats);
+        else if (d.exl3_slots * mats <= 32)
+            prefill_rot_kernel<8><<<(tasks + 3) / 4, 256, 0, s>>>(input, input_stride, picks, w->suh_g, w->suh_u,
+                                                                  fx->xg, fx->xu, d.hidden, rows, d.slots,
+                                                                  d.exl3_slots, mats);
+        else
+            prefill_rot_kernel<16><<<(tasks + 3) / 4, 256, 0, s>>>(input, input_stride, picks, w->suh_g, w->suh_u,
+                                                                   fx->xg, fx->xu, d.hidden, rows, d.slots,
+                                                                   d.exl3_slots, mats);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     const int bm = w->bits == 4 ? PF_BM4 : PF_BM;
