@@ -429,7 +429,7 @@ __global__ void __launch_bounds__(64) gateup_epilogue_kernel(const float* __rest
                                                               const uint16_t* __restrict__ svh_u,
                                                               const uint16_t* __restrict__ suh_d,
                                                               uint16_t* __restrict__ xd, int P, int N, int SK,
-                                                              int slots, int exl3_slots, float limit) {
+                                                              int slots, int exl3_slots, float limit, int pairs) {
     const int p = blockIdx.x, blk = blockIdx.y;
     const int row = p / slots, slot = p % slots;
     if (slot >= exl3_slots) return;
@@ -459,8 +459,17 @@ __global__ void __launch_bounds__(64) gateup_epilogue_kernel(const float* __rest
         v[j] = act * f16_to_f32(suh_d[(size_t)e * N + n + j]);
     }
     fwht128_w64(v, lane);
-    const uint32_t packed = (uint32_t)f16_of_product(v[0], HAD_SCALE) | ((uint32_t)f16_of_product(v[1], HAD_SCALE) << 16);
-    *reinterpret_cast<uint32_t*>(xd + (size_t)p * N + n) = packed;
+    const uint16_t h0 = f16_of_product(v[0], HAD_SCALE), h1 = f16_of_product(v[1], HAD_SCALE);
+    if (pairs) {
+        // the MFMA path's pair order: within each 16-value tile, x[m + 8] then x[m] for m = 0..7
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int k = n + j, m = k & 15;
+            xd[(size_t)p * N + (k & ~15) + (m < 8 ? 2 * m + 1 : 2 * (m - 8))] = j ? h1 : h0;
+        }
+    } else {
+        *reinterpret_cast<uint32_t*>(xd + (size_t)p * N + n) = (uint32_t)h0 | ((uint32_t)h1 << 16);
+    }
 }
 
 // down epilogue (exl3.cu:300-321): ordered split sum, rotation, svh_d -> y fp32. One wave a (pair, 128-block).
@@ -900,9 +909,9 @@ hipError_t launch_down_finish(hipStream_t s, const float* Zd, const int* pick, c
 
 hipError_t launch_gateup_epilogue(hipStream_t s, const float* Z, const int* pick, const uint16_t* svh_g,
                                   const uint16_t* svh_u, const uint16_t* suh_d, uint16_t* xd, int P, int N, int SK,
-                                  int slots, int exl3_slots, float limit) {
+                                  int slots, int exl3_slots, float limit, bool pair_order) {
     gateup_epilogue_kernel<<<dim3(P, N / 128), 64, 0, s>>>(Z, pick, svh_g, svh_u, suh_d, xd, P, N, SK, slots,
-                                                           exl3_slots, limit);
+                                                           exl3_slots, limit, pair_order ? 1 : 0);
     return hipGetLastError();
 }
 

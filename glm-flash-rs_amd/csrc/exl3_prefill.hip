@@ -239,6 +239,8 @@ struct PrefillArgs {
     uint16_t* xd;            // gate/up output [P][N] fp16 in pair order
     float* y;                // down output [P][N]
     float limit;
+    int sk, P;               // split-K launches: K splits, pairs
+    float* z;                // split-K output: partial sums [mats][sk][P][N] fp32 (no epilogue)
     uint64_t* trace;         // GFR_PF_TRACE builds only: per-workgroup timestamps [grid][8]
 };
 
@@ -313,21 +315,27 @@ __device__ __forceinline__ void wait_vmcnt() {
 // MFMAs; direct-to-LDS loads run NS - 1 steps ahead of the step that reads them. With BM = 128 two workgroups share
 // a CU, so one wave's decode (VALU) overlaps the other's MFMAs on each SIMD. A staged row keeps its four 16-byte
 // chunks XOR-swizzled by (row >> 1) & 3 to spread the B-fragment reads over the banks.
-template <int MATS, int K, int BM>
+// SPLIT: (item, column group, K split) programs over a.sk contiguous k ranges, each writing its raw partial sums to
+// a.z in the decode path's split layout (its epilogue kernels add the splits in order); for windows too small to
+// fill the GPU with full-K items.
+template <int MATS, int K, int BM, bool SPLIT = false>
 __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(const PrefillArgs a) {
     constexpr int NCOLS = MATS == 2 ? 128 : 256, RB = BM / 16;
     constexpr int OCC = BM == 256 ? 1 : 2;
-    constexpr int NS = OCC == 1 ? (MATS == 2 ? 4 : 6) : (MATS == 2 ? 3 : 4);
+#ifndef PFX_SPLIT_NS
+#define PFX_SPLIT_NS 6
+#endif
+    constexpr int NS = SPLIT ? PFX_SPLIT_NS : OCC == 1 ? (MATS == 2 ? 4 : 6) : (MATS == 2 ? 3 : 4);
     constexpr int XBUF = BM * 64;                        // one matrix's rows of a step (2 k tiles, pair order)
     constexpr int TBUF = 16 * 2 * 32 * K;                // the workgroup's 16 tiles x 2 k tiles of words
     constexpr int STAGE = MATS * XBUF + TBUF;
     constexpr int ER = BM % 64 ? 32 : BM / 4, EPITCH = 256 + 8;   // epilogue: ER rows of 256 fp32 columns at a time
-    constexpr int LDS_EPI = ER * EPITCH * 4;
+    constexpr int LDS_EPI = SPLIT ? 0 : ER * EPITCH * 4;
     constexpr int LDS_BYTES = NS * STAGE > LDS_EPI ? NS * STAGE : LDS_EPI;
     constexpr int XLOADS = (MATS * RB + 3) / 4;          // direct loads of rows a wave a step (the last repeated)
     constexpr int TL = (K + 3) / 4;                      // direct loads of trellis words a wave a step
     constexpr int LOADS = XLOADS + TL;
-    static_assert((BM == 256 || BM == 160 || BM == 128) && NS <= 6, "tile shape");
+    static_assert((BM == 256 || BM == 160 || BM == 128 || BM == 32) && NS <= 8, "tile shape");
     __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
     __shared__ int rows_sh[BM];
     // K != 4: each lane decodes one trellis lane's 32 values of one tile and the fragments are exchanged here
@@ -335,13 +343,16 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
 
     const int ncg = a.N / NCOLS;
     // XCD-aware order: the hardware deals consecutive workgroups to the 8 XCDs in turn; renumber so that each XCD gets
-    // a contiguous range of (item, column group) -- an item's column groups then share one L2 (its token rows).
-    const int nblk = gridDim.x, per = (nblk + 7) >> 3;
+    // a contiguous range of (item, column group[, split]) -- an item's column groups then share one L2 (its token
+    // rows). The grid is sized for the most items a window can have; the window's real programs (nact, known once
+    // the plan has run) are spread over all 8 XCDs, taken by the first-dispatched workgroups.
+    const int nsk = SPLIT ? a.sk : 1;
+    const int nact = a.plan[0] * ncg * nsk, per = (nact + 7) >> 3;
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-    const int full = nblk & 7 ? nblk & 7 : 8;            // XCDs holding `per` workgroups (the rest hold per - 1)
+    const int full = nact & 7 ? nact & 7 : 8;            // XCDs holding `per` programs (the rest hold per - 1)
+    if (slot >= (xcd < full ? per : per - 1)) return;
     const int logical = (xcd < full ? xcd * per : full * per + (xcd - full) * (per - 1)) + slot;
-    const int item = logical / ncg, cg = logical % ncg;
-    if (item >= a.plan[0]) return;
+    const int item = logical / (ncg * nsk), cg = logical / nsk % ncg, split = logical % nsk;
     const int it = a.items[item];
     const int u = it >> 16, pass = it & 0xffff;
     const int e = a.uids[u];
@@ -356,7 +367,7 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
     }
     __syncthreads();
 
-    const int KT = a.Kin >> 4, NT = a.N >> 4, S = KT / 2;
+    const int KT = a.Kin >> 4, NT = a.N >> 4, S = KT / 2 / nsk, s0 = split * S;   // this program's steps s0 ..
     const int col0 = cg * NCOLS;
     const int mat = MATS == 2 ? wave >> 1 : 0;
     const int wtile0 = MATS == 2 ? (wave & 1) * 4 : wave * 4;   // the wave's first tile within its matrix's columns
@@ -369,7 +380,7 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
         const int t = min(wave * XLOADS + j, MATS * RB - 1);   // 16-row block of the stage (MATS * RB of them)
         const int m = t / RB, row = (t % RB) * 16 + lane / 4, pos = lane & 3;
         const int c = pos ^ ((row >> 1) & 3);              // the global chunk this LDS position holds
-        xsrc[j] = (m ? a.x1 : a.x0) + (size_t)rows_sh[row] * a.Kin + (c >> 1) * 16 + (c & 1) * 8;
+        xsrc[j] = (m ? a.x1 : a.x0) + (size_t)rows_sh[row] * a.Kin + (size_t)s0 * 32 + (c >> 1) * 16 + (c & 1) * 8;
     }
     // trellis words: 32 blocks (tile, k tile) of 32 K bytes, K loads of 64 16-byte chunks; wave w issues loads
     // w, w + 4, ... (the last one repeated where K is not a multiple of 4: the same bytes to the same place)
@@ -382,7 +393,7 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
         const int tile = blk >> 1, kt = blk & 1;
         const int tmat = MATS == 2 ? tile >> 3 : 0;
         const int ntile = col0 / 16 + (MATS == 2 ? (tile & 7) : tile);
-        tsrc[j] = (tmat ? a.t1 : a.t0) + (((size_t)e * KT + kt) * NT + ntile) * (8 * K) + ch * 4;
+        tsrc[j] = (tmat ? a.t1 : a.t0) + (((size_t)e * KT + 2 * s0 + kt) * NT + ntile) * (8 * K) + ch * 4;
         tdst[j] = MATS * XBUF + li * 1024;
     }
     auto issue = [&](int s) {
@@ -394,8 +405,10 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
         for (int j = 0; j < TL; ++j) load_lds16(tsrc[j] + (size_t)s * 2 * NT * (8 * K), st + tdst[j]);
     };
     // wait until at most n stages' loads of this wave are outstanding
+    static_assert(NS - 2 <= 6 && 6 * LOADS < 64, "vmcnt range");
     auto wait_stages = [&](int n) {
-        if (n >= 5) wait_vmcnt<5 * LOADS>();
+        if (n >= 6) wait_vmcnt<6 * LOADS>();
+        else if (n == 5) wait_vmcnt<5 * LOADS>();
         else if (n == 4) wait_vmcnt<4 * LOADS>();
         else if (n == 3) wait_vmcnt<3 * LOADS>();
         else if (n == 2) wait_vmcnt<2 * LOADS>();
@@ -455,7 +468,7 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
         if (s < S) issue(s);
     wait_stages(min(S, NS - 1) - 1);                      // stage 0 landed
     lds_barrier();
-    constexpr int D = RB % 4 == 0 ? 4 : 2;                // B fragments read ahead (a ring of registers; RB % D == 0
+    constexpr int D = RB % 4 == 0 ? 4 : (RB % 2 == 0 ? 2 : 1);   // B fragments read ahead (a ring; RB % D == 0
     static_assert(RB % D == 0, "ring");                   // so that step s + 1's first fragments land in ring[0 ..])
     h8_t ring[D], a0[4], a1[4];
 #pragma unroll
@@ -522,6 +535,28 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
         step(s, a0, a1);
 #pragma unroll
         for (int t4 = 0; t4 < 4; ++t4) a0[t4] = a1[t4];
+    }
+    if constexpr (SPLIT) {
+        // raw partial sums, no epilogue: lane (row 16 b + lane % 16) holds columns 16 t4 + 4 (lane / 16) + 0..3 of
+        // the wave's tiles
+        const int cbase = col0 + wtile0 * 16 + 4 * (lane >> 4);
+#pragma unroll
+        for (int b = 0; b < RB; ++b) {
+            const int row = 16 * b + (lane & 15);
+            if (row < nrows) {
+                float* zr = a.z + ((size_t)(mat * nsk + split) * a.P + rows_sh[row]) * a.N + cbase;
+#pragma unroll
+                for (int t4 = 0; t4 < 4; ++t4) *reinterpret_cast<f4_t*>(zr + t4 * 16) = acc[t4][b];
+            }
+        }
+#ifdef GFR_PF_TRACE
+        if (tid == 0) {
+            uint64_t* o = a.trace + (size_t)(MATS == 2 ? 0 : 16384) * 8 + (size_t)blockIdx.x * 8;
+            o[0] = tl0; o[1] = __builtin_amdgcn_s_memtime(); o[2] = o[1]; o[3] = tw;
+            o[4] = __builtin_amdgcn_s_memrealtime(); o[5] = MATS;
+        }
+#endif
+        return;
     }
     __syncthreads();
 #ifdef GFR_PF_TRACE
@@ -631,6 +666,7 @@ struct gfr_fast_experts {
     uint16_t *xg, *xu, *xd;
     float* out;
     int *ucnt, *items, *plan;
+    float *zgu, *zd;          // split-K partials of windows of at most PF_SPLIT_PAIRS pairs (else null)
 #ifdef GFR_PF_TRACE
     uint64_t* trace;
 #endif
@@ -638,10 +674,22 @@ struct gfr_fast_experts {
 
 namespace gfr {
 
+// Windows of at most PF_SPLIT_PAIRS pairs (verify windows, short chunks) run split-K: 32-row items, each K range
+// of PF_SPLIT_K a program, partial sums added in order by the decode path's epilogue kernels. Their full-K items
+// would leave most CUs idle behind a few long programs.
+#ifndef PF_SPLIT_PAIRS_MAX
+#define PF_SPLIT_PAIRS_MAX 2048
+#endif
+constexpr int PF_SPLIT_PAIRS = PF_SPLIT_PAIRS_MAX;
+constexpr int PF_SPLIT_K = 512;
+constexpr int PF_SPLIT_BM = 32;
+static bool split_ok(int hidden, int inter) { return hidden % PF_SPLIT_K == 0 && inter % PF_SPLIT_K == 0; }
+
 hipError_t prefill_create(gfr_fast_experts** out, int hidden, int inter, int slots, int exl3_slots, int experts,
                           int max_rows) {
     gfr_fast_experts* fx = new gfr_fast_experts{{hidden, inter, slots, exl3_slots, experts, max_rows},
-                                                nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+                                                nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                                nullptr, nullptr};
     const size_t P = (size_t)max_rows * slots;
     const size_t max_items = P / PF_BM + PF_MAXU + 1;
     hipError_t e;
@@ -656,11 +704,31 @@ hipError_t prefill_create(gfr_fast_experts** out, int hidden, int inter, int slo
         prefill_destroy(fx);
         return e;
     }
+    if (split_ok(hidden, inter)) {
+        const size_t Ps = P < (size_t)PF_SPLIT_PAIRS ? P : (size_t)PF_SPLIT_PAIRS;
+        if ((e = hipMalloc(&fx->zgu, 2 * (size_t)(hidden / PF_SPLIT_K) * Ps * inter * 4)) != hipSuccess ||
+            (e = hipMalloc(&fx->zd, (size_t)(inter / PF_SPLIT_K) * Ps * hidden * 4)) != hipSuccess) {
+            prefill_destroy(fx);
+            return e;
+        }
+    }
     *out = fx;
     return hipSuccess;
 }
 
 PrefillDims prefill_dims(const gfr_fast_experts* fx) { return fx->d; }
+
+template <int MATS>
+static hipError_t launch_gemm_split(int bits, dim3 grid, hipStream_t s, const PrefillArgs& a) {
+    switch (bits) {
+        case 2: prefill_gemm_kernel<MATS, 2, PF_SPLIT_BM, true><<<grid, 256, 0, s>>>(a); break;
+        case 3: prefill_gemm_kernel<MATS, 3, PF_SPLIT_BM, true><<<grid, 256, 0, s>>>(a); break;
+        case 4: prefill_gemm_kernel<MATS, 4, PF_SPLIT_BM, true><<<grid, 256, 0, s>>>(a); break;
+        case 5: prefill_gemm_kernel<MATS, 5, PF_SPLIT_BM, true><<<grid, 256, 0, s>>>(a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
 
 template <int MATS>
 static hipError_t launch_gemm(int bits, dim3 grid, hipStream_t s, const PrefillArgs& a) {
@@ -701,7 +769,8 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
                                                                    d.exl3_slots, mats);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    const int bm = w->bits == 4 ? PF_BM4 : PF_BM;
+    const bool split = fx->zgu && P <= PF_SPLIT_PAIRS;
+    const int bm = split ? PF_SPLIT_BM : w->bits == 4 ? PF_BM4 : PF_BM;
     prefill_plan_kernel<<<1, 1024, 0, s>>>(ids, count, members, maxm, w->experts, maxu, bm, fx->ucnt, fx->items,
                                            fx->plan);
     if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -712,6 +781,20 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
 #endif
     a.uids = ids; a.members = members; a.ucnt = fx->ucnt; a.items = fx->items; a.plan = fx->plan;
     a.maxm = maxm; a.slots = d.slots; a.limit = 10.f;
+    if (split) {
+        // gate / up partials -> epilogue (xd in pair order) -> down partials -> epilogue -> output
+        const int skg = d.hidden / PF_SPLIT_K, skd = d.inter / PF_SPLIT_K;
+        a.sk = skg; a.P = P; a.z = fx->zgu;
+        a.x0 = fx->xg; a.x1 = shared_x ? fx->xg : fx->xu; a.t0 = w->gt; a.t1 = w->ut; a.Kin = d.hidden; a.N = d.inter;
+        if ((e = launch_gemm_split<2>(w->bits, dim3(max_items * (d.inter / 128) * skg), s, a)) != hipSuccess) return e;
+        if ((e = launch_gateup_epilogue(s, fx->zgu, picks, w->svh_g, w->svh_u, w->suh_d, fx->xd, P, d.inter, skg,
+                                        d.slots, d.exl3_slots, 10.f, true)) != hipSuccess)
+            return e;
+        a.sk = skd; a.z = fx->zd;
+        a.x0 = fx->xd; a.x1 = fx->xd; a.t0 = w->dt; a.t1 = w->dt; a.Kin = d.inter; a.N = d.hidden;
+        if ((e = launch_gemm_split<1>(w->bits, dim3(max_items * (d.hidden / 256) * skd), s, a)) != hipSuccess) return e;
+        return launch_down_epilogue(s, fx->zd, picks, w->svh_d, fx->out, P, d.hidden, skd, d.slots, d.exl3_slots);
+    }
     // gate / up -> xd
     a.x0 = fx->xg; a.x1 = shared_x ? fx->xg : fx->xu; a.t0 = w->gt; a.t1 = w->ut; a.Kin = d.hidden; a.N = d.inter;
     a.sv0 = w->svh_g; a.sv1 = w->svh_u; a.sd = w->suh_d; a.xd = fx->xd; a.y = fx->out;
@@ -731,7 +814,7 @@ uint16_t* prefill_xd(const gfr_fast_experts* fx) { return fx->xd; }
 void prefill_destroy(gfr_fast_experts* fx) {
     if (!fx) return;
     for (void* p : {(void*)fx->xg, (void*)fx->xu, (void*)fx->xd, (void*)fx->out, (void*)fx->ucnt, (void*)fx->items,
-                    (void*)fx->plan})
+                    (void*)fx->plan, (void*)fx->zgu, (void*)fx->zd})
         if (p) (void)hipFree(p);
     delete fx;
 }

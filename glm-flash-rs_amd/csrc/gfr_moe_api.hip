@@ -386,13 +386,19 @@ int gfr_moe_create(gfr_moe** out, int hidden, int inter, int routed, int topk, i
     if (routed <= 0 || routed > 1023) return fail(GFR_EINVAL, "routed experts %d outside 1..1023", routed);
     if (topk <= 0 || topk > 31 || topk > routed) return fail(GFR_EINVAL, "topk %d", topk);
     if (max_rows <= 0 || max_rows > (1 << 16)) return fail(GFR_EINVAL, "max_rows %d", max_rows);
-    gfr_moe* m = new gfr_moe{hidden, inter, routed, topk, topk + 1, max_rows, 64 < max_rows ? 64 : max_rows,
+    // decode engine for up to 64 rows; by default it takes windows of at most MOE_DECODE_ROWS rows, the prefill
+    // engine (split-K MFMA for small windows) the rest: measured crossover on MI355X between 4 and 8 rows at both
+    // benchmark shapes (hidden 2048 top-4 and hidden 5120 top-8)
+    constexpr int MOE_DECODE_ROWS = 6;
+    const int dec_cap = 64 < max_rows ? 64 : max_rows;
+    gfr_moe* m = new gfr_moe{hidden, inter, routed, topk, topk + 1, max_rows,
+                             MOE_DECODE_ROWS < max_rows ? MOE_DECODE_ROWS : max_rows,
                              nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, {0}, 0};
     const size_t P = (size_t)max_rows * m->slots;
     if ((rc = alloc_zero(&m->weights, P, "moe weights")) || (rc = alloc_zero(&m->picks, P, "moe picks")) ||
         (rc = alloc_zero(&m->out, (size_t)max_rows * hidden, "moe output")) ||
-        (rc = gfr_grouping_create(&m->group_dec, routed + 1, m->slots, m->decode_rows)) ||
-        (rc = gfr_experts_create(&m->dec, hidden, inter, m->slots, m->slots, m->decode_rows))) {
+        (rc = gfr_grouping_create(&m->group_dec, routed + 1, m->slots, dec_cap)) ||
+        (rc = gfr_experts_create(&m->dec, hidden, inter, m->slots, m->slots, dec_cap))) {
         gfr_moe_destroy(m);
         return rc;
     }

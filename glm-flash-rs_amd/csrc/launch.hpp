@@ -52,9 +52,10 @@ hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, const uint
 hipError_t launch_down_finish(hipStream_t s, const float* Zd, const int* pick, const uint16_t* svh_d, float* y,
                               int rows, int P, int D, int SK, int slots, int exl3_slots, const float* weights,
                               float* out);
+// pair_order: xd in the MFMA path's pair order (x[m + 8], x[m] within each 16-value tile) instead of k order
 hipError_t launch_gateup_epilogue(hipStream_t s, const float* Z, const int* pick, const uint16_t* svh_g,
                                   const uint16_t* svh_u, const uint16_t* suh_d, uint16_t* xd, int P, int N, int SK,
-                                  int slots, int exl3_slots, float limit);
+                                  int slots, int exl3_slots, float limit, bool pair_order = false);
 hipError_t launch_down_epilogue(hipStream_t s, const float* Z, const int* pick, const uint16_t* svh_d, float* y,
                                 int P, int D, int SK, int slots, int exl3_slots);
 
