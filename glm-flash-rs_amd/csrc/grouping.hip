@@ -82,23 +82,23 @@ __device__ __forceinline__ void group_small_body(const int* picks, int rows, int
     __syncthreads();
     const int used = base;
     if (threadIdx.x == 0) *count = used;
-    // members: thread per (expert, bitmap word); the word's offset is the popcount of the expert's earlier words
-    for (int i = threadIdx.x; i < E * NWD; i += blockDim.x) {
-        const int e = i / NWD, w = i % NWD;
-        uint32_t b = bits[i];
-        if (!b) continue;
-        int off = 0;
-        for (int q = 0; q < w; ++q) off += __popc(bits[e * NWD + q]);
-        const int u = place[e];
-        while (b) {
-            const int r = w * 32 + __builtin_ctz(b);
-            members[(size_t)u * maxm + off++] = r * 32 + first_slot(picks, r, slots, e);
-            b &= b - 1;
-        }
+    // members: thread per (row, slot); the first slot of row r holding expert e writes code r * 32 + slot at the
+    // row's rank among e's rows (the popcount of e's bitmap below bit r) -- no serial walk over an expert's rows
+    for (int i = threadIdx.x; i < rows * slots; i += blockDim.x) {
+        const int r = i / slots, sl = i - r * slots, e = picks[i];
+        if (e < 0 || e >= E) continue;
+        bool first = true;
+        for (int q = 0; q < sl; ++q) first &= picks[r * slots + q] != e;
+        if (!first) continue;
+        const uint32_t* be = bits + e * NWD;
+        int off = __popc(be[r >> 5] & ((1u << (r & 31)) - 1u));
+        for (int q = 0; q < (r >> 5); ++q) off += __popc(be[q]);
+        members[(size_t)place[e] * maxm + off] = r * 32 + sl;
     }
     // every other entry of the E x maxm table is -1
-    for (size_t i = threadIdx.x; i < (size_t)E * maxm; i += blockDim.x) {
-        const int u = (int)(i / maxm), j = (int)(i % maxm);
+    const int total = E * maxm;
+    for (int i = threadIdx.x; i < total; i += blockDim.x) {
+        const int u = i / maxm, j = i - u * maxm;
         if (u >= used || j >= ucnt[u]) members[i] = -1;
     }
 }
@@ -108,7 +108,10 @@ __global__ void __launch_bounds__(1024) group_small_kernel(const int* __restrict
                                                            int* __restrict__ members, int maxm) {
     extern __shared__ uint32_t lds[];
     __shared__ int scan_scratch[16];
-    group_small_body(picks, rows, slots, E, ids, count, members, maxm, lds, scan_scratch);
+    int* pk = reinterpret_cast<int*>(lds);                     // [rows][slots], read many times below
+    for (int i = threadIdx.x; i < rows * slots; i += blockDim.x) pk[i] = picks[i];
+    __syncthreads();
+    group_small_body(pk, rows, slots, E, ids, count, members, maxm, lds + rows * slots, scan_scratch);
 }
 
 // Decode windows in one launch: wave w routes tokens w, w + 16, ... (route.hpp) into LDS and global picks /
@@ -228,7 +231,7 @@ namespace gfr {
 
 hipError_t launch_group_small(hipStream_t s, const int* picks, int rows, int slots, int E, int* ids, int* count,
                               int* members, int maxm) {
-    const size_t lds = ((size_t)E * ((rows + 31) / 32) + 2 * (size_t)E) * 4;
+    const size_t lds = ((size_t)rows * slots + (size_t)E * ((rows + 31) / 32) + 2 * (size_t)E) * 4;
     group_small_kernel<<<1, 1024, lds, s>>>(picks, rows, slots, E, ids, count, members, maxm);
     return hipGetLastError();
 }
