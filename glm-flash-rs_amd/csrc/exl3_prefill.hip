@@ -322,10 +322,7 @@ template <int MATS, int K, int BM, bool SPLIT = false>
 __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(const PrefillArgs a) {
     constexpr int NCOLS = MATS == 2 ? 128 : 256, RB = BM / 16;
     constexpr int OCC = BM == 256 ? 1 : 2;
-#ifndef PFX_SPLIT_NS
-#define PFX_SPLIT_NS 6
-#endif
-    constexpr int NS = SPLIT ? PFX_SPLIT_NS : OCC == 1 ? (MATS == 2 ? 4 : 6) : (MATS == 2 ? 3 : 4);
+    constexpr int NS = SPLIT ? 4 : OCC == 1 ? (MATS == 2 ? 4 : 6) : (MATS == 2 ? 3 : 4);
     constexpr int XBUF = BM * 64;                        // one matrix's rows of a step (2 k tiles, pair order)
     constexpr int TBUF = 16 * 2 * 32 * K;                // the workgroup's 16 tiles x 2 k tiles of words
     constexpr int STAGE = MATS * XBUF + TBUF;
