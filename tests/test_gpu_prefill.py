@@ -116,11 +116,13 @@ def test_moe_prefill_config4_tokens(gfr, oracle):
 
 
 @pytest.mark.parametrize("bits", [2, 3, 5])
-def test_fast_experts_bit_widths(gfr, oracle, bits):
+@pytest.mark.parametrize("rows", [40, 320])
+def test_fast_experts_bit_widths(gfr, oracle, bits, rows):
     """K = 2, 3, 5 (config 5's mixed bit rates): the MFMA path's generic decode (one trellis lane a thread, pieces
-    handed to their MFMA lanes through LDS) against the oracle, at C5's hidden size."""
+    handed to their MFMA lanes through LDS) against the oracle, at C5's hidden size. 40 rows (360 pairs) run the
+    split-K programs, 320 rows (2880 pairs) the full-K items with the fused epilogues."""
     import synth
-    Dk, Nk, E, slots, rows, maxm = 5120, 1536, 9, 9, 40, 40
+    Dk, Nk, E, slots, maxm = 5120, 1536, 9, 9, rows
     w = synth.experts(E, Dk, Nk, bits, seed=90 + bits)
     picks_np = np.array([[(r * 3 + s) % (E - 1) if s < slots - 1 else E - 1 for s in range(slots)]
                          for r in range(rows)], np.int32)
