@@ -12,7 +12,8 @@ Also measured in the same run:
                 algorithmic bytes per launch / average launch time against the 8 TB/s HBM peak;
   cpu_baseline  the scalar CPU oracle (decode + fp32 matvec of the token's 5 experts, oracle/gfr_oracle.c) on a
                 bounded sample of tokens, 1 thread;
-  prefill       config 4 (8192 tokens, uniform top-4) through the prefill path, against the fp16 MFMA peak.
+  prefill       config 4 (8192 tokens, uniform top-4) through the prefill path, against the fp16 MFMA peak;
+  other_configs configs 1, 3 and 5 (decode and prefill), each against its HBM or MFMA roofline.
 Prints one JSON line.
 """
 import argparse
@@ -198,6 +199,122 @@ def prefill_bench(args, copies, stream):
             "mfma_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
 
 
+def other_configs(args, copies, stream):
+    """The other BASELINE configs, each against its own roofline (secondary lines; `value` stays config 2):
+      c1   one EXL3 linear 2048 -> 1536, K = 4, one fp16 token, cycled over >= 2 GiB of distinct weight copies;
+      c3   the 32-token verify window (Zipf(1.1) top-4) through the layer's decode path, over the 8 layer copies;
+      c5   the 4-layer hidden-5120 stack (160 + 1 experts, top-8, K = 2, 3, 4, 5): bs=1 decode (Zipf top-8) and
+           one 16384-token prefill chunk (Zipf) per step."""
+    import numpy as np
+    import torch
+    import gfr_moe
+    import synth
+    out = {}
+
+    # ---- c1
+    kin, n = 2048, 1536
+    per = kin * n * BITS // 8
+    ncopy = max(2 * 1024 ** 3 // per + 1, 2)
+    pool = synth.trellis((ncopy, kin // 16, n // 16, 8 * BITS), 901)
+    suh, svh = synth.scales((kin,), 902), synth.scales((n,), 903)
+    x = torch.randn(kin, device="cuda").half()
+    y = torch.empty(n, device="cuda")
+    lin = gfr_moe.Linear(kin, n, BITS)
+    glen = min(ncopy, 1024)
+    graph = graph_of([(lambda j=j: lin.run(x, pool[j], suh, svh, y, stream=stream)) for j in range(glen)], stream)
+    reps = max(args.extra_launches // glen, 1)
+    time_graphs([graph], stream)
+    secs = time_graphs([graph] * reps, stream) / (reps * glen)
+    algo = per + kin * 2 + n * 2 + kin * 2 + n * 4
+    out["c1"] = {"config": "config 1: one EXL3 linear 2048->1536, K=4, one fp16 token", "us": round(secs * 1e6, 3),
+                 "bytes": algo, "gbs": round(algo / secs / 1e9, 1), "hbm_frac": round(algo / secs / 1e9 / HBM_PEAK_GBS, 4),
+                 "weight_copies": ncopy}
+    del pool, graph, lin
+    torch.cuda.empty_cache()
+
+    # ---- c3: 32 tokens (4 streams x 8 drafts), Zipf(1.1) top-4, the layer's decode path
+    rows = 32
+    moe = gfr_moe.Moe(D, N, E, TOPK, rows)
+    R = 16
+    xs = synth.activations(R * rows, D, 911)
+    lgs = synth.zipf_logits(R * rows, E, TOPK, 1.1, 912)
+    uniq = []
+    for j in range(R):
+        picks, _ = gfr_moe.route(lgs[j * rows:(j + 1) * rows], TOPK)
+        uniq.append(len(set(picks.cpu().numpy().reshape(-1).tolist())))
+    glen = R * len(copies)
+    graph = graph_of([(lambda j=j: moe.run(copies[j % len(copies)], xs[(j % R) * rows:(j % R + 1) * rows],
+                                           lgs[(j % R) * rows:(j % R + 1) * rows], rows, stream=stream))
+                      for j in range(glen)], stream)
+    time_graphs([graph], stream)
+    reps = 4
+    secs = time_graphs([graph] * reps, stream) / (reps * glen)
+    expert_bytes = 3 * D * N * BITS // 8 + (3 * D + 3 * N) * 2     # trellis + suh_g,u,d / svh_g,u,d
+    algo = float(np.mean(uniq)) * expert_bytes + rows * D * 2 + rows * D * 4
+    out["c3"] = {"config": "config 3: 32-token verify window, Zipf(1.1) top-4 + shared, one MoE layer (the layer's default path for 32 rows: split-K MFMA programs)",
+                 "us_per_window": round(secs * 1e6, 2), "tok_per_s": round(rows / secs, 1),
+                 "distinct_experts_mean": round(float(np.mean(uniq)), 2), "bytes_per_window": int(algo),
+                 "gbs": round(algo / secs / 1e9, 1), "hbm_frac": round(algo / secs / 1e9 / HBM_PEAK_GBS, 4)}
+    del graph, moe
+    torch.cuda.empty_cache()
+
+    # ---- c5: 4 layers, hidden 5120, 160 routed + 1 shared, top-8, K = 2, 3, 4, 5
+    D5, N5, E5, K5 = 5120, 1536, 160, 8
+    bits5 = (2, 3, 4, 5)
+    layers = [synth.experts(E5 + 1, D5, N5, b, seed=920 + 10 * b) for b in bits5]
+    decode = gfr_moe.Moe(D5, N5, E5, K5, 1)
+    R = 16
+    x5 = synth.activations(R, D5, 931)
+    l5 = synth.zipf_logits(R, E5, K5, 1.1, 932)
+    graph = graph_of([(lambda j=j, l=l: decode.run(layers[l], x5[j:j + 1], l5[j:j + 1], 1, stream=stream))
+                      for j in range(R) for l in range(4)], stream)
+    time_graphs([graph], stream)
+    reps = 8
+    secs = time_graphs([graph] * reps, stream) / (reps * R)
+    stack_bytes = sum((K5 + 1) * 3 * D5 * N5 * b // 8 for b in bits5)
+    out["c5_decode"] = {"config": "config 5: 4-layer stack (K=2,3,4,5), hidden 5120, 160+1 experts, top-8, bs=1 "
+                                  "decode, Zipf(1.1)", "us_per_token": round(secs * 1e6, 2),
+                        "tok_per_s": round(1 / secs, 1), "bytes_per_token": stack_bytes,
+                        "gbs": round(stack_bytes / secs / 1e9, 1),
+                        "hbm_frac": round(stack_bytes / secs / 1e9 / HBM_PEAK_GBS, 4)}
+    del graph, decode
+    torch.cuda.empty_cache()
+    if not args.no_prefill:
+        rows5 = args.c5_prefill_rows
+        pre = gfr_moe.Moe(D5, N5, E5, K5, rows5)
+        xp = synth.activations(rows5, D5, 941)
+        lp = synth.zipf_logits(rows5, E5, K5, 1.1, 942) if rows5 <= 4096 else _zipf_logits_gpu(rows5, E5, K5, 1.1, 943)
+        graph = graph_of([(lambda l=l: pre.run(layers[l], xp, lp, rows5, stream=stream)) for l in range(4)], stream)
+        time_graphs([graph], stream)
+        reps = 2
+        secs = time_graphs([graph] * reps, stream) / reps
+        flop = 4 * rows5 * (K5 + 1) * 2 * 3 * D5 * N5
+        out["c5_prefill"] = {"config": f"config 5: 4-layer stack, one {rows5}-token prefill chunk per layer, "
+                                       "Zipf(1.1) top-8 + shared", "ms_per_chunk_4_layers": round(secs * 1e3, 3),
+                             "tok_per_s": round(rows5 / secs, 1), "tflops": round(flop / secs / 1e12, 1),
+                             "mfma_frac": round(flop / secs / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+        del graph, pre
+    del layers
+    torch.cuda.empty_cache()
+    return out
+
+
+def _zipf_logits_gpu(rows, E, topk, s, seed):
+    """Zipf(s) top-k routing logits for many rows, built on the GPU (same construction as synth.zipf_logits:
+    distinct experts drawn with probability 1 / (rank + 1)^s over a seeded permutation, picked logits above the
+    rest and decreasing with the slot)."""
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    perm = torch.randperm(E, generator=g, device="cuda")
+    p = 1.0 / torch.arange(1, E + 1, device="cuda", dtype=torch.float64) ** s
+    chosen = torch.multinomial((p / p.sum()).float().expand(rows, E), topk, replacement=False, generator=g)
+    base = torch.randn((rows, E), generator=g, device="cuda")
+    vals = (8.0 - 0.25 * torch.arange(topk, device="cuda", dtype=torch.float32)).expand(rows, topk)
+    base.scatter_(1, perm[chosen], vals.contiguous())
+    return base
+
+
 def cpu_baseline(args, copies, xs, logits):
     import numpy as np
     import torch
@@ -254,6 +371,9 @@ def main():
     ap.add_argument("--prefill-steps", type=int, default=20)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true", help="first run a 256 MiB copy (counter reference)")
+    ap.add_argument("--no-extra", action="store_true", help="skip the secondary config 1 / 3 / 5 lines")
+    ap.add_argument("--extra-launches", type=int, default=4096)
+    ap.add_argument("--c5-prefill-rows", type=int, default=16384)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -269,6 +389,10 @@ def main():
     if not args.no_prefill:
         prefill = prefill_bench(args, copies, stream)
         log(f"prefill: {prefill['ms_per_layer']} ms/layer, {prefill['achieved_tflops']} TFLOP/s")
+    extra = None
+    if not args.no_extra:
+        extra = other_configs(args, copies, stream)
+        log("other configs: " + json.dumps(extra))
     cpu = cpu_all = None
     if not args.no_cpu:
         cpu, cpu_all = cpu_baseline(args, copies, xs, logits)
@@ -282,6 +406,7 @@ def main():
                                "experts, inter 1536, top-4, K=4", "global_batch": 1, "seq_len": 1,
                    "parallelism": "single-gpu", "weight_copies": args.copies, "routings": args.routings},
         "roofline": roof, "cpu_baseline": cpu, "cpu_baseline_all_cores": cpu_all, "prefill": prefill,
+        "other_configs": extra,
     }
     print(json.dumps(out), flush=True)
 
