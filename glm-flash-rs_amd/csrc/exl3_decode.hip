@@ -199,6 +199,10 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
     uint32_t xv[RB], sv = 0, sg = 0, su = 0;             // XSRC 1: bf16 pairs; scale pairs
     uint4 va = {0, 0, 0, 0}, vb = {0, 0, 0, 0};           // XSRC 0: this lane's k tile of one member
     float gsum[RB][2], usum[RB][2];
+    // XSRC 2, one member at a time: the first four gate / up partials are only loaded here (so that the trellis
+    // loads issue right behind them) and added in build_acts, in split order as the later ones
+    constexpr int EARLY = (XSRC == 2 && RB == 1) ? 4 : 0;
+    float2 zg0[RB][EARLY > 0 ? EARLY : 1], zu0[RB][EARLY > 0 ? EARLY : 1];
     auto load_acts = [&](int r0, int nr) {
         if constexpr (XSRC == 1) {
             sv = *reinterpret_cast<const uint32_t*>((mat ? a.suh1 : a.suh0) + (size_t)e * a.Kin + kt0 * 16 + 2 * lane);
@@ -215,6 +219,16 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
 #pragma unroll
             for (int m = 0; m < RB; ++m) gsum[m][0] = gsum[m][1] = usum[m][0] = usum[m][1] = 0.f;
             const int n = kt0 * 16 + 2 * lane;
+            if constexpr (EARLY > 0) {
+                const int p = __builtin_amdgcn_readlane(pair_l, r0);
+#pragma unroll
+                for (int q = 0; q < EARLY; ++q) {
+                    const int sq = q < a.SKgu ? q : 0;
+                    zg0[0][q] = *reinterpret_cast<const float2*>(a.zgu + ((size_t)sq * a.P + p) * a.Kin + n);
+                    zu0[0][q] = *reinterpret_cast<const float2*>(a.zgu + ((size_t)(a.SKgu + sq) * a.P + p) * a.Kin + n);
+                }
+                return;                                   // the rest is added in build_acts
+            }
             for (int s0 = 0; s0 < a.SKgu; s0 += 4) {      // partials in split order, four in flight
                 float2 zg[RB][4], zu[RB][4];
 #pragma unroll
@@ -260,6 +274,33 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
                     store_block<K>(&xs[wave][m][0], v, lane);
                 }
         } else if constexpr (XSRC == 2) {
+            if constexpr (EARLY > 0) {
+                // the early partials, then the rest four at a time, all in split order
+                const int n = kt0 * 16 + 2 * lane;
+#pragma unroll
+                for (int q = 0; q < EARLY; ++q)
+                    if (q < a.SKgu) {
+                        gsum[0][0] += zg0[0][q].x; gsum[0][1] += zg0[0][q].y;
+                        usum[0][0] += zu0[0][q].x; usum[0][1] += zu0[0][q].y;
+                    }
+                const int p = __builtin_amdgcn_readlane(pair_l, r0);
+                for (int s0 = EARLY; s0 < a.SKgu; s0 += 4) {
+                    float2 zg[4], zu[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if (s0 + q < a.SKgu) {
+                            zg[q] = *reinterpret_cast<const float2*>(a.zgu + ((size_t)(s0 + q) * a.P + p) * a.Kin + n);
+                            zu[q] = *reinterpret_cast<const float2*>(
+                                a.zgu + ((size_t)(a.SKgu + s0 + q) * a.P + p) * a.Kin + n);
+                        }
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if (s0 + q < a.SKgu) {
+                            gsum[0][0] += zg[q].x; gsum[0][1] += zg[q].y;
+                            usum[0][0] += zu[q].x; usum[0][1] += zu[q].y;
+                        }
+                }
+            }
             const float svg[2] = {f16_to_f32((uint16_t)sg), f16_to_f32((uint16_t)(sg >> 16))};
             const float svu[2] = {f16_to_f32((uint16_t)su), f16_to_f32((uint16_t)(su >> 16))};
             const float sdd[2] = {f16_to_f32((uint16_t)sv), f16_to_f32((uint16_t)(sv >> 16))};
@@ -312,16 +353,27 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
 #pragma unroll
         for (int kk = 0; kk < KTW; ++kk) load_words<K>(src + (size_t)kk * NT * (8 * K), wr[kk]);
     }
+    // keep this order: activation loads, every trellis load, then the activations built (waiting only for their
+    // own loads), then tile by tile decode + products as the words land. Left alone, the scheduler sinks the
+    // activation loads below the decode and splits the trellis loads into dependent rounds.
+    __builtin_amdgcn_sched_barrier(0);
 
-    for (int r0 = 0; r0 < cnt; r0 += RB) {
-        const int nr = cnt - r0 < RB ? cnt - r0 : RB;
-        if (r0 > 0) load_acts(r0, nr);
+    // one chunk of up to RB members (the first chunk's activations are already loading; the later chunks load
+    // theirs first). The first chunk is its own copy of the code so that its activation wait covers its own loads
+    // only, not the trellis words issued after them.
+    auto chunk = [&](int r0, int nr) {
         build_acts(r0, nr);
+        __builtin_amdgcn_sched_barrier(0);
         float acc[RB][2];
 #pragma unroll
         for (int m = 0; m < RB; ++m) acc[m][0] = acc[m][1] = 0.f;
 #pragma unroll
         for (int kk = 0; kk < KTW; ++kk) {
+            // tile kk's words, as a value of this iteration: its decode waits for its own load only and is not
+            // hoisted above the activation build (the words are loop-invariant otherwise; hoisted, the decoded
+            // tiles held 128 registers and cut the resident waves)
+#pragma unroll
+            for (int j = 0; j < K; ++j) __asm__ volatile("" : "+v"(wr[kk][j]));
             const uint32_t prev = prev_word(wr[kk][K - 1], i);
             h2_t d[2][8];
             decode_lane<K>(wr[kk], prev, d);
@@ -366,6 +418,12 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
             }
             if (r0 + RB < cnt) __syncthreads();            // red is rewritten by the next chunk
         }
+    };
+    chunk(0, nr0);
+    for (int r0 = RB; r0 < cnt; r0 += RB) {
+        const int nr = cnt - r0 < RB ? cnt - r0 : RB;
+        load_acts(r0, nr);
+        chunk(r0, nr);
     }
 }
 
