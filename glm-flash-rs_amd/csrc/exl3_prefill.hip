@@ -353,10 +353,13 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
     const int it = a.items[item];
     const int u = it >> 16, pass = it & 0xffff;
     const int e = a.uids[u];
-    const int nrows = min(BM, a.ucnt[u] - pass * BM);
+    // the expert's members split evenly over its ceil(cnt / BM) passes; row blocks past nrows skip their MFMAs
+    const int ucnt = a.ucnt[u], npass = (ucnt + BM - 1) / BM;
+    const int rbeg = pass * ucnt / npass, nrows = (pass + 1) * ucnt / npass - rbeg;
+    const int nblk = (nrows + 15) >> 4;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     {
-        const int* mrow = a.members + (size_t)u * a.maxm + pass * BM;
+        const int* mrow = a.members + (size_t)u * a.maxm + rbeg;
         const int c0 = mrow[0];
         const int p0 = (c0 >> 5) * a.slots + (c0 & 31);
         const int code = tid < nrows ? mrow[tid] : -1;
@@ -500,9 +503,11 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
             for (int b = 0; b < RB; ++b) {
                 const h8_t bc = ring[b % D];
                 ring[b % D] = b + D < RB ? read_b(s, b + D) : read_b(sn, b + D - RB);
+                if (b < nblk) {
 #pragma unroll
-                for (int t4 = 0; t4 < 4; ++t4)
-                    acc[t4][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac[t4], bc, acc[t4][b], 0, 0, 0);
+                    for (int t4 = 0; t4 < 4; ++t4)
+                        acc[t4][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac[t4], bc, acc[t4][b], 0, 0, 0);
+                }
 #pragma unroll
                 for (int pr = b * 16 / RB; pr < (b + 1) * 16 / RB; ++pr) {   // the 16 decoded pairs spread evenly
                     const int t = pr >> 2, j = pr & 3;
@@ -519,9 +524,11 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
             for (int b = 0; b < RB; ++b) {
                 const h8_t bc = ring[b % D];
                 ring[b % D] = b + D < RB ? read_b(s, b + D) : read_b(sn, b + D - RB);
+                if (b < nblk) {
 #pragma unroll
-                for (int t4 = 0; t4 < 4; ++t4)
-                    acc[t4][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac[t4], bc, acc[t4][b], 0, 0, 0);
+                    for (int t4 = 0; t4 < 4; ++t4)
+                        acc[t4][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac[t4], bc, acc[t4][b], 0, 0, 0);
+                }
             }
         }
         // keep the decode inside this step (the compiler would otherwise sink it next to its use)
