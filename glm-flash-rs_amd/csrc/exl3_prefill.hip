@@ -296,6 +296,18 @@ __device__ __forceinline__ void load_lds16(const void* g, void* lds_base) {
     __asm__ volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(g), "{m0}"(m0) : "memory");
 }
 
+// The same load in the scalar-base form: lane i reads sbase + voff_i (32-bit unsigned per-lane offset), so a
+// per-step advance is one 64-bit scalar add and the LDS destination (m0) stays in scalar registers.
+__device__ __forceinline__ void load_lds16_s(uint64_t sbase, uint32_t voff, uint32_t m0) {
+    __asm__ volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" :: "v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+}
+__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
+    // readfirstlane returns int: through uint32_t, so that the low word is not sign-extended into the high one
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (uint64_t)lo | ((uint64_t)hi << 32);
+}
+
 // Workgroup barrier for LDS-only hand-offs: this wave's LDS operations complete, then s_barrier. Unlike
 // __syncthreads() it does not wait for outstanding global loads (the staged direct-to-LDS loads of later steps).
 __device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
@@ -373,36 +385,58 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
     const int wtile0 = MATS == 2 ? (wave & 1) * 4 : wave * 4;   // the wave's first tile within its matrix's columns
     const int stile0 = MATS == 2 ? mat * 8 + wtile0 : wtile0;    // ... within the staged tiles
 
-    // the lane's direct loads: rows (XLOADS of them, 16 rows a load) and one trellis chunk
-    const uint16_t* xsrc[XLOADS];
+    // the lane's direct loads: rows (XLOADS of them, 16 rows a load) and one trellis chunk, each as a uniform 64-bit
+    // base (advanced per step with scalar adds) and a per-lane 32-bit byte offset (the host keeps every offset below
+    // 2^32); the LDS destinations are uniform too
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t lds_u = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
+    uint64_t xbase[XLOADS];
+    uint32_t xoff[XLOADS];
 #pragma unroll
     for (int j = 0; j < XLOADS; ++j) {
-        const int t = min(wave * XLOADS + j, MATS * RB - 1);   // 16-row block of the stage (MATS * RB of them)
+        const int t = min(wv * XLOADS + j, MATS * RB - 1);     // 16-row block of the stage (MATS * RB of them)
         const int m = t / RB, row = (t % RB) * 16 + lane / 4, pos = lane & 3;
         const int c = pos ^ ((row >> 1) & 3);              // the global chunk this LDS position holds
-        xsrc[j] = (m ? a.x1 : a.x0) + (size_t)rows_sh[row] * a.Kin + (size_t)s0 * 32 + (c >> 1) * 16 + (c & 1) * 8;
+        xbase[j] = uniform64((uint64_t)(uintptr_t)(m ? a.x1 : a.x0) + (uint64_t)s0 * 64);
+        xoff[j] = (uint32_t)rows_sh[row] * (uint32_t)(a.Kin * 2) + (uint32_t)((c >> 1) * 32 + (c & 1) * 16);
     }
     // trellis words: 32 blocks (tile, k tile) of 32 K bytes, K loads of 64 16-byte chunks; wave w issues loads
-    // w, w + 4, ... (the last one repeated where K is not a multiple of 4: the same bytes to the same place)
+    // w, w + 4, ... (the last one repeated where K is not a multiple of 4: the same bytes to the same place). The
+    // matrix of a load is uniform unless a load straddles the gate / up halves (MATS = 2, K = 3 or 5): then the
+    // lanes keep 64-bit addresses.
+    constexpr bool TUNI = MATS == 1 || K == 2 || K == 4;
     const uint32_t* tsrc[TL];
+    uint64_t tbase[TL];
+    uint32_t toff[TL];
     int tdst[TL];
 #pragma unroll
     for (int j = 0; j < TL; ++j) {
-        const int li = wave + 4 * j < K ? wave + 4 * j : K - 1;
+        const int li = wv + 4 * j < K ? wv + 4 * j : K - 1;
         const int c = li * 64 + lane, blk = c / (2 * K), ch = c % (2 * K);
         const int tile = blk >> 1, kt = blk & 1;
         const int tmat = MATS == 2 ? tile >> 3 : 0;
         const int ntile = col0 / 16 + (MATS == 2 ? (tile & 7) : tile);
-        tsrc[j] = (tmat ? a.t1 : a.t0) + (((size_t)e * KT + 2 * s0 + kt) * NT + ntile) * (8 * K) + ch * 4;
+        const uint32_t* tm = tmat ? a.t1 : a.t0;
+        if constexpr (TUNI) {
+            tbase[j] = uniform64((uint64_t)(uintptr_t)tm + (uint64_t)s0 * 2 * NT * (8 * K) * 4);
+            toff[j] = (uint32_t)((((e * KT + kt) * NT + ntile) * (8 * K) + ch * 4) * 4);
+        } else {
+            tsrc[j] = tm + (((size_t)e * KT + 2 * s0 + kt) * NT + ntile) * (8 * K) + ch * 4;
+        }
         tdst[j] = MATS * XBUF + li * 1024;
     }
     auto issue = [&](int s) {
-        unsigned char* st = lds + (s % NS) * STAGE;
+        const uint32_t st = lds_u + (uint32_t)((s % NS) * STAGE);
 #pragma unroll
         for (int j = 0; j < XLOADS; ++j)
-            load_lds16(xsrc[j] + (size_t)s * 32, st + min(wave * XLOADS + j, MATS * RB - 1) * 1024);
+            load_lds16_s(xbase[j] + (uint64_t)s * 64, xoff[j], st + min(wv * XLOADS + j, MATS * RB - 1) * 1024);
 #pragma unroll
-        for (int j = 0; j < TL; ++j) load_lds16(tsrc[j] + (size_t)s * 2 * NT * (8 * K), st + tdst[j]);
+        for (int j = 0; j < TL; ++j) {
+            if constexpr (TUNI)
+                load_lds16_s(tbase[j] + (uint64_t)s * 2 * NT * (8 * K) * 4, toff[j], st + tdst[j]);
+            else
+                load_lds16(tsrc[j] + (size_t)s * 2 * NT * (8 * K), lds + (s % NS) * STAGE + tdst[j]);
+        }
     };
     // wait until at most n stages' loads of this wave are outstanding
     static_assert(NS - 2 <= 6 && 6 * LOADS < 64, "vmcnt range");
@@ -754,6 +788,11 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
     const int P = rows * d.slots;
     const int maxu = P < w->experts ? P : w->experts;
     if (maxu > PF_MAXU) return hipErrorInvalidValue;
+    // the GEMM's direct loads address rows and trellis words by 32-bit byte offsets from their matrix
+    const uint64_t lim = 1ull << 32;
+    if ((uint64_t)P * d.hidden * 2 >= lim || (uint64_t)P * d.inter * 2 >= lim ||
+        (uint64_t)w->experts * d.hidden * d.inter * w->bits / 8 >= lim)
+        return hipErrorInvalidValue;
     hipError_t e;
     // rotated rows of every EXL3 pair (one copy when the two input rotations are the same)
     {
