@@ -118,15 +118,35 @@ __global__ void __launch_bounds__(1024) prefill_plan_kernel(const int* __restric
 __device__ __forceinline__ int l8_j(int lane) { return (lane & 3) | ((lane >> 3) & 3) << 2; }
 __device__ __forceinline__ int l8_row(int lane) { return ((lane >> 2) & 1) | ((lane >> 5) & 1) << 1; }
 
+// One butterfly stage across lanes (lane xor M) on values held with a lane sign: every lane computes u + m p, with
+// p the partner's value and m = -1 on the upper lane of the pair, +1 on the lower. The lower lane gets the true
+// lower + upper; the upper lane gets lower - upper negated. Partners of a stage share their sign so far (they differ
+// only in this stage's lane bit), so the plain +-1 multiplier is right at every stage, and after the four stages the
+// lane holds sigma * H(x) with sigma = (-1)^popcount(lane & 0b11011) (lane_sign). Negation is exact, so every value is
+// bit for bit +- the reference's butterfly result. Stages xor 1, 2, 8 are one v_fmac_f32_dpp a value (the DPP read of
+// a VGPR written by the VALU just before needs two wait states: the s_nop); xor 16 goes through ds_swizzle.
 template <int M>
-__device__ __forceinline__ void fwht_l8_cross(float (&v)[8], int lane) {
-    const float sgn = (lane & M) ? -1.f : 1.f;            // lower: v + other, upper: other - v
+__device__ __forceinline__ void fwht_l8_cross(float (&v)[8], float m) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(sgn, v[i], lane_xor_f<M>(v[i]));
+    for (int i = 0; i < 8; ++i) {
+        if constexpr (M == 1)
+            __asm__ volatile("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf"
+                             : "+v"(v[i]) : "v"(m));
+        else if constexpr (M == 2)
+            __asm__ volatile("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf"
+                             : "+v"(v[i]) : "v"(m));
+        else if constexpr (M == 8)
+            __asm__ volatile("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 row_ror:8 row_mask:0xf bank_mask:0xf"
+                             : "+v"(v[i]) : "v"(m));
+        else
+            v[i] = __builtin_fmaf(lane_xor_f<M>(v[i]), m, v[i]);
+    }
 }
+// sigma of the lane (see fwht_l8_cross): the sign a transformed value carries
+__device__ __forceinline__ float lane_sign(int lane) { return (__popc(lane & 0x1b) & 1) ? -1.f : 1.f; }
 
 // 128-point unnormalised Walsh-Hadamard transform of four rows a wave (butterflies at strides 1, 2, ..., 64, each
-// (lower + upper, lower - upper) in fp32, as experts.rs:25-42).
+// (lower + upper, lower - upper) in fp32, as experts.rs:25-42), returned times lane_sign(lane).
 __device__ __forceinline__ void fwht128_l8(float (&v)[8], int lane) {
 #pragma unroll
     for (int st = 1; st < 8; st <<= 1)
@@ -137,20 +157,29 @@ __device__ __forceinline__ void fwht128_l8(float (&v)[8], int lane) {
                 v[i] = a + b;
                 v[i + st] = a - b;
             }
-    fwht_l8_cross<1>(v, lane);
-    fwht_l8_cross<2>(v, lane);
-    fwht_l8_cross<8>(v, lane);
-    fwht_l8_cross<16>(v, lane);
+    fwht_l8_cross<1>(v, (lane & 1) ? -1.f : 1.f);
+    fwht_l8_cross<2>(v, (lane & 2) ? -1.f : 1.f);
+    fwht_l8_cross<8>(v, (lane & 8) ? -1.f : 1.f);
+    fwht_l8_cross<16>(v, (lane & 16) ? -1.f : 1.f);
 }
 
-// fp16(v / sqrt(128)) of a row held as above, stored in the pair order of pair_row (K != 2) into a 128-value block:
+// Round two values to bf16 (round to nearest even) with one v_cvt_pk_bf16_f32.
+typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
+typedef float f2v_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void bf16r2(float& a, float& b) {
+    const uint32_t d = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v_t){a, b}, bf2_t));
+    a = __builtin_bit_cast(float, d << 16);
+    b = __builtin_bit_cast(float, d & 0xffff0000u);
+}
+
+// fp16(v * scale) of a row held as above (scale = lane_sign / sqrt(128) undoes the transform's lane sign), stored in the pair order of pair_row (K != 2) into a 128-value block:
 // pair m of k tile kt = (x[m + 8] low, x[m] high), so the lane of the tile's first half (j even) pairs with its
 // neighbour (lane xor 1) that holds the second; the even lane stores pairs 0-3, the odd lane pairs 4-7.
-__device__ __forceinline__ void store_pairs_l8(uint16_t* block, const float (&v)[8], int lane) {
+__device__ __forceinline__ void store_pairs_l8(uint16_t* block, const float (&v)[8], int lane, float scale) {
     uint32_t w[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        w[i] = (uint32_t)f16_of_product(v[2 * i], HAD_SCALE) | ((uint32_t)f16_of_product(v[2 * i + 1], HAD_SCALE) << 16);
+        w[i] = (uint32_t)f16_of_product(v[2 * i], scale) | ((uint32_t)f16_of_product(v[2 * i + 1], scale) << 16);
     const int j = l8_j(lane);
     const bool odd = j & 1;
     const uint32_t r0 = lane_xor<1>(odd ? w[0] : w[2]), r1 = lane_xor<1>(odd ? w[1] : w[3]);
@@ -217,7 +246,7 @@ __global__ void __launch_bounds__(256) prefill_rot_kernel(const uint16_t* __rest
             v[2 * i + 1] = xf[2 * i + 1] * f16_to_f32((uint16_t)(sw[i] >> 16));
         }
         fwht128_l8(v, lane);
-        if (valid) store_pairs_l8((m ? out1 : out0) + (size_t)p * K + blk * 128, v, lane);
+        if (valid) store_pairs_l8((m ? out1 : out0) + (size_t)p * K + blk * 128, v, lane, lane_sign(lane) * HAD_SCALE);
     }
 }
 
@@ -619,7 +648,15 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
                 sc[m][2 * i + 1] = f16_to_f32((uint16_t)(vv[i] >> 16));
             }
         }
+        // the transformed accumulators carry lane_sign: fold it into the scales that multiply them (exact)
+        const float sg = lane_sign(lane);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            sc[0][i] *= sg;
+            sc[1][i] *= sg;
+        }
     }
+    const float had_sg = lane_sign(lane) * HAD_SCALE;
     const int ncol = (MATS == 2 ? mat * 128 : 0) + wtile0 * 16 + 4 * (lane >> 4);
     auto ld8 = [&](int row, int col, float (&v)[8]) {
         const float4 x = *reinterpret_cast<const float4*>(ep + row * EPITCH + col);
@@ -651,17 +688,27 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
                 fwht128_l8(gv, lane);
                 fwht128_l8(uv, lane);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float gg = fminf(bf16r(gv[i] * HAD_SCALE * sc[0][i]), a.limit);
-                    const float uu = fminf(fmaxf(bf16r(uv[i] * HAD_SCALE * sc[1][i]), -a.limit), a.limit);
+                for (int i = 0; i < 8; i += 2) {
+                    // bf16 roundings two values at a time (g with u, then element i with i + 1)
+                    float g0 = gv[i] * HAD_SCALE * sc[0][i], u0 = uv[i] * HAD_SCALE * sc[1][i];
+                    float g1 = gv[i + 1] * HAD_SCALE * sc[0][i + 1], u1 = uv[i + 1] * HAD_SCALE * sc[1][i + 1];
+                    bf16r2(g0, u0);
+                    bf16r2(g1, u1);
+                    const float gg0 = fminf(g0, a.limit), uu0 = fminf(fmaxf(u0, -a.limit), a.limit);
+                    const float gg1 = fminf(g1, a.limit), uu1 = fminf(fmaxf(u1, -a.limit), a.limit);
                     // silu through the hardware exp2 / reciprocal (within an ulp or two of expf and the IEEE divide;
                     // the bf16 rounding that follows absorbs the difference)
-                    const float ex = __builtin_amdgcn_exp2f(gg * -1.4426950408889634f);
-                    const float act = bf16r(bf16r(gg * __builtin_amdgcn_rcpf(1.f + ex)) * uu);
-                    gv[i] = act * sc[2][i];
+                    const float ex0 = __builtin_amdgcn_exp2f(gg0 * -1.4426950408889634f);
+                    const float ex1 = __builtin_amdgcn_exp2f(gg1 * -1.4426950408889634f);
+                    float s0 = gg0 * __builtin_amdgcn_rcpf(1.f + ex0), s1 = gg1 * __builtin_amdgcn_rcpf(1.f + ex1);
+                    bf16r2(s0, s1);
+                    float a0 = s0 * uu0, a1 = s1 * uu1;
+                    bf16r2(a0, a1);
+                    gv[i] = a0 * sc[2][i];
+                    gv[i + 1] = a1 * sc[2][i + 1];
                 }
                 fwht128_l8(gv, lane);
-                if (row < nrows) store_pairs_l8(a.xd + (size_t)rows_sh[row] * a.N + col0, gv, lane);
+                if (row < nrows) store_pairs_l8(a.xd + (size_t)rows_sh[row] * a.N + col0, gv, lane, had_sg);
             } else {
                 float v[2][8];
                 ld8(rr, 8 * j8, v[0]);
