@@ -71,6 +71,11 @@ int check_shape(int hidden, int inter) {
 
 }  // namespace
 
+namespace gfr {
+// the thread's last error, for the other translation units of the library (prepared.hip)
+int set_error(int code, const std::string& msg) { return fail(code, "%s", msg.c_str()); }
+}  // namespace gfr
+
 struct gfr_grouping {
     int experts, slots, max_rows;
     uint32_t* bits;

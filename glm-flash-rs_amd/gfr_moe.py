@@ -67,6 +67,20 @@ def _load() -> ctypes.CDLL:
         "gfr_exl3_rotate": ([P, P, I, I, P, P, I, I, P], I),
         "gfr_route_topk": ([P, P, I, I, I, P, P], I),
         "gfr_exl3_grouped_gemv": ([P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I], I),
+        "gfr_prepared_open": ([ctypes.POINTER(VP), ctypes.c_char_p], I),
+        "gfr_prepared_tensor_count": ([VP], I),
+        "gfr_prepared_tensor_name": ([VP, I], ctypes.c_char_p),
+        "gfr_prepared_tensor": ([VP, ctypes.c_char_p, ctypes.POINTER(TensorInfo)], I),
+        "gfr_prepared_expect": ([VP, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64), I], I),
+        "gfr_prepared_read_tensor": ([VP, ctypes.c_char_p, ctypes.c_uint64, ctypes.c_uint64, P], I),
+        "gfr_prepared_load": ([VP, ctypes.POINTER(ctypes.c_char_p), I], I),
+        "gfr_prepared_loaded": ([VP, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_double)], I),
+        "gfr_prepared_pointer": ([VP, ctypes.c_char_p, ctypes.POINTER(VP)], I),
+        "gfr_prepared_experts": ([VP, I, ctypes.POINTER(_Exl3Struct)], I),
+        "gfr_prepared_destroy": ([VP], I),
+        "gfr_sha256_hex": ([P, ctypes.c_uint64, ctypes.c_char_p], I),
+        "gfr_tensor_extent": ([ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64), I, I,
+                               ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)], I),
     }
     for name, (args, res) in sig.items():
         f = getattr(lib, name)
@@ -320,3 +334,94 @@ def decode_tiles(trellis: torch.Tensor, kin: int, n: int, bits: int, stream=None
     out = torch.empty((kin, n), dtype=torch.float16, device=trellis.device)
     _check(lib().gfr_exl3_decode_tiles(_stream(stream), _ptr(trellis), kin, n, bits, _ptr(out)))
     return out
+
+
+# ---- prepared weights (src/prepared.rs) ------------------------------------------------------------------------------
+
+class TensorInfo(ctypes.Structure):
+    """gfr_tensor_info: one tensor view of a prepared model (the reference's prepared::Tensor, prepared.rs:32-41)."""
+    _fields_ = [("storage", ctypes.c_int), ("dtype", ctypes.c_char * 24), ("rank", ctypes.c_int),
+                ("shape", ctypes.c_uint64 * 8), ("stride", ctypes.c_uint64 * 8), ("off", ctypes.c_uint64),
+                ("cuda", ctypes.c_int), ("extent_bytes", ctypes.c_uint64)]
+
+
+def _u64s(xs):
+    return (ctypes.c_uint64 * max(len(xs), 1))(*xs)
+
+
+def sha256_hex(data: bytes) -> str:
+    """The prepared format's chunk hash (FIPS 180-4 SHA-256), computed by the library."""
+    out = ctypes.create_string_buffer(65)
+    buf = ctypes.create_string_buffer(bytes(data), len(data))
+    _check(lib().gfr_sha256_hex(ctypes.addressof(buf), len(data), out))
+    return out.value.decode()
+
+
+def tensor_extent(dtype: str, shape, stride, off: int) -> int:
+    """Tensor::extent (prepared.rs:51-71): bytes from the storage start past the view's last element."""
+    out = ctypes.c_uint64()
+    _check(lib().gfr_tensor_extent(dtype.encode(), _u64s(shape), _u64s(stride), len(shape), len(stride), off,
+                                   ctypes.byref(out)))
+    return out.value
+
+
+class Prepared(_Engine):
+    """Prepared::open / tensor / expect / read_tensor / load_selected + Loaded::pointer (src/prepared.rs) over the
+    library's loader. open and read_tensor need no GPU; load copies the selected storages into device memory."""
+
+    _destroy = "gfr_prepared_destroy"
+
+    def __init__(self, manifest_path: str):
+        super().__init__()
+        _check(lib().gfr_prepared_open(ctypes.byref(self._h), str(manifest_path).encode()))
+
+    def names(self):
+        L = lib()
+        return [L.gfr_prepared_tensor_name(self._h, i).decode() for i in range(L.gfr_prepared_tensor_count(self._h))]
+
+    def tensor(self, path: str) -> TensorInfo:
+        info = TensorInfo()
+        _check(lib().gfr_prepared_tensor(self._h, path.encode(), ctypes.byref(info)))
+        return info
+
+    def expect(self, path: str, dtype: str, shape):
+        _check(lib().gfr_prepared_expect(self._h, path.encode(), dtype.encode(), _u64s(shape), len(shape)))
+
+    def read_tensor(self, path: str, offset: int = 0, length: int = None) -> bytes:
+        """read_tensor / read_tensor_segment: bytes of the view's extent past its start, from disk."""
+        if length is None:
+            t = self.tensor(path)
+            eb = {"bool": 1, "uint8": 1, "int8": 1, "float8_e4m3fn": 1, "float8_e5m2": 1, "bfloat16": 2, "float16": 2,
+                  "int16": 2, "uint16": 2, "float32": 4, "int32": 4, "uint32": 4, "float64": 8, "int64": 8,
+                  "uint64": 8}[t.dtype.decode()]
+            length = t.extent_bytes - t.off * eb - offset
+        buf = ctypes.create_string_buffer(max(length, 1))
+        _check(lib().gfr_prepared_read_tensor(self._h, path.encode(), offset, length, ctypes.addressof(buf)))
+        return buf.raw[:length]
+
+    def load(self, prefixes=()):
+        arr = (ctypes.c_char_p * max(len(prefixes), 1))(*[p.encode() for p in prefixes])
+        _check(lib().gfr_prepared_load(self._h, arr, len(prefixes)))
+        b, s = ctypes.c_uint64(), ctypes.c_double()
+        _check(lib().gfr_prepared_loaded(self._h, ctypes.byref(b), ctypes.byref(s)))
+        return b.value, s.value
+
+    def pointer(self, path: str) -> int:
+        p = ctypes.c_void_p()
+        _check(lib().gfr_prepared_pointer(self._h, path.encode(), ctypes.byref(p)))
+        return p.value
+
+    def experts(self, layer: int, device="cuda") -> Exl3Experts:
+        """weights.layers[layer].moe.experts.* as an Exl3Experts of views into the loaded storages (no copy; valid
+        while this object lives)."""
+        st = _Exl3Struct()
+        _check(lib().gfr_prepared_experts(self._h, layer, ctypes.byref(st)))
+        E, D, N, b = st.experts, st.hidden, st.inter, st.bits
+        _TYPESTR.setdefault(torch.int32, "<i4")
+        v = lambda name, shape, dt: _view(getattr(st, name), shape, dt, device)
+        return Exl3Experts(gt=v("gt", (E, D // 16, N // 16, 8 * b), torch.int32),
+                           ut=v("ut", (E, D // 16, N // 16, 8 * b), torch.int32),
+                           dt=v("dt", (E, N // 16, D // 16, 8 * b), torch.int32),
+                           suh_g=v("suh_g", (E, D), torch.float16), suh_u=v("suh_u", (E, D), torch.float16),
+                           suh_d=v("suh_d", (E, N), torch.float16), svh_g=v("svh_g", (E, N), torch.float16),
+                           svh_u=v("svh_u", (E, N), torch.float16), svh_d=v("svh_d", (E, D), torch.float16), bits=b)

@@ -153,6 +153,50 @@ int gfr_exl3_rotate(hipStream_t stream, const uint16_t* x, int x_stride, int x_f
 /* ---- Debug / parity: decoded fp16 weights of one matrix [kin][n] (row = k), bit-exact to experts.rs:47-74 ---- */
 int gfr_exl3_decode_tiles(hipStream_t stream, const uint32_t* trellis, int kin, int n, int bits, uint16_t* out);
 
+/* ---- Prepared weights (src/prepared.rs) ------------------------------------------------------------------------
+ * The reference's prepared format: a JSON manifest {format: 1, file_size, chunk, chunk_sha256[], storages[], tree,
+ * key} next to data.bin (prepared.rs:15-40). Tensor paths are the reference's ("weights.layers[3].moe.experts.gt").
+ * open     = Prepared::open_parts + the tree walk (prepared.rs:101-132, 186-230): storages ascending, non-overlapping,
+ *            inside data.bin; every tensor view inside its storage and on its storage's device. The reference's
+ *            model-identity checks (model name, TP4 rank, GLM geometry, :151-185) are not applied: they belong to its
+ *            full model.
+ * load     = Prepared::load_selected (:270-366): storages holding a tensor under one of the prefixes (all when
+ *            nprefixes = 0), data.bin read in manifest-chunk pieces through pinned staging, each needed piece checked
+ *            against its SHA-256 before it is copied; keeps 8 GiB of device memory free. Allocates (hipMalloc).
+ * pointer  = Loaded::pointer (:369-377); expect = Prepared::expect (:236-248); read_tensor = read_tensor_segment
+ *            (:253-266, from disk, no device needed); experts = the weights.layers[L].moe.experts.* lookups of
+ *            ExpertGpu::run_rows (experts.rs:467) with the shapes of experts::probe (:146-156), any E / hidden / inter /
+ *            bits. Not thread-safe; one prepared model per thread. */
+#define GFR_TENSOR_MAX_RANK 8
+typedef struct gfr_tensor_info {
+    int storage;
+    char dtype[24];
+    int rank;
+    uint64_t shape[GFR_TENSOR_MAX_RANK];
+    uint64_t stride[GFR_TENSOR_MAX_RANK];
+    uint64_t off;            /* element offset into the storage */
+    int cuda;                /* 1: device storage, 0: host ("cpu") */
+    uint64_t extent_bytes;   /* Tensor::extent (prepared.rs:51-71) */
+} gfr_tensor_info;
+typedef struct gfr_prepared gfr_prepared;
+int gfr_prepared_open(gfr_prepared** out, const char* manifest_path);
+int gfr_prepared_tensor_count(const gfr_prepared* p);
+const char* gfr_prepared_tensor_name(const gfr_prepared* p, int i);           /* path order */
+int gfr_prepared_tensor(const gfr_prepared* p, const char* path, gfr_tensor_info* info);
+int gfr_prepared_expect(const gfr_prepared* p, const char* path, const char* dtype, const uint64_t* shape, int rank);
+int gfr_prepared_read_tensor(const gfr_prepared* p, const char* path, uint64_t offset, uint64_t len, void* host_out);
+int gfr_prepared_load(gfr_prepared* p, const char* const* prefixes, int nprefixes);
+int gfr_prepared_loaded(const gfr_prepared* p, uint64_t* device_bytes, double* seconds);
+int gfr_prepared_pointer(const gfr_prepared* p, const char* path, void** device_ptr);
+int gfr_prepared_experts(const gfr_prepared* p, int layer, gfr_exl3_experts* out);
+int gfr_prepared_destroy(gfr_prepared* p);
+/* The format's hash: lowercase hex SHA-256 (FIPS 180-4) of a host buffer into out65 (64 digits + NUL). */
+int gfr_sha256_hex(const void* data, uint64_t len, char* out65);
+/* Tensor::extent (prepared.rs:51-71) of a described view: bytes from the storage start past its last element;
+ * GFR_EINVAL on a rank mismatch, an unknown dtype or overflow. */
+int gfr_tensor_extent(const char* dtype, const uint64_t* shape, const uint64_t* stride, int shape_rank,
+                      int stride_rank, uint64_t off, uint64_t* bytes);
+
 #ifdef __cplusplus
 }
 #endif
