@@ -18,6 +18,7 @@
 
 #include <algorithm>
 #include <chrono>
+#include <thread>
 #include <map>
 #include <memory>
 #include <string>
@@ -536,7 +537,8 @@ int gfr_prepared_read_tensor(const gfr_prepared* p, const char* path, uint64_t o
 // Prepared::load_selected (prepared.rs:270-366): the storages holding a tensor under one of the prefixes (all when
 // there are none) are allocated (device storages with hipMalloc, host ones in memory), then data.bin is read chunk by
 // chunk through pinned staging; every chunk that overlaps a selected storage is SHA-256-checked against the manifest
-// before its bytes are copied. Requires 8 GiB of device memory to stay free, as the reference does.
+// before its bytes are copied (the chunks of a batch are hashed in parallel threads, which the reference does one at
+// a time). Requires 8 GiB of device memory to stay free, as the reference does.
 int gfr_prepared_load(gfr_prepared* p, const char* const* prefixes, int nprefixes) {
     if (!p || nprefixes < 0 || (nprefixes && !prefixes)) return err("bad arguments");
     release(p);
@@ -564,47 +566,72 @@ int gfr_prepared_load(gfr_prepared* p, const char* const* prefixes, int nprefixe
             p->host[j].resize(p->storages[j].nbytes);
         }
     }
+    // staging for a batch of chunks, hashed in parallel (one thread a chunk); at most 1 GiB of pinned memory
+    const unsigned hw = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    const uint64_t nbuf = std::max<uint64_t>(1, std::min<uint64_t>(hw, (1ull << 30) / p->chunk));
     uint8_t* staging = nullptr;
-    if ((e = hipHostMalloc((void**)&staging, p->chunk, hipHostMallocDefault)) != hipSuccess) {
+    if ((e = hipHostMalloc((void**)&staging, nbuf * p->chunk, hipHostMallocDefault)) != hipSuccess) {
         release(p);
         return gfr::set_error((int)e, std::string("hipHostMalloc: ") + hipGetErrorString(e));
     }
     FILE* f = fopen(p->data_path.c_str(), "rb");
     int rc = f ? 0 : err("cannot open " + p->data_path);
     size_t first = 0;
-    uint64_t offset = 0;
-    for (size_t i = 0; rc == 0 && i < p->chunk_sha256.size(); ++i) {
-        const uint64_t len = std::min(p->file_size - offset, p->chunk);
-        bool needed = false;
-        for (size_t j = 0; j < p->storages.size() && !needed; ++j)
-            needed = sel[j] && p->storages[j].offset < offset + len && p->storages[j].offset + p->storages[j].nbytes > offset;
-        if (!needed) {
-            offset += len;
-            if (fseeko(f, (off_t)offset, SEEK_SET) != 0) rc = err("seek in " + p->data_path);
-            continue;
+    uint64_t pos = 0;                           // file position of the reader
+    auto needed = [&](uint64_t off, uint64_t len) {
+        for (size_t j = 0; j < p->storages.size(); ++j)
+            if (sel[j] && p->storages[j].offset < off + len && p->storages[j].offset + p->storages[j].nbytes > off)
+                return true;
+        return false;
+    };
+    for (size_t i0 = 0; rc == 0 && i0 < p->chunk_sha256.size();) {
+        // the next batch: up to nbuf needed chunks, read in file order
+        std::vector<size_t> idx;
+        for (size_t i = i0; i < p->chunk_sha256.size() && idx.size() < nbuf; ++i) {
+            i0 = i + 1;
+            const uint64_t off = i * p->chunk, len = std::min(p->file_size - off, p->chunk);
+            if (!needed(off, len)) continue;
+            if (pos != off && fseeko(f, (off_t)off, SEEK_SET) != 0) { rc = err("seek in " + p->data_path); break; }
+            if (fread(staging + idx.size() * p->chunk, 1, len, f) != len) { rc = err("short read of " + p->data_path); break; }
+            pos = off + len;
+            idx.push_back(i);
         }
-        if (fread(staging, 1, len, f) != len) { rc = err("short read of " + p->data_path); break; }
-        Sha256 h;
-        h.update(staging, len);
-        if (h.hex() != p->chunk_sha256[i]) { rc = err("weight hash mismatch in chunk " + std::to_string(i)); break; }
-        while (first < p->storages.size() && p->storages[first].offset + p->storages[first].nbytes <= offset) ++first;
-        for (size_t j = first; j < p->storages.size(); ++j) {
-            const Storage& s = p->storages[j];
-            if (s.offset >= offset + len) break;
-            if (!sel[j]) continue;
-            const uint64_t lo = std::max(s.offset, offset), hi = std::min(s.offset + s.nbytes, offset + len);
-            if (hi <= lo) continue;
-            const uint8_t* src = staging + (lo - offset);
-            if (s.cuda) {
-                if ((e = hipMemcpy((uint8_t*)p->dev[j] + (lo - s.offset), src, hi - lo, hipMemcpyHostToDevice)) != hipSuccess) {
-                    rc = gfr::set_error((int)e, std::string("hipMemcpy: ") + hipGetErrorString(e));
-                    break;
+        if (rc) break;
+        std::vector<std::string> got(idx.size());
+        {
+            std::vector<std::thread> th;
+            for (size_t b = 0; b < idx.size(); ++b)
+                th.emplace_back([&, b] {
+                    const uint64_t off = idx[b] * p->chunk, len = std::min(p->file_size - off, p->chunk);
+                    Sha256 h;
+                    h.update(staging + b * p->chunk, len);
+                    got[b] = h.hex();
+                });
+            for (auto& t : th) t.join();
+        }
+        for (size_t b = 0; b < idx.size() && rc == 0; ++b) {
+            const size_t i = idx[b];
+            if (got[b] != p->chunk_sha256[i]) { rc = err("weight hash mismatch in chunk " + std::to_string(i)); break; }
+            const uint64_t offset = i * p->chunk, len = std::min(p->file_size - offset, p->chunk);
+            const uint8_t* data = staging + b * p->chunk;
+            while (first < p->storages.size() && p->storages[first].offset + p->storages[first].nbytes <= offset) ++first;
+            for (size_t j = first; j < p->storages.size(); ++j) {
+                const Storage& s = p->storages[j];
+                if (s.offset >= offset + len) break;
+                if (!sel[j]) continue;
+                const uint64_t lo = std::max(s.offset, offset), hi = std::min(s.offset + s.nbytes, offset + len);
+                if (hi <= lo) continue;
+                const uint8_t* src = data + (lo - offset);
+                if (s.cuda) {
+                    if ((e = hipMemcpy((uint8_t*)p->dev[j] + (lo - s.offset), src, hi - lo, hipMemcpyHostToDevice)) != hipSuccess) {
+                        rc = gfr::set_error((int)e, std::string("hipMemcpy: ") + hipGetErrorString(e));
+                        break;
+                    }
+                } else {
+                    memcpy(p->host[j].data() + (lo - s.offset), src, hi - lo);
                 }
-            } else {
-                memcpy(p->host[j].data() + (lo - s.offset), src, hi - lo);
             }
         }
-        offset += len;
     }
     if (f) fclose(f);
     (void)hipHostFree(staging);
