@@ -829,8 +829,10 @@ static hipError_t launch_gemm(int bits, dim3 grid, hipStream_t s, const PrefillA
 
 hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_experts* w, const uint16_t* input,
                        int input_stride, const int* picks, const int* ids, const int* count, const int* members,
-                       int rows, int maxm, bool shared_x) {
+                       int rows, int maxm, bool shared_x, const float* combine_weights, float* combine_out,
+                       bool* combined) {
     const PrefillDims& d = fx->d;
+    if (combined) *combined = false;
     if (w->bits < 2 || w->bits > 5) return hipErrorInvalidValue;
     const int P = rows * d.slots;
     const int maxu = P < w->experts ? P : w->experts;
@@ -883,6 +885,12 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
         a.sk = skd; a.z = fx->zd;
         a.x0 = fx->xd; a.x1 = fx->xd; a.t0 = w->dt; a.t1 = w->dt; a.Kin = d.inter; a.N = d.hidden;
         if ((e = launch_gemm_split<1>(w->bits, dim3(max_items * (d.hidden / 256) * skd), s, a)) != hipSuccess) return e;
+        if (combine_weights && combine_out && d.exl3_slots <= 16) {
+            // the down epilogue and the layer's slot-ordered combine in one launch (the decode path's finish)
+            if (combined) *combined = true;
+            return launch_down_finish(s, fx->zd, picks, w->svh_d, fx->out, rows, P, d.hidden, skd, d.slots,
+                                      d.exl3_slots, combine_weights, combine_out);
+        }
         return launch_down_epilogue(s, fx->zd, picks, w->svh_d, fx->out, P, d.hidden, skd, d.slots, d.exl3_slots);
     }
     // gate / up -> xd

@@ -465,10 +465,6 @@ int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const
     if (rows <= 0 || rows > m->max_rows) return fail(GFR_EINVAL, "rows %d outside 1..%d", rows, m->max_rows);
     if (!input || !logits) return fail(GFR_EINVAL, "null input");
     hipError_t e;
-    if (rows > m->decode_rows &&
-        (e = gfr::launch_route(stream, logits, rows, m->routed, m->topk, m->routed, m->picks, m->weights)) !=
-            hipSuccess)
-        return hip_fail(e, "route");
     if (rows <= m->decode_rows) {
         gfr_grouping* g = m->group_dec;
         if (rows == 1 && m->single_launch) {
@@ -503,16 +499,27 @@ int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const
         return experts_run(m->dec, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members, rows,
                            g->max_rows, m->weights, m->out);
     }
-    const float* y;
-    {
-        gfr_grouping* g = m->group_pre;
+    gfr_grouping* g = m->group_pre;
+    const size_t rg_lds = (2 * (size_t)rows * m->slots + (size_t)g->experts * ((rows + 31) / 32) + 2 * (size_t)g->experts) * 4;
+    if (rows <= gfr::GROUP_SMALL_ROWS && g->experts <= 1024 && rg_lds <= 65536) {
+        // route + group in one launch (the same router and grouping as the two launches below)
+        if ((e = gfr::launch_route_group(stream, logits, rows, m->routed, m->topk, m->picks, m->weights, g->ids,
+                                         g->count, g->members, g->max_rows)) != hipSuccess)
+            return hip_fail(e, "route + group");
+    } else {
+        if ((e = gfr::launch_route(stream, logits, rows, m->routed, m->topk, m->routed, m->picks, m->weights)) !=
+            hipSuccess)
+            return hip_fail(e, "route");
         if ((rc = gfr_grouping_run(g, stream, m->picks, rows))) return rc;
-        if ((rc = gfr_fast_experts_run(m->pre, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members,
-                                       rows, g->max_rows, 0)))
-            return rc;
-        y = gfr::prefill_output(m->pre);
     }
-    if ((e = gfr::launch_combine(stream, y, m->weights, rows, m->slots, m->hidden, m->out)) != hipSuccess)
+    // windows on the split-K programs fold the combine into their down epilogue
+    bool combined = false;
+    if ((e = gfr::prefill_run(m->pre, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members, rows,
+                              g->max_rows, false, m->weights, m->out, &combined)) != hipSuccess)
+        return hip_fail(e, "prefill run");
+    if (!combined &&
+        (e = gfr::launch_combine(stream, gfr::prefill_output(m->pre), m->weights, rows, m->slots, m->hidden, m->out)) !=
+            hipSuccess)
         return hip_fail(e, "combine");
     return 0;
 }

@@ -16,7 +16,8 @@ hipError_t prefill_create(gfr_fast_experts** out, int hidden, int inter, int slo
 PrefillDims prefill_dims(const gfr_fast_experts* fx);
 hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_experts* w, const uint16_t* input,
                        int input_stride, const int* picks, const int* ids, const int* count, const int* members,
-                       int rows, int maxm, bool shared_x);
+                       int rows, int maxm, bool shared_x, const float* combine_weights = nullptr,
+                       float* combine_out = nullptr, bool* combined = nullptr);
 float* prefill_output(const gfr_fast_experts* fx);
 uint16_t* prefill_xd(const gfr_fast_experts* fx);
 void prefill_destroy(gfr_fast_experts* fx);
