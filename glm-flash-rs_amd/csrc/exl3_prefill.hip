@@ -830,7 +830,7 @@ static hipError_t launch_gemm(int bits, dim3 grid, hipStream_t s, const PrefillA
 hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_experts* w, const uint16_t* input,
                        int input_stride, const int* picks, const int* ids, const int* count, const int* members,
                        int rows, int maxm, bool shared_x, const float* combine_weights, float* combine_out,
-                       bool* combined) {
+                       bool* combined, bool planned) {
     const PrefillDims& d = fx->d;
     if (combined) *combined = false;
     if (w->bits < 2 || w->bits > 5) return hipErrorInvalidValue;
@@ -863,9 +863,11 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
     }
     const bool split = fx->zgu && P <= PF_SPLIT_PAIRS;
     const int bm = split ? PF_SPLIT_BM : w->bits == 4 ? PF_BM4 : PF_BM;
-    prefill_plan_kernel<<<1, 1024, 0, s>>>(ids, count, members, maxm, w->experts, maxu, bm, fx->ucnt, fx->items,
-                                           fx->plan);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (!planned) {
+        prefill_plan_kernel<<<1, 1024, 0, s>>>(ids, count, members, maxm, w->experts, maxu, bm, fx->ucnt, fx->items,
+                                               fx->plan);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
     const int max_items = P / bm + maxu;
     PrefillArgs a{};
 #ifdef GFR_PF_TRACE
@@ -904,6 +906,15 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
 }
 
 float* prefill_output(const gfr_fast_experts* fx) { return fx->out; }
+int prefill_item_rows(const gfr_fast_experts* fx, int rows, int bits) {
+    const bool split = fx->zgu && rows * fx->d.slots <= PF_SPLIT_PAIRS;
+    return split ? PF_SPLIT_BM : bits == 4 ? PF_BM4 : PF_BM;
+}
+void prefill_plan_buffers(gfr_fast_experts* fx, int** ucnt, int** items, int** plan) {
+    *ucnt = fx->ucnt;
+    *items = fx->items;
+    *plan = fx->plan;
+}
 #ifdef GFR_PF_TRACE
 extern "C" uint64_t* gfr_fast_experts_trace(const gfr_fast_experts* fx) { return fx->trace; }
 #endif

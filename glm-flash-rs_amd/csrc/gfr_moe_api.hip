@@ -500,12 +500,18 @@ int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const
                            g->max_rows, m->weights, m->out);
     }
     gfr_grouping* g = m->group_pre;
+    bool planned = false;
     const size_t rg_lds = (2 * (size_t)rows * m->slots + (size_t)g->experts * ((rows + 31) / 32) + 2 * (size_t)g->experts) * 4;
     if (rows <= gfr::GROUP_SMALL_ROWS && g->experts <= 1024 && rg_lds <= 65536) {
-        // route + group in one launch (the same router and grouping as the two launches below)
+        // route + group + the prefill engine's item plan in one launch (the same router, grouping and plan as the
+        // separate launches below)
+        int *pu, *pi, *pp;
+        gfr::prefill_plan_buffers(m->pre, &pu, &pi, &pp);
         if ((e = gfr::launch_route_group(stream, logits, rows, m->routed, m->topk, m->picks, m->weights, g->ids,
-                                         g->count, g->members, g->max_rows)) != hipSuccess)
+                                         g->count, g->members, g->max_rows,
+                                         gfr::prefill_item_rows(m->pre, rows, w->bits), pu, pi, pp)) != hipSuccess)
             return hip_fail(e, "route + group");
+        planned = true;
     } else {
         if ((e = gfr::launch_route(stream, logits, rows, m->routed, m->topk, m->routed, m->picks, m->weights)) !=
             hipSuccess)
@@ -515,7 +521,7 @@ int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const
     // windows on the split-K programs fold the combine into their down epilogue
     bool combined = false;
     if ((e = gfr::prefill_run(m->pre, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members, rows,
-                              g->max_rows, false, m->weights, m->out, &combined)) != hipSuccess)
+                              g->max_rows, false, m->weights, m->out, &combined, planned)) != hipSuccess)
         return hip_fail(e, "prefill run");
     if (!combined &&
         (e = gfr::launch_combine(stream, gfr::prefill_output(m->pre), m->weights, rows, m->slots, m->hidden, m->out)) !=

@@ -47,9 +47,14 @@ __device__ __forceinline__ int first_slot(const int* __restrict__ picks, int r, 
 
 // One workgroup (blockDim.x a multiple of 64, <= 1024). lds: E * ceil(rows / 32) bitmap words + 2 E ints.
 // picks may live in LDS or global memory.
+// With `plan` (the prefill engine's item plan, bm rows an item): plan_ucnt[u] = members of used expert u,
+// plan_items[k] = (u << 16) | pass over the ceil(count / bm) passes of each u in u order, plan[0] = item count -- what
+// prefill_plan_kernel derives from the members table, here from the counts already in LDS.
 __device__ __forceinline__ void group_small_body(const int* picks, int rows, int slots, int E, int* __restrict__ ids,
                                                  int* __restrict__ count, int* __restrict__ members, int maxm,
-                                                 uint32_t* lds, int* scan_scratch) {
+                                                 uint32_t* lds, int* scan_scratch, int bm = 0,
+                                                 int* __restrict__ plan_ucnt = nullptr,
+                                                 int* __restrict__ plan_items = nullptr, int* __restrict__ plan = nullptr) {
     const int NWD = (rows + 31) >> 5;
     uint32_t* bits = lds;                                    // [E][NWD]
     int* ucnt = reinterpret_cast<int*>(lds + (size_t)E * NWD);  // [E]: count of the u-th used expert
@@ -82,6 +87,21 @@ __device__ __forceinline__ void group_small_body(const int* picks, int rows, int
     __syncthreads();
     const int used = base;
     if (threadIdx.x == 0) *count = used;
+    if (plan) {
+        int ibase = 0;
+        for (int u0 = 0; u0 < used; u0 += blockDim.x) {
+            const int u = u0 + threadIdx.x;
+            const int c = u < used ? ucnt[u] : 0, np = (c + bm - 1) / bm;
+            int total;
+            const int first = ibase + block_scan(np, scan_scratch, &total) - np;
+            if (u < used) {
+                plan_ucnt[u] = c;
+                for (int k = 0; k < np; ++k) plan_items[first + k] = (u << 16) | k;
+            }
+            ibase += total;
+        }
+        if (threadIdx.x == 0) plan[0] = ibase;
+    }
     // members: thread per (row, slot); the first slot of row r holding expert e writes code r * 32 + slot at the
     // row's rank among e's rows (the popcount of e's bitmap below bit r) -- no serial walk over an expert's rows
     for (int i = threadIdx.x; i < rows * slots; i += blockDim.x) {
@@ -120,7 +140,8 @@ __global__ void __launch_bounds__(1024) route_group_kernel(const float* __restri
                                                            int topk, int* __restrict__ picks,
                                                            float* __restrict__ weights, int* __restrict__ ids,
                                                            int* __restrict__ count, int* __restrict__ members,
-                                                           int maxm) {
+                                                           int maxm, int bm, int* __restrict__ plan_ucnt,
+                                                           int* __restrict__ plan_items, int* __restrict__ plan) {
     extern __shared__ uint32_t lds[];
     __shared__ int scan_scratch[16];
     const int slots = topk + 1, E = routed + 1;
@@ -134,7 +155,8 @@ __global__ void __launch_bounds__(1024) route_group_kernel(const float* __restri
         picks[i] = pk[i];
         weights[i] = wt[i];
     }
-    group_small_body(pk, rows, slots, E, ids, count, members, maxm, rest, scan_scratch);
+    group_small_body(pk, rows, slots, E, ids, count, members, maxm, rest, scan_scratch, bm, plan_ucnt, plan_items,
+                     plan);
 }
 
 // Large windows, launch 1: the 256 rows of this workgroup marked in an LDS bitmap [E][8], stored to
@@ -237,10 +259,12 @@ hipError_t launch_group_small(hipStream_t s, const int* picks, int rows, int slo
 }
 
 hipError_t launch_route_group(hipStream_t s, const float* logits, int rows, int routed, int topk, int* picks,
-                              float* weights, int* ids, int* count, int* members, int maxm) {
+                              float* weights, int* ids, int* count, int* members, int maxm, int bm, int* plan_ucnt,
+                              int* plan_items, int* plan) {
     const int E = routed + 1, slots = topk + 1;
     const size_t lds = (2 * (size_t)rows * slots + (size_t)E * ((rows + 31) / 32) + 2 * (size_t)E) * 4;
-    route_group_kernel<<<1, 1024, lds, s>>>(logits, rows, routed, topk, picks, weights, ids, count, members, maxm);
+    route_group_kernel<<<1, 1024, lds, s>>>(logits, rows, routed, topk, picks, weights, ids, count, members, maxm,
+                                            bm, plan_ucnt, plan_items, plan);
     return hipGetLastError();
 }
 

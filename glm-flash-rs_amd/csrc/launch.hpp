@@ -10,8 +10,10 @@ constexpr int GROUP_SMALL_ROWS = 256;
 hipError_t launch_group_small(hipStream_t s, const int* picks, int rows, int slots, int E, int* ids, int* count,
                               int* members, int maxm);
 // route (route.hpp) + group_small in one launch; rows <= GROUP_SMALL_ROWS, routed + 1 <= 1024
+// with plan != nullptr it also writes the prefill engine's item plan for bm-row items (prefill_plan_buffers)
 hipError_t launch_route_group(hipStream_t s, const float* logits, int rows, int routed, int topk, int* picks,
-                              float* weights, int* ids, int* count, int* members, int maxm);
+                              float* weights, int* ids, int* count, int* members, int maxm, int bm = 0,
+                              int* plan_ucnt = nullptr, int* plan_items = nullptr, int* plan = nullptr);
 hipError_t launch_group_large(hipStream_t s, const int* picks, int rows, int slots, int E, uint32_t* bits,
                               int* prefix, int* counts, int* ids, int* count, int* members, int maxm);
 
