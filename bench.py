@@ -296,6 +296,22 @@ def other_configs(args, copies, stream):
         del graph, pre
     del layers
     torch.cuda.empty_cache()
+
+    # ---- prepared-weight loader: config 2's 65 experts written in the reference's format, loaded with every chunk's
+    # SHA-256 checked (file -> pinned staging -> HBM)
+    import tempfile
+    with tempfile.TemporaryDirectory() as tmp:
+        chunk = 16 << 20
+        path = gfr_moe.write_prepared(tmp, [copies[0]], chunk=chunk)
+        prep = gfr_moe.Prepared(path)
+        nbytes, secs = prep.load()
+        nbytes, secs = prep.load()
+        prep.close()
+    nchunks = -(-nbytes // chunk)
+    out["loader"] = {"config": "prepared-weight load of config 2's 65 EXL3 experts (src/prepared.rs format, 16 MiB "
+                               "chunks, each SHA-256-checked, file in the page cache)",
+                     "bytes": nbytes, "seconds": round(secs, 4), "gbs": round(nbytes / secs / 1e9, 3),
+                     "hash_threads": min(16, os.cpu_count() or 1, nchunks)}
     return out
 
 

@@ -425,3 +425,47 @@ class Prepared(_Engine):
                            suh_g=v("suh_g", (E, D), torch.float16), suh_u=v("suh_u", (E, D), torch.float16),
                            suh_d=v("suh_d", (E, N), torch.float16), svh_g=v("svh_g", (E, N), torch.float16),
                            svh_u=v("svh_u", (E, N), torch.float16), svh_d=v("svh_d", (E, D), torch.float16), bits=b)
+
+
+def write_prepared(directory: str, layers, chunk: int = 64 << 20) -> str:
+    """Write expert tensors in the reference's prepared format (src/prepared.rs:15-40): manifest.json + data.bin, one
+    storage per tensor, tree weights.layers[L].moe.experts.{gt, ut, dt, suh_*, svh_*}, chunk hashes by hashlib.
+    `layers`: a list of Exl3Experts (or dicts name -> numpy array). Returns the manifest path (for Prepared)."""
+    import hashlib
+    import json
+    names = ("gt", "ut", "dt", "suh_g", "suh_u", "suh_d", "svh_g", "svh_u", "svh_d")
+    os.makedirs(directory, exist_ok=True)
+    data_path = os.path.join(directory, "data.bin")
+    storages, nodes, off = [], [], 0
+    hashes, pending = [], bytearray()
+    with open(data_path, "wb") as f:
+        for layer in layers:
+            fields = {}
+            for name in names:
+                t = layer[name] if isinstance(layer, dict) else getattr(layer, name)
+                arr = t.cpu().numpy() if isinstance(t, torch.Tensor) else t
+                blob = arr.tobytes()
+                dtype = {"int32": "int32", "float16": "float16"}[str(arr.dtype)]
+                shape = list(arr.shape)
+                stride, acc = [], 1
+                for n in reversed(shape):
+                    stride.insert(0, acc)
+                    acc *= n
+                fields[name] = {"T": len(storages), "dtype": dtype, "shape": shape, "stride": stride, "off": 0,
+                                "dev": "cuda"}
+                storages.append({"offset": off, "nbytes": len(blob), "dev": "cuda"})
+                f.write(blob)
+                off += len(blob)
+                pending += blob
+                while len(pending) >= chunk:
+                    hashes.append(hashlib.sha256(bytes(pending[:chunk])).hexdigest())
+                    del pending[:chunk]
+            nodes.append({"O": "Layer", "f": {"moe": {"O": "Moe", "f": {"experts": {"O": "Experts", "f": fields}}}}})
+    if pending:
+        hashes.append(hashlib.sha256(bytes(pending)).hexdigest())
+    manifest = {"format": 1, "file_size": off, "chunk": chunk, "chunk_sha256": hashes, "storages": storages,
+                "tree": {"O": "Weights", "f": {"layers": {"L": nodes}}}, "key": {"rank": 0, "world": 1}}
+    path = os.path.join(directory, "manifest.json")
+    with open(path, "w") as f:
+        json.dump(manifest, f)
+    return path

@@ -194,3 +194,21 @@ def test_moe_layer_from_prepared_weights(tmp_path, rows):
         outs.append(m.output.clone().cpu())
     assert torch.equal(outs[0], outs[1])
     p.close()
+
+
+def test_package_writer_round_trip(tmp_path):
+    """gfr_moe.write_prepared (the bench's writer) produces a model the loader opens, with the expert paths and bytes."""
+    rng = np.random.default_rng(9)
+    names = ("gt", "ut", "dt", "suh_g", "suh_u", "suh_d", "svh_g", "svh_u", "svh_d")
+    layers = []
+    for _ in range(2):
+        layers.append({n: rng.integers(-2 ** 31, 2 ** 31, (3, 2, 3, 24), dtype=np.int64).astype(np.int32)
+                       if n in ("gt", "ut", "dt") else rng.standard_normal((3, 32)).astype(np.float16) for n in names})
+    p = gfr_moe.Prepared(gfr_moe.write_prepared(str(tmp_path), layers, chunk=700))
+    for L, layer in enumerate(layers):
+        for n in names:
+            path = f"weights.layers[{L}].moe.experts.{n}"
+            assert p.read_tensor(path) == layer[n].tobytes()
+            t = p.tensor(path)
+            assert list(t.shape[:t.rank]) == list(layer[n].shape)
+    p.close()
