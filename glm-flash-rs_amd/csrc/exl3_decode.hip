@@ -125,6 +125,7 @@ struct GemvArgs {
     int* ids_out;
     int* count_out;
     int* members_out;
+    int x_f16;               // XSRC 1: the input rows are fp16 (the single linear) instead of bf16
 };
 
 // The 128 activations of one Hadamard block for one member, already in fp32 lanes v[0..1] = elements 2 lane + j,
@@ -269,7 +270,9 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
 #pragma unroll
             for (int m = 0; m < RB; ++m)
                 if (m < nr) {
-                    float v[2] = {bf16_to_f32((uint16_t)xv[m]) * s0, bf16_to_f32((uint16_t)(xv[m] >> 16)) * s1};
+                    const uint16_t x0 = (uint16_t)xv[m], x1 = (uint16_t)(xv[m] >> 16);
+                    float v[2] = {(a.x_f16 ? f16_to_f32(x0) : bf16_to_f32(x0)) * s0,
+                                  (a.x_f16 ? f16_to_f32(x1) : bf16_to_f32(x1)) * s1};
                     fwht128_w64(v, lane);
                     store_block<K>(&xs[wave][m][0], v, lane);
                 }
@@ -954,6 +957,32 @@ hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, const uint
     a.xd = xd; a.t0 = dt; a.t1 = dt; a.uids = uids; a.ucount = ucount; a.members = members; a.z = Zd;
     a.Kin = N; a.N = D; a.P = P; a.SK = gemv_down_splits(N); a.maxm = maxm; a.slots = slots; a.E = E;
     return gemv_bits<8, 2, 1, 2>(bits, rb_for(rows), dim3(maxu, D / 128, a.SK), s, a);
+}
+
+// One linear with its input rotation fused (XSRC 1, fp16 input): Z[split][n] partials of
+// W_q[0] over one row, SK = kin / 128 / NW splits in fixed order (gemv_linear_splits).
+static int nw_linear(int kin) { return (kin / 128) % 4 == 0 ? 4 : 2; }
+int gemv_linear_splits(int kin) { return kin / 128 / nw_linear(kin); }
+hipError_t launch_linear_fused(hipStream_t s, const uint16_t* x, const uint16_t* suh, const uint32_t* trellis,
+                               const int* uids, const int* ucount, const int* members, float* z, int kin, int n,
+                               int bits) {
+    GemvArgs a{};
+    a.x0 = x; a.x_stride = kin; a.x_f16 = 1; a.suh0 = suh; a.suh1 = suh; a.t0 = trellis; a.t1 = trellis;
+    a.uids = uids; a.ucount = ucount; a.members = members; a.z = z; a.Kin = kin; a.N = n; a.P = 1;
+    a.SK = gemv_linear_splits(kin); a.maxm = 1; a.slots = 1; a.E = 1;
+    const dim3 grid(1, n / 128, a.SK);
+    const bool four = nw_linear(kin) == 4;
+    switch (bits) {
+#define GFR_LIN(KB)                                                                                                 \
+        case KB:                                                                                                  \
+            if (four) expert_gemv_kernel<KB, 8, 4, 1, 1, 1, false><<<grid, 256, 0, s>>>(a);                         \
+            else expert_gemv_kernel<KB, 8, 2, 1, 1, 1, false><<<grid, 128, 0, s>>>(a);                              \
+            break;
+        GFR_LIN(2) GFR_LIN(3) GFR_LIN(4) GFR_LIN(5)
+#undef GFR_LIN
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_down_finish(hipStream_t s, const float* Zd, const int* pick, const uint16_t* svh_d, float* y,

@@ -91,7 +91,6 @@ struct gfr_experts {
 struct gfr_linear {
     int kin, n, bits;
     int *pick, *ids, *count, *members;
-    uint16_t* xh;
     float* z;
 };
 
@@ -244,11 +243,10 @@ int gfr_linear_create(gfr_linear** out, int kin, int n, int bits) {
     int rc = check_shape(kin, n);
     if (rc) return rc;
     if (bits < 2 || bits > 5) return fail(GFR_EINVAL, "bits %d outside 2..5", bits);
-    gfr_linear* l = new gfr_linear{kin, n, bits, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    gfr_linear* l = new gfr_linear{kin, n, bits, nullptr, nullptr, nullptr, nullptr, nullptr};
     if ((rc = alloc_zero(&l->pick, 1, "linear pick")) || (rc = alloc_zero(&l->ids, 1, "linear ids")) ||
         (rc = alloc_zero(&l->count, 1, "linear count")) || (rc = alloc_zero(&l->members, 1, "linear members")) ||
-        (rc = alloc_zero(&l->xh, (size_t)kin, "linear xh")) ||
-        (rc = alloc_zero(&l->z, (size_t)gfr::gemv_splits(kin) * n, "linear z"))) {
+        (rc = alloc_zero(&l->z, (size_t)gfr::gemv_linear_splits(kin) * n, "linear z"))) {
         gfr_linear_destroy(l);
         return rc;
     }
@@ -266,21 +264,20 @@ int gfr_linear_run(gfr_linear* l, hipStream_t stream, const uint16_t* x, const u
                    const uint16_t* svh, float* y) {
     if (!l || !x || !trellis || !suh || !svh || !y) return fail(GFR_EINVAL, "null argument");
     hipError_t e;
-    if ((e = gfr::launch_rot_in(stream, x, l->kin, true, l->pick, suh, suh, l->xh, l->xh, l->kin, 1, 1, 1, 1)) !=
-        hipSuccess)
-        return hip_fail(e, "linear rot");
-    if ((e = gfr::launch_gemv(stream, l->xh, l->xh, trellis, trellis, l->ids, l->count, l->members, l->z, l->kin, l->n,
-                              1, 1, 1, 1, l->bits, 1, 1)) != hipSuccess)
+    // two launches: the GEMV with the input rotation fused (rot_in's arithmetic, exl3.cu:224-241), then the
+    // ordered split sum, transform and output scale (down_epilogue_kernel)
+    if ((e = gfr::launch_linear_fused(stream, x, suh, trellis, l->ids, l->count, l->members, l->z, l->kin, l->n,
+                                      l->bits)) != hipSuccess)
         return hip_fail(e, "linear gemv");
-    if ((e = gfr::launch_down_epilogue(stream, l->z, l->pick, svh, y, 1, l->n, gfr::gemv_splits(l->kin), 1, 1)) !=
-        hipSuccess)
+    if ((e = gfr::launch_down_epilogue(stream, l->z, l->pick, svh, y, 1, l->n, gfr::gemv_linear_splits(l->kin), 1,
+                                       1)) != hipSuccess)
         return hip_fail(e, "linear epilogue");
     return 0;
 }
 
 int gfr_linear_destroy(gfr_linear* l) {
     if (!l) return 0;
-    free_all({l->pick, l->ids, l->count, l->members, l->xh, l->z});
+    free_all({l->pick, l->ids, l->count, l->members, l->z});
     delete l;
     return 0;
 }

@@ -51,6 +51,11 @@ hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, const uint
                               const uint16_t* suh_d, float limit, uint16_t* xd, const uint32_t* dt, const int* uids,
                               const int* ucount, const int* members, float* Zd, int N, int P, int rows, int maxm,
                               int slots, int E, int bits, int maxu);
+// one fp16 row through one linear with the input rotation fused (partials for down_epilogue)
+int gemv_linear_splits(int kin);
+hipError_t launch_linear_fused(hipStream_t s, const uint16_t* x, const uint16_t* suh, const uint32_t* trellis,
+                               const int* uids, const int* ucount, const int* members, float* z, int kin, int n,
+                               int bits);
 hipError_t launch_down_finish(hipStream_t s, const float* Zd, const int* pick, const uint16_t* svh_d, float* y,
                               int rows, int P, int D, int SK, int slots, int exl3_slots, const float* weights,
                               float* out);

@@ -91,10 +91,11 @@ def test_grouping_benchmark_shapes(gfr, oracle, E, slots, rows):
     assert np.array_equal(g.members.cpu().numpy(), mem)
 
 
-def test_linear_config1(gfr, oracle):
-    """one EXL3 linear 2048 -> 1536, K = 4, one fp16 token."""
+@pytest.mark.parametrize("kin,n,bits", [(2048, 1536, 4), (2048, 1536, 3), (768, 512, 2), (1280, 256, 5)])
+def test_linear_config1(gfr, oracle, kin, n, bits):
+    """one EXL3 linear 2048 -> 1536, K = 4, one fp16 token (and other widths / shapes: 768 and 1280
+    inputs take the two-wave form of the fused-rotation GEMV)."""
     import synth
-    kin, n, bits = 2048, 1536, 4
     t = synth.trellis((kin // 16, n // 16, 8 * bits), 11)
     suh, svh = synth.scales((kin,), 12), synth.scales((n,), 13)
     x = torch.randn(kin, generator=torch.Generator(device="cuda").manual_seed(14), device="cuda").half()
