@@ -119,6 +119,8 @@ struct GemvArgs {
     float limit;
     uint16_t* xd;            // XSRC 2: the down input, also stored (column block 0 only) [P][Kin] fp16
     const float* logits;     // ROUTE1: the token's router logits [routed]
+    const float* route_bias; // ROUTE1: the gate (route.hpp RouteGate): nullptr = softmax
+    float route_scale;
     int routed;
     int* pick_out;           // ROUTE1 outputs (program 0): picks / weights [slots], ids [slots], count, members
     float* weight_out;
@@ -170,7 +172,7 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
     if constexpr (ROUTE1) {
         int pick;
         float weight;
-        route_token_regs(a.logits, a.routed, a.slots - 1, a.routed, pick, weight);
+        route_token_regs(a.logits, a.routed, a.slots - 1, a.routed, pick, weight, RouteGate{a.route_bias, a.route_scale});
         int rank = 0;                                    // ascending order of the token's slots' experts
         for (int j = 0; j < a.slots; ++j) rank += __builtin_amdgcn_readlane(pick, j) < pick;
         const uint64_t mine = __ballot(lane < a.slots && rank == u);
@@ -653,7 +655,7 @@ __global__ void __launch_bounds__(256) moe_token_kernel(const TokenArgs a) {
 
     int pick;                                        // lane s < S: slot s's expert and weight
     float weight;
-    route_token_regs(a.logits, a.routed, S - 1, a.routed, pick, weight);
+    route_token_regs(a.logits, a.routed, S - 1, a.routed, pick, weight, RouteGate{a.route_bias, a.route_scale});
     int rank = 0;                                    // ascending order of the slots' experts
     for (int j = 0; j < S; ++j) rank += __builtin_amdgcn_readlane(pick, j) < pick;
     const uint32_t gen = ld_agent(genp);
@@ -942,6 +944,7 @@ hipError_t launch_expert_gateup(hipStream_t s, const uint16_t* x, int x_stride, 
     const int nw = nw_gateup(D), rb = rb_for(rows);
     if (route) {
         a.logits = route->logits; a.routed = route->routed; a.pick_out = route->picks; a.weight_out = route->weights;
+        a.route_bias = route->bias; a.route_scale = route->scale;
         a.ids_out = route->ids; a.count_out = route->count; a.members_out = route->members;
         return nw == 4 ? gemv_bits<8, 4, 2, 1, true>(bits, 1, grid, s, a) : gemv_bits<8, 2, 2, 1, true>(bits, 1, grid, s, a);
     }

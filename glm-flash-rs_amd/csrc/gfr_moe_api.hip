@@ -105,6 +105,8 @@ struct gfr_moe {
     gfr_fast_experts* pre;
     uint32_t* tok_sync;        // the one-launch token layer's counters / flags (nullptr: shape not supported)
     int tok_grid[6];           // its grid a bit width: min(units, resident workgroups)
+    const float* route_bias;   // the router's gate (gfr_moe_set_router): nullptr = softmax
+    float route_scale;
     int single_launch;         // rows == 1 runs the one-launch layer (default on when the shape allows)
 #ifdef GFR_TOKEN_TRACE
     uint64_t* tok_trace;
@@ -315,6 +317,17 @@ int gfr_route_topk(hipStream_t stream, const float* logits, int rows, int routed
     return 0;
 }
 
+int gfr_route_topk_biased(hipStream_t stream, const float* logits, const float* bias, float scale, int rows,
+                          int routed, int topk, int32_t* picks, float* weights) {
+    if (!logits || !bias || !picks || !weights) return fail(GFR_EINVAL, "null argument");
+    if (rows <= 0 || routed <= 0 || routed > 1024 || topk <= 0 || topk > 31 || topk > routed)
+        return fail(GFR_EINVAL, "rows %d routed %d topk %d", rows, routed, topk);
+    if (!(scale > 0.f)) return fail(GFR_EINVAL, "router scale %g must be positive", (double)scale);
+    hipError_t e = gfr::launch_route(stream, logits, rows, routed, topk, routed, picks, weights, bias, scale);
+    if (e != hipSuccess) return hip_fail(e, "route");
+    return 0;
+}
+
 // ---- debug rotation ---------------------------------------------------------------------------------------------
 int gfr_exl3_rotate(hipStream_t stream, const uint16_t* x, int x_stride, int x_f16, const int32_t* expert,
                     const uint16_t* suh, int k, int rows, uint16_t* out) {
@@ -396,6 +409,9 @@ int gfr_moe_create(gfr_moe** out, int hidden, int inter, int routed, int topk, i
     gfr_moe* m = new gfr_moe{hidden, inter, routed, topk, topk + 1, max_rows,
                              MOE_DECODE_ROWS < max_rows ? MOE_DECODE_ROWS : max_rows,
                              nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, {0}, 0};
+    m->route_bias = nullptr;   // the softmax gate until gfr_moe_set_router
+    m->route_scale = 1.f;
+    m->single_launch = 0;
     const size_t P = (size_t)max_rows * m->slots;
     if ((rc = alloc_zero(&m->weights, P, "moe weights")) || (rc = alloc_zero(&m->picks, P, "moe picks")) ||
         (rc = alloc_zero(&m->out, (size_t)max_rows * hidden, "moe output")) ||
@@ -468,7 +484,8 @@ int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const
             // one launch: route, gate/up, gate/up epilogue, down, down epilogue, combine
             gfr::TokenArgs a{};
             gfr_experts* ex = m->dec;
-            a.x = input; a.logits = logits; a.routed = m->routed; a.slots = m->slots; a.D = m->hidden;
+            a.x = input; a.logits = logits; a.route_bias = m->route_bias; a.route_scale = m->route_scale;
+            a.routed = m->routed; a.slots = m->slots; a.D = m->hidden;
             a.N = m->inter; a.E = w->experts; a.limit = 10.f;
             a.gt = w->gt; a.ut = w->ut; a.dt = w->dt;
             a.suh_g = w->suh_g; a.suh_u = w->suh_u; a.suh_d = w->suh_d;
@@ -485,13 +502,15 @@ int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const
         }
         if (rows == 1) {
             // three launches: gate/up (+ route, rotation), down (+ gate/up epilogue), down epilogue (+ combine)
-            const gfr::RouteOne r{logits, m->routed, m->picks, m->weights, g->ids, g->count, g->members};
+            const gfr::RouteOne r{logits, m->route_bias, m->route_scale, m->routed, m->picks, m->weights, g->ids,
+                                  g->count, g->members};
             return experts_run(m->dec, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members, 1,
                                g->max_rows, m->weights, m->out, &r);
         }
         // four launches: route + group, gate/up (+ rotation), down (+ gate/up epilogue), down epilogue (+ combine)
         if ((e = gfr::launch_route_group(stream, logits, rows, m->routed, m->topk, m->picks, m->weights, g->ids,
-                                         g->count, g->members, g->max_rows)) != hipSuccess)
+                                         g->count, g->members, g->max_rows, 0, nullptr, nullptr, nullptr,
+                                         m->route_bias, m->route_scale)) != hipSuccess)
             return hip_fail(e, "route + group");
         return experts_run(m->dec, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members, rows,
                            g->max_rows, m->weights, m->out);
@@ -506,12 +525,13 @@ int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const
         gfr::prefill_plan_buffers(m->pre, &pu, &pi, &pp);
         if ((e = gfr::launch_route_group(stream, logits, rows, m->routed, m->topk, m->picks, m->weights, g->ids,
                                          g->count, g->members, g->max_rows,
-                                         gfr::prefill_item_rows(m->pre, rows, w->bits), pu, pi, pp)) != hipSuccess)
+                                         gfr::prefill_item_rows(m->pre, rows, w->bits), pu, pi, pp, m->route_bias,
+                                         m->route_scale)) != hipSuccess)
             return hip_fail(e, "route + group");
         planned = true;
     } else {
-        if ((e = gfr::launch_route(stream, logits, rows, m->routed, m->topk, m->routed, m->picks, m->weights)) !=
-            hipSuccess)
+        if ((e = gfr::launch_route(stream, logits, rows, m->routed, m->topk, m->routed, m->picks, m->weights,
+                                   m->route_bias, m->route_scale)) != hipSuccess)
             return hip_fail(e, "route");
         if ((rc = gfr_grouping_run(g, stream, m->picks, rows))) return rc;
     }
@@ -524,6 +544,14 @@ int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const
         (e = gfr::launch_combine(stream, gfr::prefill_output(m->pre), m->weights, rows, m->slots, m->hidden, m->out)) !=
             hipSuccess)
         return hip_fail(e, "combine");
+    return 0;
+}
+
+int gfr_moe_set_router(gfr_moe* m, const float* bias, float scale) {
+    if (!m) return fail(GFR_EINVAL, "null moe");
+    if (bias && !(scale > 0.f)) return fail(GFR_EINVAL, "router scale %g must be positive", (double)scale);
+    m->route_bias = bias;
+    m->route_scale = bias ? scale : 1.f;
     return 0;
 }
 

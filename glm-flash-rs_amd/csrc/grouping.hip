@@ -141,7 +141,8 @@ __global__ void __launch_bounds__(1024) route_group_kernel(const float* __restri
                                                            float* __restrict__ weights, int* __restrict__ ids,
                                                            int* __restrict__ count, int* __restrict__ members,
                                                            int maxm, int bm, int* __restrict__ plan_ucnt,
-                                                           int* __restrict__ plan_items, int* __restrict__ plan) {
+                                                           int* __restrict__ plan_items, int* __restrict__ plan,
+                                                           RouteGate gate) {
     extern __shared__ uint32_t lds[];
     __shared__ int scan_scratch[16];
     const int slots = topk + 1, E = routed + 1;
@@ -149,7 +150,7 @@ __global__ void __launch_bounds__(1024) route_group_kernel(const float* __restri
     float* wt = reinterpret_cast<float*>(pk + rows * slots);   // [rows][slots]
     uint32_t* rest = reinterpret_cast<uint32_t*>(wt + rows * slots);
     for (int r = threadIdx.x >> 6; r < rows; r += blockDim.x >> 6)
-        route_token(logits + (size_t)r * routed, routed, topk, routed, pk + r * slots, wt + r * slots);
+        route_token(logits + (size_t)r * routed, routed, topk, routed, pk + r * slots, wt + r * slots, gate);
     __syncthreads();
     for (int i = threadIdx.x; i < rows * slots; i += blockDim.x) {
         picks[i] = pk[i];
@@ -260,11 +261,11 @@ hipError_t launch_group_small(hipStream_t s, const int* picks, int rows, int slo
 
 hipError_t launch_route_group(hipStream_t s, const float* logits, int rows, int routed, int topk, int* picks,
                               float* weights, int* ids, int* count, int* members, int maxm, int bm, int* plan_ucnt,
-                              int* plan_items, int* plan) {
+                              int* plan_items, int* plan, const float* bias, float scale) {
     const int E = routed + 1, slots = topk + 1;
     const size_t lds = (2 * (size_t)rows * slots + (size_t)E * ((rows + 31) / 32) + 2 * (size_t)E) * 4;
     route_group_kernel<<<1, 1024, lds, s>>>(logits, rows, routed, topk, picks, weights, ids, count, members, maxm,
-                                            bm, plan_ucnt, plan_items, plan);
+                                            bm, plan_ucnt, plan_items, plan, RouteGate{bias, scale});
     return hipGetLastError();
 }
 

@@ -13,7 +13,8 @@ hipError_t launch_group_small(hipStream_t s, const int* picks, int rows, int slo
 // with plan != nullptr it also writes the prefill engine's item plan for bm-row items (prefill_plan_buffers)
 hipError_t launch_route_group(hipStream_t s, const float* logits, int rows, int routed, int topk, int* picks,
                               float* weights, int* ids, int* count, int* members, int maxm, int bm = 0,
-                              int* plan_ucnt = nullptr, int* plan_items = nullptr, int* plan = nullptr);
+                              int* plan_ucnt = nullptr, int* plan_items = nullptr, int* plan = nullptr,
+                              const float* bias = nullptr, float scale = 1.f);
 hipError_t launch_group_large(hipStream_t s, const int* picks, int rows, int slots, int E, uint32_t* bits,
                               int* prefix, int* counts, int* ids, int* count, int* members, int maxm);
 
@@ -36,6 +37,8 @@ int gemv_down_splits(int N);    // K splits of the decode down GEMV (one 128-blo
 // weights and the window's grouping (ids, count, members with stride maxm) for the later launches.
 struct RouteOne {
     const float* logits;
+    const float* bias;        // the gate (route.hpp RouteGate): nullptr = softmax
+    float scale;
     int routed;
     int* picks;
     float* weights;
@@ -72,6 +75,8 @@ hipError_t launch_down_epilogue(hipStream_t s, const float* Z, const int* pick, 
 struct TokenArgs {
     const uint16_t* x;        // the token, bf16 [D]
     const float* logits;      // [routed]
+    const float* route_bias;  // the gate (route.hpp RouteGate): nullptr = softmax
+    float route_scale;
     int routed, slots, D, N, E;
     float limit;
     const uint32_t *gt, *ut, *dt;
@@ -99,8 +104,9 @@ int token_blocks_per_cu(int bits);   // resident 256-thread workgroups a CU (0: 
 hipError_t launch_moe_token(hipStream_t s, const TokenArgs& a, int bits);
 
 // router.hip
+// bias == nullptr: the softmax gate; else GLM's sigmoid + bias gate with weights times scale (route.hpp RouteGate)
 hipError_t launch_route(hipStream_t s, const float* logits, int rows, int E, int topk, int shared_id, int* picks,
-                        float* weights);
+                        float* weights, const float* bias = nullptr, float scale = 1.f);
 hipError_t launch_combine(hipStream_t s, const float* y, const float* weights, int rows, int slots, int D,
                           float* out);
 

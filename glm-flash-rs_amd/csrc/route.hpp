@@ -10,18 +10,28 @@ namespace gfr {
 
 constexpr int ROUTE_MAX_E = 64 * 16;
 
+// The router's gate. bias == nullptr: the benchmark's softmax gate (top-k by logit, softmax over the picks).
+// Otherwise GLM's gate, the arguments of the reference's `topk` call (moe.rs:89-99: logits, bias, picks, weights,
+// 2.5), with the published DeepSeek-V3 / GLM-4.5 "noaux" gating: scores = sigmoid(logit); selection by
+// score + bias[e]; weights = score / (sum of the k picked scores + 1e-20) * scale.
+struct RouteGate {
+    const float* bias;
+    float scale;
+};
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
+
 // One wave (64 lanes) routes one token into registers: lane s < topk holds the s-th pick and its weight, lane topk
 // the shared expert (weight 1). Lane l holds logits l, l + 64, ... (PER of them); k rounds of a wave-wide max (DPP /
 // permlane, no LDS) whose winner is the lowest id holding it (a ballot per register, lowest set lane).
 template <int PER>
 __device__ __forceinline__ void route_token_per(const float* __restrict__ l, int E, int topk, int shared_id,
-                                                int& pick, float& weight) {
+                                                int& pick, float& weight, RouteGate g) {
     const int lane = threadIdx.x & 63;
     float v[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
         const int e = j * 64 + lane;
-        v[j] = e < E ? l[e] : -__builtin_inff();
+        v[j] = e < E ? (g.bias ? sigmoidf_(l[e]) + g.bias[e] : l[e]) : -__builtin_inff();
     }
     float my_v = 0.f;                                  // lane s < topk: the s-th pick's logit and id
     int my_e = 0;
@@ -46,28 +56,36 @@ __device__ __forceinline__ void route_token_per(const float* __restrict__ l, int
             my_e = be;
         }
     }
+    pick = lane < topk ? my_e : shared_id;
+    if (g.bias) {
+        // the picked experts' unbiased scores, normalised over the picks in slot order, times the scale
+        const float sc = lane < topk ? sigmoidf_(l[my_e]) : 0.f;
+        float sum = 0.f;
+        for (int s = 0; s < topk; ++s) sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), s));
+        weight = lane < topk ? sc / (sum + 1e-20f) * g.scale : 1.f;
+        return;
+    }
     const float top = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_v), 0));
     const float ex = lane < topk ? expf(my_v - top) : 0.f;
     float sum = 0.f;
     for (int s = 0; s < topk; ++s) sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), s));
-    pick = lane < topk ? my_e : shared_id;
     weight = lane < topk ? ex / sum : 1.f;
 }
 
 __device__ __forceinline__ void route_token_regs(const float* __restrict__ l, int E, int topk, int shared_id,
-                                                 int& pick, float& weight) {
-    if (E <= 64) route_token_per<1>(l, E, topk, shared_id, pick, weight);
-    else if (E <= 128) route_token_per<2>(l, E, topk, shared_id, pick, weight);
-    else if (E <= 256) route_token_per<4>(l, E, topk, shared_id, pick, weight);
-    else route_token_per<ROUTE_MAX_E / 64>(l, E, topk, shared_id, pick, weight);
+                                                 int& pick, float& weight, RouteGate g = {nullptr, 1.f}) {
+    if (E <= 64) route_token_per<1>(l, E, topk, shared_id, pick, weight, g);
+    else if (E <= 128) route_token_per<2>(l, E, topk, shared_id, pick, weight, g);
+    else if (E <= 256) route_token_per<4>(l, E, topk, shared_id, pick, weight, g);
+    else route_token_per<ROUTE_MAX_E / 64>(l, E, topk, shared_id, pick, weight, g);
 }
 
 // One wave routes one token; pk / wt (LDS or global) receive topk + 1 entries.
 __device__ __forceinline__ void route_token(const float* __restrict__ l, int E, int topk, int shared_id, int* pk,
-                                            float* wt) {
+                                            float* wt, RouteGate g = {nullptr, 1.f}) {
     int pick;
     float weight;
-    route_token_regs(l, E, topk, shared_id, pick, weight);
+    route_token_regs(l, E, topk, shared_id, pick, weight, g);
     const int lane = threadIdx.x & 63;
     if (lane <= topk) {
         pk[lane] = pick;

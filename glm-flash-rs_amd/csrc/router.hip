@@ -1,7 +1,8 @@
 // Router and combine around the expert path (the reference runs them as precompiled Triton kernels `topk` and
-// `combine`, glm-flash-rs src/moe.rs:89-100,171-181, whose source is not in its repository). Semantics here are the
-// benchmark's: softmax over the routed experts' logits, top-k by logit (ties: lower id), weights renormalised over
-// the k picks, the shared expert appended as the last slot with weight 1; combine = the slot-ordered weighted sum.
+// `combine`, glm-flash-rs src/moe.rs:89-100,171-181, whose source is not in its repository). Two gates (route.hpp):
+// the benchmark's softmax (top-k by logit, ties: lower id, weights renormalised over the k picks) and GLM's
+// sigmoid + bias selection with scaled renormalised weights; the shared expert is appended as the last slot with
+// weight 1; combine = the slot-ordered weighted sum.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -10,9 +11,10 @@
 namespace gfr {
 
 __global__ void __launch_bounds__(64) route_kernel(const float* __restrict__ logits, int E, int topk, int shared_id,
-                                                   int* __restrict__ picks, float* __restrict__ weights) {
+                                                   int* __restrict__ picks, float* __restrict__ weights, RouteGate g) {
     const int r = blockIdx.x, slots = topk + 1;
-    route_token(logits + (size_t)r * E, E, topk, shared_id, picks + (size_t)r * slots, weights + (size_t)r * slots);
+    route_token(logits + (size_t)r * E, E, topk, shared_id, picks + (size_t)r * slots, weights + (size_t)r * slots,
+                g);
 }
 
 // out[r][n] = sum over slots s (in order) of weights[r][s] * y[r * slots + s][n]; four columns a thread (16-byte
@@ -47,8 +49,8 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
 namespace gfr {
 
 hipError_t launch_route(hipStream_t s, const float* logits, int rows, int E, int topk, int shared_id, int* picks,
-                        float* weights) {
-    route_kernel<<<rows, 64, 0, s>>>(logits, E, topk, shared_id, picks, weights);
+                        float* weights, const float* bias, float scale) {
+    route_kernel<<<rows, 64, 0, s>>>(logits, E, topk, shared_id, picks, weights, RouteGate{bias, scale});
     return hipGetLastError();
 }
 

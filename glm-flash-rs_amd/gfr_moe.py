@@ -66,6 +66,8 @@ def _load() -> ctypes.CDLL:
         "gfr_exl3_gemv_splits": ([I], I),
         "gfr_exl3_rotate": ([P, P, I, I, P, P, I, I, P], I),
         "gfr_route_topk": ([P, P, I, I, I, P, P], I),
+        "gfr_route_topk_biased": ([P, P, P, ctypes.c_float, I, I, I, P, P], I),
+        "gfr_moe_set_router": ([VP, P, ctypes.c_float], I),
         "gfr_exl3_grouped_gemv": ([P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I], I),
         "gfr_prepared_open": ([ctypes.POINTER(VP), ctypes.c_char_p], I),
         "gfr_prepared_tensor_count": ([VP], I),
@@ -269,7 +271,8 @@ class FastExperts(_Engine):
 
 
 class Moe(_Engine):
-    """Moe::run_prefetched (moe.rs:66-182) for the benchmark's router: softmax top-k + EXL3 shared expert."""
+    """Moe::run_prefetched (moe.rs:66-182): router (the benchmark's softmax top-k, or GLM's sigmoid + bias gate via
+    set_router) -> grouping -> EXL3 experts (routed + shared) -> combine."""
 
     _destroy = "gfr_moe_destroy"
 
@@ -284,6 +287,12 @@ class Moe(_Engine):
 
     def set_decode_rows(self, n: int):
         _check(lib().gfr_moe_set_decode_rows(self._h, n))
+
+    def set_router(self, bias: torch.Tensor = None, scale: float = 2.5):
+        """GLM's gate (the reference's topk(logits, bias, picks, weights, 2.5), moe.rs:89-99) with this fp32 bias
+        [routed]; None: back to the softmax gate. The tensor must outlive the runs."""
+        self._router_bias = bias
+        _check(lib().gfr_moe_set_router(self._h, _ptr(bias), float(scale) if bias is not None else 1.0))
 
     def set_single_launch(self, enable: bool):
         """rows == 1 as one persistent launch (default where the shape allows) or as three launches."""
@@ -317,6 +326,16 @@ def route(logits: torch.Tensor, topk: int, stream=None):
     picks = torch.empty((rows, topk + 1), dtype=torch.int32, device=logits.device)
     weights = torch.empty((rows, topk + 1), dtype=torch.float32, device=logits.device)
     _check(lib().gfr_route_topk(_stream(stream), _ptr(logits), rows, routed, topk, _ptr(picks), _ptr(weights)))
+    return picks, weights
+
+
+def route_biased(logits: torch.Tensor, bias: torch.Tensor, topk: int, scale: float = 2.5, stream=None):
+    """GLM's gate alone (gfr_route_topk_biased): (picks, weights) [rows, topk + 1], shared id = routed."""
+    rows, routed = logits.shape
+    picks = torch.empty((rows, topk + 1), dtype=torch.int32, device=logits.device)
+    weights = torch.empty((rows, topk + 1), dtype=torch.float32, device=logits.device)
+    _check(lib().gfr_route_topk_biased(_stream(stream), _ptr(logits), _ptr(bias), float(scale), rows, routed, topk,
+                                       _ptr(picks), _ptr(weights)))
     return picks, weights
 
 

@@ -113,6 +113,9 @@ int gfr_moe_set_decode_rows(gfr_moe* m, int decode_rows);  /* rows at or below r
 /* rows == 1 as one persistent launch (route .. combine; default on when hidden % 512 == 0 and inter % 256 == 0) or
  * as three launches (gate/up + route, down + gate/up epilogue, down epilogue + combine); both give the same bits.
  * No counterpart in the reference, whose decode layer is a captured graph of separate launches (model.rs:634). */
+/* The layer's router gate: bias == NULL (default) the softmax gate of gfr_route_topk; else GLM's gate of
+ * gfr_route_topk_biased with this bias [routed] (device, fp32; must outlive the runs) and scale (2.5 for GLM). */
+int gfr_moe_set_router(gfr_moe* m, const float* bias, float scale);
 int gfr_moe_set_single_launch(gfr_moe* m, int enable);
 /* Synchronous check of the one-launch layer's error word: GFR_ESTALL if a launch ever waited past its bound
  * for an activation block (results of that launch are invalid), else 0. */
@@ -122,6 +125,12 @@ int gfr_moe_destroy(gfr_moe* m);
 /* ---- The router alone (the reference's Triton topk, moe.rs:89-100; source absent, semantics of the benchmark):
  * logits [rows][routed] fp32 -> picks / weights [rows][topk + 1]: top-k by logit (ties: lower id), weights the
  * softmax over the k picks (summed in slot order), then the shared expert id `routed` with weight 1. */
+/* GLM's gate, the arguments of the reference's `topk` call (moe.rs:89-99: logits, bias, picks, weights, 2.5), with
+ * the published DeepSeek-V3 / GLM-4.5 "noaux" gating (its Triton source is not in the reference): score =
+ * sigmoid(logit); top-k by score + bias[e] (ties: lower id); weight = score / (sum of the picked scores + 1e-20) *
+ * scale, summed in slot order; shared expert last with weight 1. bias [routed] fp32. */
+int gfr_route_topk_biased(hipStream_t stream, const float* logits, const float* bias, float scale, int rows,
+                          int routed, int topk, int32_t* picks, float* weights);
 int gfr_route_topk(hipStream_t stream, const float* logits, int rows, int routed, int topk, int32_t* picks,
                    float* weights);
 

@@ -274,6 +274,41 @@ void gfro_route(const float* logits, int rows, int E, int topk, int shared_id, i
     free(used);
 }
 
+/* GLM's gate for the reference's `topk` call (moe.rs:89-99: logits, bias, picks, weights, 2.5; its Triton source is
+ * absent): the published DeepSeek-V3 / GLM-4.5 "noaux" gating. score = sigmoid(logit) in float; top-k by
+ * score + bias (ties: lower id); weight = score / (sum of the picked scores in slot order + 1e-20) * scale; the shared
+ * expert last with weight 1. PARITY UNPINNED against the reference (binary-only kernel). */
+void gfro_route_biased(const float* logits, const float* bias, float scale, int rows, int E, int topk, int shared_id,
+                       int32_t* picks, float* weights) {
+    const int slots = topk + 1;
+    char* used = (char*)malloc((size_t)E);
+    float* sc = (float*)malloc((size_t)E * sizeof(float));
+    float* ch = (float*)malloc((size_t)E * sizeof(float));
+    for (int r = 0; r < rows; ++r) {
+        const float* l = logits + (size_t)r * E;
+        for (int e = 0; e < E; ++e) {
+            sc[e] = 1.f / (1.f + expf(-l[e]));
+            ch[e] = sc[e] + bias[e];
+        }
+        memset(used, 0, (size_t)E);
+        for (int s = 0; s < topk; ++s) {
+            int best = -1;
+            for (int e = 0; e < E; ++e)
+                if (!used[e] && (best < 0 || ch[e] > ch[best])) best = e;
+            used[best] = 1;
+            picks[r * slots + s] = best;
+        }
+        float sum = 0.f;
+        for (int s = 0; s < topk; ++s) sum += sc[picks[r * slots + s]];
+        for (int s = 0; s < topk; ++s) weights[r * slots + s] = sc[picks[r * slots + s]] / (sum + 1e-20f) * scale;
+        picks[r * slots + topk] = shared_id;
+        weights[r * slots + topk] = 1.f;
+    }
+    free(used);
+    free(sc);
+    free(ch);
+}
+
 void gfro_combine(const float* y, const float* weights, int rows, int slots, int D, float* out) {
     for (int r = 0; r < rows; ++r)
         for (int n = 0; n < D; ++n) {

@@ -67,6 +67,8 @@ int gfro_group(const int32_t* picks, int rows, int slots, int E, int maxm, int32
  * absent): picks[r][0..topk) by descending logit (ties: lower id), picks[r][topk] = shared_id, weights the
  * renormalised softmax of the picked logits, weight 1 for the shared slot. */
 void gfro_route(const float* logits, int rows, int E, int topk, int shared_id, int32_t* picks, float* weights);
+void gfro_route_biased(const float* logits, const float* bias, float scale, int rows, int E, int topk, int shared_id,
+                       int32_t* picks, float* weights);
 /* out[r][n] = sum over slots in order of weights[r][s] * y[r*slots+s][n] */
 void gfro_combine(const float* y, const float* weights, int rows, int slots, int D, float* out);
 

@@ -36,6 +36,7 @@ def _load():
         "gfro_expert_row": ([P, I, I, P, P, P, P, P, P, P, P, P, I, I, I, F, P, P], None),
         "gfro_linear": ([P, I, I, P, P, P, P], None),
         "gfro_group": ([P, I, I, I, I, P, P, P], I), "gfro_route": ([P, I, I, I, I, P, P], None),
+        "gfro_route_biased": ([P, P, ctypes.c_float, I, I, I, I, P, P], None),
         "gfro_combine": ([P, P, I, I, I, P], None),
         "gfro_baseline_decode": ([P, I, I, I, I, P, P, P, P, P, P, P, P, P, P, P], ctypes.c_double),
     }
@@ -142,6 +143,16 @@ def route(logits, topk, shared_id):
     picks = np.empty((rows, topk + 1), np.int32)
     weights = np.empty((rows, topk + 1), np.float32)
     lib().gfro_route(_p(l), rows, E, topk, shared_id, _p(picks), _p(weights))
+    return picks, weights
+
+
+def route_biased(logits, bias, scale, topk, shared_id):
+    l = np.ascontiguousarray(logits, np.float32)
+    b = np.ascontiguousarray(bias, np.float32)
+    rows, E = l.shape
+    picks = np.empty((rows, topk + 1), np.int32)
+    weights = np.empty((rows, topk + 1), np.float32)
+    lib().gfro_route_biased(_p(l), _p(b), scale, rows, E, topk, shared_id, _p(picks), _p(weights))
     return picks, weights
 
 

@@ -390,3 +390,65 @@ def test_moe_layer_config5_decode_vs_oracle(gfr, oracle, bits):
     xb = np_u16(x)
     ys = np.stack([dec.row(xb[0], int(e))[0] for e in p[0]])
     assert_close(m.output.cpu().numpy(), oracle.combine(ys, wt, 1, topk + 1), what=f"config 5 K={bits}")
+
+
+def _biased_inputs(rows, E, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    logits = torch.randn(rows, E, generator=g, device="cuda")
+    bias = torch.randn(E, generator=g, device="cuda") * 0.05
+    return logits, bias
+
+
+def _check_biased(oracle, picks, weights, logits, bias, topk, E):
+    """GPU picks / weights of GLM's gate against the oracle; a near-tie at the k-th place may go either way."""
+    p, wt = oracle.route_biased(logits.cpu().numpy(), bias.cpu().numpy(), 2.5, topk, E)
+    gp, gw = picks.cpu().numpy(), weights.cpu().numpy()
+    s = 1.0 / (1.0 + np.exp(-logits.cpu().numpy().astype(np.float64)))
+    choice = s + bias.cpu().numpy()
+    for r in range(p.shape[0]):
+        srt = np.sort(choice[r])[::-1]
+        if srt[topk - 1] - srt[topk] > 1e-5:
+            assert list(gp[r]) == list(p[r]), r
+            np.testing.assert_allclose(gw[r], wt[r], rtol=2e-6)
+        else:   # the picks are a valid top-k of the biased scores
+            assert set(gp[r, :topk]) <= set(np.argsort(-choice[r])[:topk + 1])
+    return p, wt
+
+
+@pytest.mark.parametrize("rows,E,topk", [(64, 64, 4), (33, 160, 8), (17, 288, 8)])
+def test_route_biased_vs_oracle(gfr, oracle, rows, E, topk):
+    """GLM's gate (the reference's topk(logits, bias, .., 2.5) call, moe.rs:89-99) at the benchmark's and the
+    reference's (288 routed, top-8) shapes."""
+    logits, bias = _biased_inputs(rows, E, 70 + E)
+    picks, weights = gfr.route_biased(logits, bias, topk, 2.5)
+    torch.cuda.synchronize()
+    _check_biased(oracle, picks, weights, logits, bias, topk, E)
+
+
+@pytest.mark.parametrize("rows,single", [(1, False), (1, True), (3, False), (32, False)])
+def test_moe_layer_biased_router_vs_oracle(gfr, oracle, rows, single):
+    """A Moe layer with GLM's gate on every routing path: the router fused into the bs = 1 gate/up GEMV, the one-launch
+    layer, the decode window's route + group launch and the split-K window's route + group + plan launch."""
+    E, D, N, bits, topk = 64, 2048, 1536, 4, 4
+    w, x, _ = _moe_inputs(E, D, N, bits, rows, topk, 90 + rows)
+    logits, bias = _biased_inputs(rows, E, 95 + rows)
+    m = gfr.Moe(D, N, E, topk, rows)
+    m.set_router(bias, 2.5)
+    if rows == 1:
+        m.set_single_launch(single)
+    m.run(w, x, logits, rows)
+    torch.cuda.synchronize()
+    p, wt = _check_biased(oracle, m.picks[:rows], m.weights[:rows], logits, bias, topk, E)
+    dec = DecodedExperts(oracle, w)
+    xb = np_u16(x)
+    out = m.output.cpu().numpy()
+    gp, gw = m.picks[:rows].cpu().numpy(), m.weights[:rows].cpu().numpy()
+    for r in (range(rows) if rows <= 3 else (0, rows - 1)):
+        ys = np.stack([dec.row(xb[r], int(e))[0] for e in gp[r]])
+        want = oracle.combine(ys, gw[r:r + 1], 1, topk + 1)
+        assert_close(out[r], want[0], what=f"token {r}")
+    m.set_router(None)
+    m.run(w, x, logits, rows)
+    torch.cuda.synchronize()
+    p2, _ = oracle.route(logits.cpu().numpy(), topk, E)
+    assert np.array_equal(m.picks[:rows].cpu().numpy(), p2)

@@ -257,6 +257,32 @@ def test_route(oracle):
         assert w[r, 4] == 1.0
 
 
+def _biased_reference(logits, bias, k, scale):
+    """An independent numpy restatement of the published GLM / DeepSeek-V3 gate."""
+    s = (1.0 / (1.0 + np.exp(-logits.astype(np.float32)))).astype(np.float32)
+    choice = (s + bias.astype(np.float32)).astype(np.float32)
+    order = np.argsort(-choice, kind="stable")
+    pk = order[:k]
+    w = s[pk] / (s[pk].sum(dtype=np.float32) + np.float32(1e-20)) * np.float32(scale)
+    gap = choice[order[k - 1]] - choice[order[k]] if k < len(order) else np.inf
+    return pk, w, gap
+
+
+@pytest.mark.parametrize("E,k", [(64, 4), (160, 8), (288, 8)])
+def test_route_biased(oracle, E, k):
+    rng = np.random.default_rng(E + k)
+    logits = rng.standard_normal((40, E)).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.05).astype(np.float32)
+    picks, w = oracle.route_biased(logits, bias, 2.5, k, E)
+    for r in range(40):
+        pk, wr, gap = _biased_reference(logits[r], bias, k, 2.5)
+        if gap > 1e-6:                      # a near-tie at the k-th place may round either way
+            assert list(picks[r, :k]) == list(pk)
+            np.testing.assert_allclose(w[r, :k], wr, rtol=1e-6)
+        assert picks[r, k] == E and w[r, k] == 1.0
+        np.testing.assert_allclose(w[r, :k].sum(), 2.5, rtol=1e-6)
+
+
 def _swiglu_limited(g, u, limit=10.0):
     g = np.minimum(g, limit)
     u = np.clip(u, -limit, limit)
