@@ -919,6 +919,7 @@ void prefill_plan_buffers(gfr_fast_experts* fx, int** ucnt, int** items, int** p
 extern "C" uint64_t* gfr_fast_experts_trace(const gfr_fast_experts* fx) { return fx->trace; }
 #endif
 uint16_t* prefill_xd(const gfr_fast_experts* fx) { return fx->xd; }
+uint16_t* prefill_rotated(const gfr_fast_experts* fx, int mat) { return mat ? fx->xu : fx->xg; }
 
 void prefill_destroy(gfr_fast_experts* fx) {
     if (!fx) return;

@@ -387,6 +387,9 @@ int gfr_fast_experts_run(gfr_fast_experts* fx, hipStream_t stream, const gfr_exl
 
 float* gfr_fast_experts_output(const gfr_fast_experts* fx) { return fx ? gfr::prefill_output(fx) : nullptr; }
 uint16_t* gfr_fast_experts_xd(const gfr_fast_experts* fx) { return fx ? gfr::prefill_xd(fx) : nullptr; }
+uint16_t* gfr_fast_experts_rotated(const gfr_fast_experts* fx, int mat) {
+    return fx && (mat == 0 || mat == 1) ? gfr::prefill_rotated(fx, mat) : nullptr;
+}
 int gfr_fast_experts_destroy(gfr_fast_experts* fx) {
     gfr::prefill_destroy(fx);
     return 0;

@@ -24,6 +24,7 @@ int prefill_item_rows(const gfr_fast_experts* fx, int rows, int bits);
 void prefill_plan_buffers(gfr_fast_experts* fx, int** ucnt, int** items, int** plan);
 float* prefill_output(const gfr_fast_experts* fx);
 uint16_t* prefill_xd(const gfr_fast_experts* fx);
+uint16_t* prefill_rotated(const gfr_fast_experts* fx, int mat);
 void prefill_destroy(gfr_fast_experts* fx);
 
 }  // namespace gfr

@@ -50,6 +50,7 @@ def _load() -> ctypes.CDLL:
         "gfr_fast_experts_run": ([VP, P, P, P, I, P, P, P, P, I, I, I], I),
         "gfr_fast_experts_output": ([VP], P),
         "gfr_fast_experts_xd": ([VP], P),
+        "gfr_fast_experts_rotated": ([VP, I], P),
         "gfr_fast_experts_destroy": ([VP], I),
         "gfr_moe_create": ([ctypes.POINTER(VP), I, I, I, I, I], I),
         "gfr_moe_run": ([VP, P, P, P, P, I], I),
@@ -261,6 +262,9 @@ class FastExperts(_Engine):
         P = max_rows * slots
         self.output = _view(lib().gfr_fast_experts_output(self._h), (P, hidden), torch.float32, device)
         self.xd = _view(lib().gfr_fast_experts_xd(self._h), (P, inter), torch.float16, device)
+        # parity probe: the rotated input rows of the last run, k tiles in pair order (see gfr_fast_experts_rotated)
+        self.rotated = [_view(lib().gfr_fast_experts_rotated(self._h, m), (P, hidden), torch.float16, device)
+                        for m in (0, 1)]
 
     def run(self, w: Exl3Experts, input, picks, ids, count, members, rows: int, maxm: int, shared_x: bool,
             stream=None):

@@ -96,6 +96,10 @@ int gfr_fast_experts_run(gfr_fast_experts* fx, hipStream_t stream, const gfr_exl
                          const int32_t* members, int rows, int maxm, int shared_x);  /* FastExperts::run :91-208 */
 float* gfr_fast_experts_output(const gfr_fast_experts* fx);
 uint16_t* gfr_fast_experts_xd(const gfr_fast_experts* fx);
+/* Parity probe, no reference counterpart (the reference keeps rot_in's output internal, exl3.cu:224-241): the rotated
+ * input rows of the last run, [rows * slots][hidden] fp16, matrix 0 (gate, or both when shared_x) or 1 (up); each
+ * 16-value k tile stored in pair order: u16 2m holds x[m + 8], 2m + 1 holds x[m] (m = 0..7). Null for mat not 0 or 1. */
+uint16_t* gfr_fast_experts_rotated(const gfr_fast_experts* fx, int mat);
 int gfr_fast_experts_destroy(gfr_fast_experts* fx);
 
 /* ---- One MoE layer (Moe::run_prefetched, moe.rs:66-182) ------------------------------------------------------

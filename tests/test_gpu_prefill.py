@@ -164,3 +164,44 @@ def test_moe_prefill_config5_chunk(gfr, oracle):
         ys = np.stack([dec.row(xb[r], int(e), sk_gu=1, sk_d=1, warps=1)[0] for e in p[r]])
         want = oracle.combine(ys, wt[r:r + 1], 1, topk + 1)
         assert_close(out[r], want[0], what=f"config 5 token {r}")
+
+
+def _unpair(rows_u16):
+    """Pair order of the prefill B operand (pair m of a 16-value k tile = (x[m + 8] low, x[m] high)) -> natural."""
+    t = rows_u16.reshape(rows_u16.shape[0], -1, 8, 2)
+    return np.concatenate([t[:, :, :, 1], t[:, :, :, 0]], axis=2).reshape(rows_u16.shape)
+
+
+@pytest.mark.parametrize("hidden,slots,rows,shared_x", [
+    (2048, 5, 37, False),     # the config 2-4 shape: 10 (slot, matrix) rows, up to 16 a launch form
+    (1280, 5, 1, True),       # shared rotation: 5 rows
+    (5120, 9, 13, False),     # config 5: 18 rows, up to 32
+    (1280, 17, 3, False),     # 34 rows, up to 64
+])
+def test_prefill_rotation_bitexact(gfr, oracle, hidden, slots, rows, shared_x):
+    """The prefill input rotation (prefill_rot_kernel) is rot_in (exl3.cu:224-241) bit for bit, for every pair and
+    both matrices, at every (slot, matrix) row count the launch distinguishes."""
+    import synth
+    import dataclasses
+    E = slots + 3
+    w = synth.experts(E, hidden, 256, 2, seed=hidden + slots)
+    if shared_x:
+        w = dataclasses.replace(w, suh_u=w.suh_g)
+    rng = np.random.default_rng(slots)
+    picks_np = np.stack([rng.permutation(E)[:slots] for _ in range(rows)]).astype(np.int32)
+    picks = torch.from_numpy(picks_np).cuda()
+    x = synth.activations(rows, hidden, slots + 1)
+    g = gfr.Grouping(E, slots, rows)
+    g.run(picks, rows)
+    fx = gfr.FastExperts(hidden, 256, slots, slots, E, rows)
+    fx.run(w, x, picks, g.ids, g.count, g.members, rows, rows, shared_x=shared_x)
+    torch.cuda.synchronize()
+    xs = np_u16(x)
+    for m in ((0,) if shared_x else (0, 1)):
+        got = _unpair(np_u16(fx.rotated[m][:rows * slots]))
+        suh = np_u16(w.suh_u if m else w.suh_g)
+        for r in range(rows):
+            for s in range(slots):
+                want = oracle.rot(xs[r], suh[picks_np[r, s]])
+                assert np.array_equal(got[r * slots + s], want), \
+                    f"matrix {m} row {r} slot {s}: {np.sum(got[r * slots + s] != want)} values differ"
