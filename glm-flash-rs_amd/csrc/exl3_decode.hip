@@ -85,18 +85,6 @@ __global__ void __launch_bounds__(64) rot_in_kernel(const uint16_t* __restrict__
     *reinterpret_cast<uint32_t*>(o) = packed;
 }
 
-// Position of tile row r (0..15) in the packed pair order of pair_row: pair m, low half (2m) or high half (2m + 1).
-__host__ __device__ constexpr int pair_pos(int K, int r) {
-    if (K == 2) {
-        const int lo = (r & 3) >= 2;                       // rows r + 2 of a pair sit in the low half
-        const int base = lo ? r - 2 : r;                   // the pair's r = 4v + (u & 1) + 8 (u >> 1)
-        const int m = 4 * ((base >> 2) & 1) + (base & 1) + 2 * (base >> 3);
-        return 2 * m + (lo ? 0 : 1);
-    }
-    const int lo = r >= 8;                                 // rows 2l + 8 + h in the low half
-    const int base = lo ? r - 8 : r;                       // 2l + h
-    return 2 * base + (lo ? 0 : 1);
-}
 
 // Arguments of the decode GEMV (one struct in the kernarg segment).
 struct GemvArgs {
@@ -128,22 +116,34 @@ struct GemvArgs {
     int* count_out;
     int* members_out;
     int x_f16;               // XSRC 1: the input rows are fp16 (the single linear) instead of bf16
+    int ucap;                // programs x = chunk * ucap + u: distinct-expert slots of the grid (RB members a chunk)
 };
 
 // The 128 activations of one Hadamard block for one member, already in fp32 lanes v[0..1] = elements 2 lane + j,
-// rounded to fp16 and stored into the wave's pair-ordered LDS slots of k tiles kk0 .. kk0 + 7.
-template <int K>
-__device__ __forceinline__ void store_block(uint16_t* slots16, const float (&v)[2], int lane) {
-    const int kk = (2 * lane) >> 4, r = (2 * lane) & 15;
-    slots16[kk * 16 + pair_pos(K, r)] = f16_of_product(v[0], HAD_SCALE);
-    slots16[kk * 16 + pair_pos(K, r + 1)] = f16_of_product(v[1], HAD_SCALE);
+// rounded to fp16 and staged twice in a word, (x, x), into the wave's LDS slots (tile row order) of k tiles kk0 ..
+// kk0 + 7: the operand tile_dot takes.
+__device__ __forceinline__ void store_block(uint32_t* slots, const float (&v)[2], int lane) {
+    const uint32_t h0 = f16_of_product(v[0], HAD_SCALE), h1 = f16_of_product(v[1], HAD_SCALE);
+    *reinterpret_cast<uint2*>(slots + 2 * lane) = make_uint2(h0 | h0 << 16, h1 | h1 << 16);
+}
+// One k tile's 16 staged activations (rows 0..15, each twice) into registers.
+__device__ __forceinline__ void load_tile_acts(const uint32_t* tile, uint32_t (&xd)[16]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint4 v = reinterpret_cast<const uint4*>(tile)[q];
+        xd[4 * q] = v.x;
+        xd[4 * q + 1] = v.y;
+        xd[4 * q + 2] = v.z;
+        xd[4 * q + 3] = v.w;
+    }
 }
 
-// Grouped trellis GEMV of the decode path. Program (distinct expert u, 128-column block cb, mat * SK + split): the
-// members of expert uids[u] (RB rows at a time) times W_q[mat] over k tiles [split * NW KTW, (split + 1) * NW KTW)
-// for the block's 128 columns; wave w owns k tiles split * NW KTW + w KTW + [0, KTW), ascending, one v_dot2_f32_f16
-// chain a column; the waves are added in order through LDS into Z[mat][split][pair][n] (every sum has a fixed order,
-// so a row's result never depends on the other rows or on RB).
+// Grouped trellis GEMV of the decode path. Program (chunk * ucap + distinct expert u, 128-column block cb, mat * SK +
+// split): members [chunk RB, chunk RB + RB) of expert uids[u] times W_q[mat] over k tiles [split * NW KTW,
+// (split + 1) * NW KTW) for the block's 128 columns; wave w owns k tiles split * NW KTW + w KTW + [0, KTW),
+// ascending, one v_dot2_f32_f16 chain a column (codeword halves against the activation, exl3_format.hpp lane_words /
+// tile_dot); the waves are added in order through LDS into Z[mat][split][pair][n] (every sum has a fixed order, so a
+// row's result never depends on the other rows or on RB).
 //   Prologue: the window's count, the expert id and the member codes in one round trip (ROUTE1: computed here
 //   instead), then the activation loads, then the trellis words, so that the activations are built while the
 //   trellis streams in. Activation sources (each bit for bit the reference's formula), staged per wave in LDS:
@@ -159,10 +159,10 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
     constexpr int KC = NW * KTW;
     static_assert(XSRC == 0 || KTW == 8, "a wave that builds its activations covers one 128-point block");
     static_assert(XSRC != 0 || RB * KTW <= 64, "one lane a (member, k tile) when staging rotated rows");
-    __shared__ __attribute__((aligned(16))) uint16_t xs[NW][RB][KTW * 16];
+    __shared__ __attribute__((aligned(16))) uint32_t xs[NW][RB][KTW * 16];   // activations, each twice
     __shared__ float red[NW][RB][128];
 
-    const int u = blockIdx.x, cb = blockIdx.y;
+    const int u = blockIdx.x % a.ucap, cb = blockIdx.y, c0 = (int)(blockIdx.x / a.ucap) * RB;
     const int split = blockIdx.z % a.SK, mat = MATS == 1 ? 0 : blockIdx.z / a.SK;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, t = lane >> 3, i = lane & 7;
     const int KT = a.Kin >> 4, NT = a.N >> 4;
@@ -193,12 +193,14 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
         const int cntu = a.ucount[0];
         e = a.uids[u];
         code = lane < a.maxm ? a.members[(size_t)u * a.maxm + lane] : -1;
-        if (u >= cntu || e >= a.E) return;               // past the window's experts, or not an EXL3 expert
+        // past the window's experts, not an EXL3 expert, or this program's chunk is past the expert's members (the
+        // check sits here: a later exit, after the ballot, cost the RB > 1 forms most of their registers)
+        if (u >= cntu || e >= a.E || (c0 > 0 && __builtin_amdgcn_readlane(code, c0 & 63) < 0)) return;
     }
     const int cnt = __popcll(__ballot(code >= 0));        // members come first
     const int pair_l = code >= 0 ? (code >> 5) * a.slots + (code & 31) : 0;
 
-    // ---- activation loads of a chunk of members (before the trellis words for the first chunk)
+    // ---- activation loads of this program's chunk of members (before the trellis words)
     uint32_t xv[RB], sv = 0, sg = 0, su = 0;             // XSRC 1: bf16 pairs; scale pairs
     uint4 va = {0, 0, 0, 0}, vb = {0, 0, 0, 0};           // XSRC 0: this lane's k tile of one member
     float gsum[RB][2], usum[RB][2];
@@ -276,7 +278,7 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
                     float v[2] = {(a.x_f16 ? f16_to_f32(x0) : bf16_to_f32(x0)) * s0,
                                   (a.x_f16 ? f16_to_f32(x1) : bf16_to_f32(x1)) * s1};
                     fwht128_w64(v, lane);
-                    store_block<K>(&xs[wave][m][0], v, lane);
+                    store_block(&xs[wave][m][0], v, lane);
                 }
         } else if constexpr (XSRC == 2) {
             if constexpr (EARLY > 0) {
@@ -325,7 +327,7 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
                         v[j] = act * sdd[j];
                     }
                     fwht128_w64(v, lane);
-                    store_block<K>(&xs[wave][m][0], v, lane);
+                    store_block(&xs[wave][m][0], v, lane);
                     if (cb == 0 && a.xd) {
                         const int p = __builtin_amdgcn_readlane(pair_l, r0 + m);
                         *reinterpret_cast<uint32_t*>(a.xd + (size_t)p * a.Kin + n) =
@@ -335,12 +337,14 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
         } else {
             const int m = lane / KTW, kk = lane % KTW;
             if (m < nr) {
-                const uint32_t xa[4] = {va.x, va.y, va.z, va.w}, xb[4] = {vb.x, vb.y, vb.z, vb.w};
-                uint32_t o[8];
-                pair_activations<K>(xa, xb, o);
+                const uint32_t x8[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
                 uint4* dst = reinterpret_cast<uint4*>(&xs[wave][m][kk * 16]);
-                dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
-                dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t a0 = x8[2 * q] & 0xffffu, a1 = x8[2 * q] >> 16;
+                    const uint32_t b0 = x8[2 * q + 1] & 0xffffu, b1 = x8[2 * q + 1] >> 16;
+                    dst[q] = make_uint4(a0 | a0 << 16, a1 | a1 << 16, b0 | b0 << 16, b1 | b1 << 16);
+                }
             }
         }
         // the slots are this wave's own: a wave-level barrier orders the LDS stores before the reads
@@ -349,8 +353,8 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
 
-    const int nr0 = cnt < RB ? cnt : RB;
-    load_acts(0, nr0);
+    const int nr0 = cnt - c0 < RB ? cnt - c0 : RB;
+    load_acts(c0, nr0);
     uint32_t wr[KTW][K];
     {
         const uint32_t* T = mat ? a.t1 : a.t0;
@@ -363,9 +367,7 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
     // activation loads below the decode and splits the trellis loads into dependent rounds.
     __builtin_amdgcn_sched_barrier(0);
 
-    // one chunk of up to RB members (the first chunk's activations are already loading; the later chunks load
-    // theirs first). The first chunk is its own copy of the code so that its activation wait covers its own loads
-    // only, not the trellis words issued after them.
+    // the chunk of up to RB members (its activations are already loading)
     auto chunk = [&](int r0, int nr) {
         build_acts(r0, nr);
         __builtin_amdgcn_sched_barrier(0);
@@ -380,19 +382,14 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
 #pragma unroll
             for (int j = 0; j < K; ++j) __asm__ volatile("" : "+v"(wr[kk][j]));
             const uint32_t prev = prev_word(wr[kk][K - 1], i);
-            h2_t d[2][8];
-            decode_lane<K>(wr[kk], prev, d);
+            uint32_t cw[32];
+            lane_words<K>(wr[kk], prev, cw);
 #pragma unroll
             for (int m = 0; m < RB; ++m) {
                 if (m < nr) {
-                    const uint4 xa = *reinterpret_cast<const uint4*>(&xs[wave][m][kk * 16]);
-                    const uint4 xb = *reinterpret_cast<const uint4*>(&xs[wave][m][kk * 16 + 8]);
-                    const uint32_t xp[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-#pragma unroll
-                    for (int q = 0; q < 8; ++q) {
-                        acc[m][0] = __builtin_amdgcn_fdot2(d[0][q], bits_h2(xp[q]), acc[m][0], false);
-                        acc[m][1] = __builtin_amdgcn_fdot2(d[1][q], bits_h2(xp[q]), acc[m][1], false);
-                    }
+                    uint32_t xd[16];
+                    load_tile_acts(&xs[wave][m][kk * 16], xd);
+                    tile_dot(cw, xd, acc[m]);
                 }
             }
         }
@@ -421,15 +418,9 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
                 const int p = __builtin_amdgcn_readlane(pair_l, r0 + m);
                 a.z[((size_t)(mat * a.SK + split) * a.P + p) * a.N + cb * 128 + col] = sum;
             }
-            if (r0 + RB < cnt) __syncthreads();            // red is rewritten by the next chunk
         }
     };
-    chunk(0, nr0);
-    for (int r0 = RB; r0 < cnt; r0 += RB) {
-        const int nr = cnt - r0 < RB ? cnt - r0 : RB;
-        load_acts(r0, nr);
-        chunk(r0, nr);
-    }
+    chunk(c0, nr0);
 }
 
 // Down epilogue (exl3.cu:300-321) and, with weights, the slot-ordered combine of a token. Program (token row,
@@ -611,23 +602,21 @@ constexpr int TOKEN_SPIN_LIMIT = 1 << 22;     // polls of a counter before the l
 constexpr int TOKEN_MAX_SLOTS = 16;
 constexpr int TOKEN_MAX_SPLITS = 16;           // K splits of either GEMV (hidden <= 8192, inter <= 4096)
 
-// this wave's 128 k x 16 columns of one trellis block row against its staged activations xs (pair order)
+// this wave's 128 k x 16 columns of one trellis block row against its staged activations xs (each twice)
 template <int K>
-__device__ __forceinline__ void token_dot(const uint32_t (&wr)[8][K], const uint16_t* xs, int i, float& acc0,
+__device__ __forceinline__ void token_dot(const uint32_t (&wr)[8][K], const uint32_t* xs, int i, float& acc0,
                                           float& acc1) {
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
         const uint32_t prev = prev_word(wr[kk][K - 1], i);
-        h2_t d[2][8];
-        decode_lane<K>(wr[kk], prev, d);
-        const uint4 xa = *reinterpret_cast<const uint4*>(xs + kk * 16);
-        const uint4 xb = *reinterpret_cast<const uint4*>(xs + kk * 16 + 8);
-        const uint32_t xp[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            acc0 = __builtin_amdgcn_fdot2(d[0][q], bits_h2(xp[q]), acc0, false);
-            acc1 = __builtin_amdgcn_fdot2(d[1][q], bits_h2(xp[q]), acc1, false);
-        }
+        uint32_t cw[32];
+        lane_words<K>(wr[kk], prev, cw);
+        uint32_t xd[16];
+        load_tile_acts(xs + kk * 16, xd);
+        float acc[2] = {acc0, acc1};
+        tile_dot(cw, xd, acc);
+        acc0 = acc[0];
+        acc1 = acc[1];
     }
 }
 
@@ -639,7 +628,7 @@ __device__ __forceinline__ void wave_sync_lds() {
 
 template <int K>
 __global__ void __launch_bounds__(256) moe_token_kernel(const TokenArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t xs[4][128];
+    __shared__ __attribute__((aligned(16))) uint32_t xs[4][128];   // activations, each twice
     __shared__ float red[4][128];
     __shared__ float2 ys[TOKEN_MAX_SLOTS][64];
     __shared__ uint32_t sh[2];
@@ -690,7 +679,7 @@ __global__ void __launch_bounds__(256) moe_token_kernel(const TokenArgs a) {
                 float v[2] = {bf16_to_f32((uint16_t)xv) * f16_to_f32((uint16_t)sv),
                               bf16_to_f32((uint16_t)(xv >> 16)) * f16_to_f32((uint16_t)(sv >> 16))};
                 fwht128_w64(v, lane);
-                store_block<K>(xs[wave], v, lane);
+                store_block(xs[wave], v, lane);
                 wave_sync_lds();
             }
             float acc0 = 0.f, acc1 = 0.f;
@@ -773,7 +762,7 @@ __global__ void __launch_bounds__(256) moe_token_kernel(const TokenArgs a) {
                     v[j] = act * sdd[j];
                 }
                 fwht128_w64(v, lane);
-                store_block<K>(xs[wave], v, lane);
+                store_block(xs[wave], v, lane);
                 if (hb == 0)                              // the down input, for the caller (engine xd)
                     *reinterpret_cast<uint32_t*>(a.xd + (size_t)s * a.N + n) =
                         (uint32_t)f16_of_product(v[0], HAD_SCALE) | ((uint32_t)f16_of_product(v[1], HAD_SCALE) << 16);
@@ -902,6 +891,8 @@ static hipError_t gemv_go(int rb, dim3 grid, hipStream_t s, const GemvArgs& a) {
 
 // member rows a chunk: the smallest of 1, 2, 4, 8 that holds the window's rows (an expert has at most `rows`)
 static int rb_for(int rows) { return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8; }
+// programs along x: maxu experts times the chunks of rb members that an expert with `members` members needs
+static unsigned chunks_x(int maxu, int members, int rb) { return (unsigned)maxu * (unsigned)((members + rb - 1) / rb); }
 
 template <int KTW, int NW, int MATS, int XSRC, bool ROUTE1 = false>
 static hipError_t gemv_bits(int bits, int rb, dim3 grid, hipStream_t s, const GemvArgs& a) {
@@ -921,7 +912,8 @@ hipError_t launch_gemv(hipStream_t s, const uint16_t* X0, const uint16_t* X1, co
     a.x0 = X0; a.x1 = X1; a.t0 = T0; a.t1 = T1; a.uids = uids; a.ucount = ucount; a.members = members; a.z = Z;
     a.Kin = Kin; a.N = N; a.P = P; a.SK = gemv_splits(Kin); a.maxm = maxm; a.slots = slots; a.E = E;
     const int ktw = ktw_for(Kin), rb = rb_for(maxm);
-    const dim3 grid(maxu, N / 128, mats * a.SK);
+    a.ucap = maxu;
+    const dim3 grid(chunks_x(maxu, maxm, rb), N / 128, mats * a.SK);
     if (mats == 2) {
         if (ktw == 4) return gemv_bits<4, 4, 2, 0>(bits, rb, grid, s, a);
         if (ktw == 2) return gemv_bits<2, 4, 2, 0>(bits, rb, grid, s, a);
@@ -940,8 +932,9 @@ hipError_t launch_expert_gateup(hipStream_t s, const uint16_t* x, int x_stride, 
     a.x0 = x; a.x_stride = x_stride; a.suh0 = suh_g; a.suh1 = suh_u; a.t0 = gt; a.t1 = ut;
     a.uids = uids; a.ucount = ucount; a.members = members; a.z = Zgu; a.Kin = D; a.N = N; a.P = P;
     a.SK = gemv_gateup_splits(D); a.maxm = maxm; a.slots = slots; a.E = E;
-    const dim3 grid(maxu, N / 128, 2 * a.SK);
-    const int nw = nw_gateup(D), rb = rb_for(rows);
+    const int nw = nw_gateup(D), rb = route ? 1 : rb_for(rows);
+    a.ucap = maxu;
+    const dim3 grid(chunks_x(maxu, rows < maxm ? rows : maxm, rb), N / 128, 2 * a.SK);
     if (route) {
         a.logits = route->logits; a.routed = route->routed; a.pick_out = route->picks; a.weight_out = route->weights;
         a.route_bias = route->bias; a.route_scale = route->scale;
@@ -959,7 +952,9 @@ hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, const uint
     a.zgu = Zgu; a.SKgu = gemv_gateup_splits(D); a.svh_g = svh_g; a.svh_u = svh_u; a.suh0 = suh_d; a.limit = limit;
     a.xd = xd; a.t0 = dt; a.t1 = dt; a.uids = uids; a.ucount = ucount; a.members = members; a.z = Zd;
     a.Kin = N; a.N = D; a.P = P; a.SK = gemv_down_splits(N); a.maxm = maxm; a.slots = slots; a.E = E;
-    return gemv_bits<8, 2, 1, 2>(bits, rb_for(rows), dim3(maxu, D / 128, a.SK), s, a);
+    const int rb = rb_for(rows);
+    a.ucap = maxu;
+    return gemv_bits<8, 2, 1, 2>(bits, rb, dim3(chunks_x(maxu, rows < maxm ? rows : maxm, rb), D / 128, a.SK), s, a);
 }
 
 // One linear with its input rotation fused (XSRC 1, fp16 input): Z[split][n] partials of
@@ -972,7 +967,7 @@ hipError_t launch_linear_fused(hipStream_t s, const uint16_t* x, const uint16_t*
     GemvArgs a{};
     a.x0 = x; a.x_stride = kin; a.x_f16 = 1; a.suh0 = suh; a.suh1 = suh; a.t0 = trellis; a.t1 = trellis;
     a.uids = uids; a.ucount = ucount; a.members = members; a.z = z; a.Kin = kin; a.N = n; a.P = 1;
-    a.SK = gemv_linear_splits(kin); a.maxm = 1; a.slots = 1; a.E = 1;
+    a.SK = gemv_linear_splits(kin); a.maxm = 1; a.slots = 1; a.E = 1; a.ucap = 1;
     const dim3 grid(1, n / 128, a.SK);
     const bool four = nw_linear(kin) == 4;
     switch (bits) {

@@ -13,6 +13,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <utility>
 
 namespace gfr {
 
@@ -115,28 +116,83 @@ __device__ __forceinline__ void decode_lane_std(const uint32_t (&w)[K], uint32_t
     else decode_lane<K>(w, prev, d);
 }
 
-// The 16 activations of one k tile, natural order in (a = halves 0..7, b = halves 8..15), rearranged into the 8
-// packed pairs of pair_row: out[m] = (x[ra(m)], x[rb(m)]).
-template <int K>
-__device__ __forceinline__ void pair_activations(const uint32_t (&a)[4], const uint32_t (&b)[4], uint32_t (&out)[8]) {
-    if constexpr (K == 2) {
-        // m = 4v + u: u = 0 (r = 4v), 1 (4v + 1), 2 (4v + 8), 3 (4v + 9); pair (x[r + 2], x[r])
-#pragma unroll
-        for (int v = 0; v < 2; ++v) {
-            out[4 * v + 0] = __builtin_amdgcn_perm(a[2 * v], a[2 * v + 1], 0x05040100u);
-            out[4 * v + 1] = __builtin_amdgcn_perm(a[2 * v], a[2 * v + 1], 0x07060302u);
-            out[4 * v + 2] = __builtin_amdgcn_perm(b[2 * v], b[2 * v + 1], 0x05040100u);
-            out[4 * v + 3] = __builtin_amdgcn_perm(b[2 * v], b[2 * v + 1], 0x07060302u);
+// ---- the decode GEMV's dot: codebook words against activations, without the fp16 weight in between -------------
+// For one state s (16 bits, in half SEL of r), the masked codebook word m = (s * 0xCBAC1FED mod 2^32 & 0x8FFF8FFF) ^
+// 0x3B603B60 (experts.rs:43-46) holds the two fp16 halves whose sum is the weight. The GEMV adds both halves times
+// the activation in one v_dot2_f32_f16 against the activation staged twice, (x, x): acc + x * m.lo + x * m.hi in
+// fp32. The reference rounds m.lo + m.hi to fp16 first; this sum keeps that rounding
+// out (a difference of at most half an fp16 ulp of each weight). Four VALU operations a weight:
+//   v_pk_mul_lo_u16  (0, s * 0xCBAC)                  (the high half of s * 0xCBAC0000)
+//   v_mad_u32_u16    s * 0x1FED + (s * 0xCBAC << 16) = s * 0xCBAC1FED mod 2^32
+//   v_bitop3         mask, flip
+//   v_dot2_f32_f16   acc += x * m.lo + x * m.hi
+// (op_sel on the v_dot2 operands is not encodable on gfx950, hence the doubled activations.)
+template <int SEL>
+__device__ __forceinline__ uint32_t codeword(uint32_t r) {
+    uint32_t t, x;
+    if constexpr (SEL == 0) {
+        __asm__("v_pk_mul_lo_u16 %0, %1, %2 op_sel:[0,0] op_sel_hi:[0,1]" : "=v"(t) : "v"(r), "s"(0xCBAC0000u));
+        __asm__("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(x) : "v"(r), "s"(0x1FEDu), "v"(t));
+    } else {
+        __asm__("v_pk_mul_lo_u16 %0, %1, %2 op_sel:[1,0] op_sel_hi:[1,1]" : "=v"(t) : "v"(r), "s"(0xCBAC0000u));
+        __asm__("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[1,0,0,0]" : "=v"(x) : "v"(r), "s"(0x1FEDu), "v"(t));
+    }
+    return (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
+}
+// The lane's stream shifted right so that the window of value Q ends at bit 0, all 32 bits (bits 16-31: the 16
+// stream bits before the window).
+template <int K, int Q>
+__device__ __forceinline__ uint32_t lane_window32(const uint32_t (&w)[K], uint32_t prev) {
+    constexpr int e = (Q + 1) * K, hiw = (e - 1) >> 5, shift = 32 * (hiw + 1) - e;
+    if constexpr (shift == 0) return w[hiw];
+    else return __builtin_amdgcn_alignbit(hiw == 0 ? prev : w[hiw > 0 ? hiw - 1 : 0], w[hiw], shift);
+}
+
+// Masked codebook words of the lane's 32 values, value order. K = 2 and 4: one 32-bit window holds the states of
+// values Q (low half) and Q - 16 / K (high half).
+template <int K, int Q>
+__device__ __forceinline__ void lane_word(const uint32_t (&w)[K], uint32_t prev, uint32_t (&m)[32]) {
+    if constexpr (K == 2 || K == 4) {
+        constexpr int D = 16 / K;
+        if constexpr (Q % (2 * D) >= D) {
+            const uint32_t r = lane_window32<K, Q>(w, prev);
+            m[Q] = codeword<0>(r);
+            m[Q - D] = codeword<1>(r);
         }
     } else {
-        // m = 2l + h: (x[2l + 8 + h], x[2l + h])
-#pragma unroll
-        for (int l = 0; l < 4; ++l) {
-            out[2 * l] = __builtin_amdgcn_perm(a[l], b[l], 0x05040100u);
-            out[2 * l + 1] = __builtin_amdgcn_perm(a[l], b[l], 0x07060302u);
-        }
+        m[Q] = codeword<0>(lane_window<K, Q>(w, prev));
     }
 }
+template <int K, int... Q>
+__device__ __forceinline__ void lane_words_(const uint32_t (&w)[K], uint32_t prev, uint32_t (&m)[32],
+                                            std::integer_sequence<int, Q...>) {
+    (lane_word<K, Q>(w, prev, m), ...);
+}
+template <int K>
+__device__ __forceinline__ void lane_words(const uint32_t (&w)[K], uint32_t prev, uint32_t (&m)[32]) {
+    lane_words_<K>(w, prev, m, std::make_integer_sequence<int, 32>{});
+}
+
+// Tile row of value q of a lane (the format's row 2 (q / 8) + (j & 1) + 8 ((j >> 1) & 1), j = q % 8) and its column
+// (0: i, 1: i + 8).
+__host__ __device__ constexpr int value_row(int q) { return 2 * ((q >> 3) & 3) + (q & 1) + 8 * ((q >> 1) & 1); }
+__host__ __device__ constexpr int value_col(int q) { return (q & 7) >> 2; }
+
+// One k tile of the lane's two columns against the tile's 16 activations, each staged twice (xd[r] = (x_r, x_r)):
+// acc[c] += the column's 16 weights times their rows, added in value order.
+template <int Q>
+__device__ __forceinline__ void value_dot(const uint32_t (&m)[32], const uint32_t (&xd)[16], float (&acc)[2]) {
+    acc[value_col(Q)] = __builtin_amdgcn_fdot2(bits_h2(m[Q]), bits_h2(xd[value_row(Q)]), acc[value_col(Q)], false);
+}
+template <int... Q>
+__device__ __forceinline__ void tile_dot_(const uint32_t (&m)[32], const uint32_t (&xd)[16], float (&acc)[2],
+                                          std::integer_sequence<int, Q...>) {
+    (value_dot<Q>(m, xd, acc), ...);
+}
+__device__ __forceinline__ void tile_dot(const uint32_t (&m)[32], const uint32_t (&xd)[16], float (&acc)[2]) {
+    tile_dot_(m, xd, acc, std::make_integer_sequence<int, 32>{});
+}
+
 
 // The previous word for lane i of an 8-lane tile group: lane - 1, or lane + 7 for i == 0 (DPP within a 16-lane row).
 __device__ __forceinline__ uint32_t prev_word(uint32_t last, int i) {

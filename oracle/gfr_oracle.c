@@ -63,6 +63,14 @@ uint16_t gfro_codebook(uint32_t s) {
     return gfro_f32_to_f16(gfro_f16_to_f32((uint16_t)x) + gfro_f16_to_f32((uint16_t)(x >> 16)));
 }
 
+/* The same two halves summed in fp32 and not rounded: the weight as this library's decode GEMV multiplies it (one
+ * v_dot2_f32_f16 of both halves against the activation). Exact: both halves are fp16 of magnitude 2^-3 .. 2, so the
+ * sum needs at most 16 significant bits. gfro_codebook(s) is this value rounded to fp16. */
+float gfro_codebook_sum(uint32_t s) {
+    uint32_t x = ((s * 0xcbac1fedu) & 0x8fff8fffu) ^ 0x3b603b60u;
+    return gfro_f16_to_f32((uint16_t)x) + gfro_f16_to_f32((uint16_t)(x >> 16));
+}
+
 void gfro_codebook_table(uint16_t* out) {
     for (uint32_t s = 0; s < 65536u; ++s) out[s] = gfro_codebook(s);
 }
@@ -97,6 +105,20 @@ void gfro_unpack(const uint32_t* words, int kin, int n, int bits, uint16_t* w) {
                 int row, col;
                 gfro_tile_pos(p, &row, &col);
                 w[(size_t)(kt * 16 + row) * n + nt * 16 + col] = gfro_codebook(gfro_state(tile, bits, p));
+            }
+        }
+}
+
+/* gfro_unpack with the unrounded sums of gfro_codebook_sum (the decode GEMV's weights) */
+void gfro_unpack_f32_sum(const uint32_t* words, int kin, int n, int bits, float* w) {
+    const int TW = gfro_tile_words(bits);
+    for (int kt = 0; kt < kin / 16; ++kt)
+        for (int nt = 0; nt < n / 16; ++nt) {
+            const uint32_t* tile = words + ((size_t)kt * (n / 16) + nt) * TW;
+            for (int p = 0; p < 256; ++p) {
+                int row, col;
+                gfro_tile_pos(p, &row, &col);
+                w[(size_t)(kt * 16 + row) * n + nt * 16 + col] = gfro_codebook_sum(gfro_state(tile, bits, p));
             }
         }
 }

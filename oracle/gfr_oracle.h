@@ -23,12 +23,14 @@ float gfro_bf16_to_f32(uint16_t b);
 
 uint16_t gfro_codebook(uint32_t s);         /* experts.rs:43-46 == exl3.cu:21-30 (mcg2), fp16 bits */
 void gfro_codebook_table(uint16_t* out);    /* all 65536 states */
+float gfro_codebook_sum(uint32_t s);        /* the two halves summed, unrounded (the decode GEMV's weight) */
 int gfro_tile_words(int bits);              /* 32-bit words in a 16x16 tile: 256 * bits / 32 */
 uint32_t gfro_state(const uint32_t* tile, int bits, int p);   /* experts.rs:58-64 generalised to K bits */
 void gfro_tile_pos(int p, int* row, int* col);                /* experts.rs:65-69 */
 /* experts.rs:47-74: trellis words [kin/16][n/16][tile_words] -> row-major fp16 bits [kin][n] */
 void gfro_unpack(const uint32_t* words, int kin, int n, int bits, uint16_t* w);
 void gfro_unpack_f32(const uint32_t* words, int kin, int n, int bits, float* w);
+void gfro_unpack_f32_sum(const uint32_t* words, int kin, int n, int bits, float* w);  /* unrounded weights */
 
 void gfro_had(float* x, long n);            /* experts.rs:25-42: unnormalised FWHT per 128-block */
 /* experts.rs:75-96: y[n] = sum_j x[j] w[j][n], K split into sk * warps contiguous ranges summed in order */

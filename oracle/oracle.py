@@ -30,6 +30,7 @@ def _load():
         "gfro_bf": ([F], F), "gfro_hf": ([F], F), "gfro_codebook": ([ctypes.c_uint32], ctypes.c_uint16),
         "gfro_codebook_table": ([P], None), "gfro_state": ([P, I, I], ctypes.c_uint32),
         "gfro_unpack": ([P, I, I, I, P], None), "gfro_unpack_f32": ([P, I, I, I, P], None),
+        "gfro_unpack_f32_sum": ([P, I, I, I, P], None), "gfro_codebook_sum": ([ctypes.c_uint32], F),
         "gfro_had": ([P, ctypes.c_long], None), "gfro_matmul": ([P, P, I, I, I, I, P], None),
         "gfro_rot": ([P, P, I, P], None),
         "gfro_gateup_epilogue": ([P, P, P, P, P, I, F, P], None), "gfro_down_epilogue": ([P, P, I, P], None),
@@ -76,11 +77,18 @@ def unpack(words, kin, n, bits):
     return out
 
 
-def unpack_f32(words, kin, n, bits):
+def unpack_f32(words, kin, n, bits, rounded=True):
+    """fp32 weights [kin, n]: the reference's fp16 codebook values (rounded) or the unrounded sums of the two fp16
+    halves (gfro_codebook_sum), which this library's decode GEMV multiplies."""
     w = np.ascontiguousarray(words).view(np.uint32)
     out = np.empty((kin, n), np.float32)
-    lib().gfro_unpack_f32(_p(w), kin, n, bits, _p(out))
+    (lib().gfro_unpack_f32 if rounded else lib().gfro_unpack_f32_sum)(_p(w), kin, n, bits, _p(out))
     return out
+
+
+def codebook_sums():
+    """gfro_codebook_sum of all 65536 states (fp32)."""
+    return np.array([lib().gfro_codebook_sum(s) for s in range(65536)], np.float32)
 
 
 def had(x):

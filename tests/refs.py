@@ -12,18 +12,20 @@ def np_u32(t: torch.Tensor) -> np.ndarray:
 
 
 class DecodedExperts:
-    """Decodes (and caches) experts of an Exl3Experts through the oracle."""
+    """Decodes (and caches) experts of an Exl3Experts through the oracle. rounded: the reference's fp16 weights;
+    otherwise the unrounded sums of the two codebook halves that the decode GEMV multiplies (gfro_codebook_sum)."""
 
-    def __init__(self, oracle, w):
-        self.o, self.w = oracle, w
+    def __init__(self, oracle, w, rounded=True):
+        self.o, self.w, self.rounded = oracle, w, rounded
         self.cache = {}
         self.vec = {n: np_u16(getattr(w, n)) for n in ("suh_g", "suh_u", "suh_d", "svh_g", "svh_u", "svh_d")}
 
     def mats(self, e):
         if e not in self.cache:
             w, D, N, b = self.w, self.w.hidden, self.w.inter, self.w.bits
-            self.cache[e] = (self.o.unpack_f32(np_u32(w.gt[e]), D, N, b), self.o.unpack_f32(np_u32(w.ut[e]), D, N, b),
-                             self.o.unpack_f32(np_u32(w.dt[e]), N, D, b))
+            r = self.rounded
+            self.cache[e] = (self.o.unpack_f32(np_u32(w.gt[e]), D, N, b, r), self.o.unpack_f32(np_u32(w.ut[e]), D, N, b, r),
+                             self.o.unpack_f32(np_u32(w.dt[e]), N, D, b, r))
         return self.cache[e]
 
     def row(self, x_bf16_u16, e, sk_gu=4, sk_d=1, warps=4):
@@ -31,6 +33,10 @@ class DecodedExperts:
         v = self.vec
         return self.o.expert_row(x_bf16_u16, wg, wu, wd, v["suh_g"][e], v["suh_u"][e], v["suh_d"][e], v["svh_g"][e],
                                  v["svh_u"][e], v["svh_d"][e], sk_gu, sk_d, warps)
+
+
+# The north star's bar for a layer's outputs against the reference's arithmetic: 1e-2 relative.
+NORTH_STAR_REL = 1e-2
 
 
 def assert_close(got, want, rel_rms=1e-3, rel_max=1e-2, what=""):
@@ -42,3 +48,10 @@ def assert_close(got, want, rel_rms=1e-3, rel_max=1e-2, what=""):
     mx = np.max(np.abs(err)) / max(np.max(np.abs(want)), 1e-30)
     assert rms < rel_rms and mx < rel_max, f"{what}: relative RMS {rms:.3g}, max {mx:.3g}"
     return rms, mx
+
+
+def assert_decode_close(got, want_gemv, want_ref, what=""):
+    """A decode-GEMV result against the oracle with the GEMV's own weights (unrounded codebook sums, fp32 order of the
+    kernels: the tight bar) and against the reference's fp16 weights (the north star's 1e-2)."""
+    assert_close(got, want_gemv, what=what)
+    return assert_close(got, want_ref, rel_rms=NORTH_STAR_REL, rel_max=NORTH_STAR_REL, what=what + " vs reference weights")

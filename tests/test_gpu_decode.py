@@ -4,7 +4,7 @@ import numpy as np
 import pytest
 import torch
 
-from refs import DecodedExperts, assert_close, np_u16, np_u32
+from refs import DecodedExperts, assert_close, assert_decode_close, np_u16, np_u32
 
 pytestmark = pytest.mark.gpu
 
@@ -103,8 +103,27 @@ def test_linear_config1(gfr, oracle, kin, n, bits):
     lin = gfr.Linear(kin, n, bits)
     lin.run(x, t, suh, svh, y)
     torch.cuda.synchronize()
-    want = oracle.linear(np_u16(x), oracle.unpack_f32(np_u32(t), kin, n, bits), np_u16(suh), np_u16(svh))
-    assert_close(y.cpu().numpy(), want, what="linear")
+    want = [oracle.linear(np_u16(x), oracle.unpack_f32(np_u32(t), kin, n, bits, rounded), np_u16(suh), np_u16(svh))
+            for rounded in (False, True)]
+    assert_decode_close(y.cpu().numpy(), *want, what="linear")
+
+
+DECODE_ROWS = 6   # Moe runs windows of up to this many rows on the decode engine (gfr_moe_set_decode_rows default)
+
+
+def _check_tokens(oracle, w, x, picks, weights, out, tokens, slots, what=""):
+    """Moe outputs of the given tokens against the oracle: windows on the decode engine against both weight forms
+    (assert_decode_close), larger windows (the MFMA path, fp16 weights as the reference) at the tight bar."""
+    rows = out.shape[0]
+    decs = [DecodedExperts(oracle, w, rounded) for rounded in ((False, True) if rows <= DECODE_ROWS else (True,))]
+    xb = np_u16(x)
+    for r in tokens:
+        want = [oracle.combine(np.stack([d.row(xb[r], int(e))[0] for e in picks[r]]), weights[r:r + 1], 1, slots)[0]
+                for d in decs]
+        if rows <= DECODE_ROWS:
+            assert_decode_close(out[r], *want, what=f"{what} token {r}")
+        else:
+            assert_close(out[r], want[0], what=f"{what} token {r}")
 
 
 def _moe_inputs(E_routed, D, N, bits, rows, topk, seed, zipf=False):
@@ -129,12 +148,13 @@ def test_experts_run_rows_vs_oracle(gfr, oracle, rows, zipf):
     ex.run_rows(w, x, picks, g.ids, g.count, g.members, rows, 16)
     torch.cuda.synchronize()
     y = ex.y.cpu().numpy()
-    dec = DecodedExperts(oracle, w)
+    dec, ref = DecodedExperts(oracle, w, rounded=False), DecodedExperts(oracle, w)
     xb = np_u16(x)
     for r in range(rows):
         for s in range(slots):
-            want, _ = dec.row(xb[r], int(p[r, s]))
-            assert_close(y[r * slots + s], want, what=f"row {r} slot {s} expert {p[r, s]}")
+            e = int(p[r, s])
+            assert_decode_close(y[r * slots + s], dec.row(xb[r], e)[0], ref.row(xb[r], e)[0],
+                                what=f"row {r} slot {s} expert {e}")
 
 
 def test_batched_rows_equal_serial_rows(gfr, oracle):
@@ -197,11 +217,12 @@ def test_moe_layer_decode_vs_oracle(gfr, oracle):
     p, wt = oracle.route(lg.cpu().numpy(), topk, E)
     assert np.array_equal(m.picks.cpu().numpy(), p)
     np.testing.assert_allclose(m.weights.cpu().numpy(), wt, rtol=1e-6)
-    dec = DecodedExperts(oracle, w)
-    xb = np_u16(x)
-    ys = np.stack([dec.row(xb[0], int(e))[0] for e in p[0]])
-    want = oracle.combine(ys, wt, 1, topk + 1)
-    assert_close(m.output.cpu().numpy(), want, what="moe output")
+    want = []
+    for rounded in (False, True):
+        dec = DecodedExperts(oracle, w, rounded)
+        ys = np.stack([dec.row(np_u16(x)[0], int(e))[0] for e in p[0]])
+        want.append(oracle.combine(ys, wt, 1, topk + 1))
+    assert_decode_close(m.output.cpu().numpy(), *want, what="moe output")
 
 
 def test_moe_graph_replay_bytes(gfr):
@@ -268,14 +289,8 @@ def test_moe_layer_verify_window_vs_oracle(gfr, oracle, rows):
     torch.cuda.synchronize()
     p, wt = oracle.route(lg.cpu().numpy(), topk, E)
     assert np.array_equal(m.picks[:rows].cpu().numpy(), p)
-    dec = DecodedExperts(oracle, w)
-    xb = np_u16(x)
-    check = range(rows) if rows <= 4 else (0, 7, rows - 1)
-    out = m.output.cpu().numpy()
-    for r in check:
-        ys = np.stack([dec.row(xb[r], int(e))[0] for e in p[r]])
-        want = oracle.combine(ys, wt[r:r + 1], 1, topk + 1)
-        assert_close(out[r], want[0], what=f"token {r}")
+    _check_tokens(oracle, w, x, p, wt, m.output[:rows].cpu().numpy(), range(rows) if rows <= 4 else (0, 7, rows - 1),
+                  topk + 1)
 
 
 def test_rotation_bitexact(gfr, oracle):
@@ -386,10 +401,7 @@ def test_moe_layer_config5_decode_vs_oracle(gfr, oracle, bits):
     torch.cuda.synchronize()
     p, wt = oracle.route(lg.cpu().numpy(), topk, E)
     assert np.array_equal(m.picks.cpu().numpy(), p)
-    dec = DecodedExperts(oracle, w)
-    xb = np_u16(x)
-    ys = np.stack([dec.row(xb[0], int(e))[0] for e in p[0]])
-    assert_close(m.output.cpu().numpy(), oracle.combine(ys, wt, 1, topk + 1), what=f"config 5 K={bits}")
+    _check_tokens(oracle, w, x, p, wt, m.output[:1].cpu().numpy(), (0,), topk + 1, what=f"config 5 K={bits}")
 
 
 def _biased_inputs(rows, E, seed):
@@ -439,14 +451,9 @@ def test_moe_layer_biased_router_vs_oracle(gfr, oracle, rows, single):
     m.run(w, x, logits, rows)
     torch.cuda.synchronize()
     p, wt = _check_biased(oracle, m.picks[:rows], m.weights[:rows], logits, bias, topk, E)
-    dec = DecodedExperts(oracle, w)
-    xb = np_u16(x)
-    out = m.output.cpu().numpy()
     gp, gw = m.picks[:rows].cpu().numpy(), m.weights[:rows].cpu().numpy()
-    for r in (range(rows) if rows <= 3 else (0, rows - 1)):
-        ys = np.stack([dec.row(xb[r], int(e))[0] for e in gp[r]])
-        want = oracle.combine(ys, gw[r:r + 1], 1, topk + 1)
-        assert_close(out[r], want[0], what=f"token {r}")
+    _check_tokens(oracle, w, x, gp, gw, m.output[:rows].cpu().numpy(), range(rows) if rows <= 3 else (0, rows - 1),
+                  topk + 1)
     m.set_router(None)
     m.run(w, x, logits, rows)
     torch.cuda.synchronize()

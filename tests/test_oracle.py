@@ -30,6 +30,27 @@ def test_codebook_independent_numpy(oracle):
     assert np.array_equal(oracle.codebook_table(), want)
 
 
+def test_codebook_sum(oracle):
+    # the decode GEMV's weight: the two halves summed without the final fp16 rounding. Independently restated in
+    # numpy (float32 add of the two float16 halves), exact (float64 sum agrees), and rounding it to fp16 gives the
+    # reference's codebook for every state
+    s = np.arange(65536, dtype=np.uint64)
+    x = ((s * 0xCBAC1FED) & 0xFFFFFFFF) & 0x8FFF8FFF ^ 0x3B603B60
+    lo = (x & 0xFFFF).astype(np.uint16).view(np.float16)
+    hi = (x >> 16).astype(np.uint16).view(np.float16)
+    got = oracle.codebook_sums()
+    assert np.array_equal(got, lo.astype(np.float32) + hi.astype(np.float32))
+    assert np.array_equal(got.astype(np.float64), lo.astype(np.float64) + hi.astype(np.float64))
+    assert np.array_equal(got.astype(np.float16).view(np.uint16), oracle.codebook_table())
+    r16 = oracle.codebook_table().view(np.float16)
+    assert np.all(np.abs(got - r16.astype(np.float32)) <= np.abs(got) * 2.0 ** -11)   # fp16's unit roundoff a weight
+    # the unrounded unpack places the same values as the rounded one
+    rng = np.random.default_rng(5)
+    words = rng.integers(0, 2 ** 32, size=(4, 3, 32), dtype=np.uint64).astype(np.uint32)
+    a, b = oracle.unpack_f32(words, 64, 48, 4, False), oracle.unpack_f32(words, 64, 48, 4)
+    assert np.array_equal(a.astype(np.float16).astype(np.float32), b)
+
+
 def test_hadamard_involution(oracle):
     # experts.rs:569-576: had(had(x)) == 128 x exactly for x = i - 64
     x = np.arange(128, dtype=np.float32) - 64
