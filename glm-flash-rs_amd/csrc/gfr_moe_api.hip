@@ -405,9 +405,10 @@ int gfr_moe_create(gfr_moe** out, int hidden, int inter, int routed, int topk, i
     if (topk <= 0 || topk > 31 || topk > routed) return fail(GFR_EINVAL, "topk %d", topk);
     if (max_rows <= 0 || max_rows > (1 << 16)) return fail(GFR_EINVAL, "max_rows %d", max_rows);
     // decode engine for up to 64 rows; by default it takes windows of at most MOE_DECODE_ROWS rows, the prefill
-    // engine (split-K MFMA for small windows) the rest: measured crossover on MI355X between 4 and 8 rows at both
-    // benchmark shapes (hidden 2048 top-4 and hidden 5120 top-8)
-    constexpr int MOE_DECODE_ROWS = 6;
+    // engine (split-K MFMA for small windows) the rest: measured on MI355X (Zipf(1.1) routing), the decode engine wins
+    // up to 4 rows and split-K from 6 at both benchmark shapes (hidden 2048 top-4: 49.8 / 57.9 us at 4 rows, 72.2 /
+    // 63.6 at 6; hidden 5120 top-8 K = 3: 169 / 173 at 4, 256 / 204 at 6)
+    constexpr int MOE_DECODE_ROWS = 4;
     const int dec_cap = 64 < max_rows ? 64 : max_rows;
     gfr_moe* m = new gfr_moe{hidden, inter, routed, topk, topk + 1, max_rows,
                              MOE_DECODE_ROWS < max_rows ? MOE_DECODE_ROWS : max_rows,

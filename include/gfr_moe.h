@@ -113,7 +113,7 @@ int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const
 float* gfr_moe_output(const gfr_moe* m);
 int32_t* gfr_moe_picks(const gfr_moe* m);        /* [rows][topk + 1] */
 float* gfr_moe_weights(const gfr_moe* m);        /* [rows][topk + 1] */
-int gfr_moe_set_decode_rows(gfr_moe* m, int decode_rows);  /* rows at or below run the decode path (default 6, max 64) */
+int gfr_moe_set_decode_rows(gfr_moe* m, int decode_rows);  /* rows at or below run the decode path (default 4, max 64) */
 /* rows == 1 as one persistent launch (route .. combine; default on when hidden % 512 == 0 and inter % 256 == 0) or
  * as three launches (gate/up + route, down + gate/up epilogue, down epilogue + combine); both give the same bits.
  * No counterpart in the reference, whose decode layer is a captured graph of separate launches (model.rs:634). */

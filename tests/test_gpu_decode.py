@@ -108,7 +108,7 @@ def test_linear_config1(gfr, oracle, kin, n, bits):
     assert_decode_close(y.cpu().numpy(), *want, what="linear")
 
 
-DECODE_ROWS = 6   # Moe runs windows of up to this many rows on the decode engine (gfr_moe_set_decode_rows default)
+DECODE_ROWS = 4   # Moe runs windows of up to this many rows on the decode engine (gfr_moe_set_decode_rows default)
 
 
 def _check_tokens(oracle, w, x, picks, weights, out, tokens, slots, what=""):
