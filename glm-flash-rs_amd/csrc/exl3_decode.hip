@@ -267,7 +267,7 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
             }
         }
     };
-    // ---- the loaded activations of a chunk -> this wave's pair-ordered LDS slots
+    // ---- the loaded activations of a chunk -> this wave's LDS slots (tile row order, each value twice)
     auto build_acts = [&](int r0, int nr) {
         if constexpr (XSRC == 1) {
             const float s0 = f16_to_f32((uint16_t)sv), s1 = f16_to_f32((uint16_t)(sv >> 16));

@@ -58,8 +58,9 @@ __device__ __forceinline__ uint32_t lane_window(const uint32_t (&w)[K], uint32_t
 
 // Row pairs: decode_lane produces, for each of the lane's two columns (i, i + 8), 8 packed weight pairs
 // d[c][m] = (W[ra(m)][col], W[rb(m)][col]) (low, high half). The pairing depends on K so that the two states of a
-// pair come out of one register cheaply; rows are those of the tile (0..15). The activations are stored in the same
-// pair order (row_of_slot), so one dot2 per pair multiplies the right rows.
+// pair come out of one register cheaply; rows are those of the tile (0..15). These fp16 weights (the reference's
+// rounding) serve the decoded-weight probe (gfr_exl3_decode_tiles) and, in the K != 2 pairing, the prefill MFMA's A
+// fragments, whose token rows are staged in the same pair order. The decode GEMV uses lane_words / tile_dot below.
 //   K != 2: m = 2l + h  -> rows (2l + 8 + h, 2l + h)             values (8l + j + 2, 8l + j), j = h or 4 + h
 //   K == 2: m = 4v + u  -> rows (r + 2, r), r = 4v + (u&1) + 8(u>>1)  values (16v + j + 8, 16v + j), j = u or 4 + u
 __host__ __device__ constexpr int pair_row(int K, int m, int half) {
