@@ -479,14 +479,15 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
         else wait_vmcnt<0>();
     };
     const int q = lane >> 4;
-    // B fragment b of step s from LDS; the 4 decoded A fragments of step s
-    auto read_b = [&](int s, int b) {
-        const unsigned char* xb = lds + (s % NS) * STAGE + mat * XBUF;
+    // B fragment b from LDS stage buffer `slot`; the 4 decoded A fragments of the step in `slot` (the slot is a
+    // compile-time constant in the unrolled main loop, so the stage offset folds into the LDS instructions)
+    auto read_b = [&](int slot, int b) {
+        const unsigned char* xb = lds + slot * STAGE + mat * XBUF;
         const int row = 16 * b + (lane & 15);
         return *reinterpret_cast<const h8_t*>(xb + row * 64 + ((q ^ ((row >> 1) & 3)) << 4));
     };
-    auto decode_a = [&](int s, h8_t (&af)[4]) {
-        const uint32_t* tw = reinterpret_cast<const uint32_t*>(lds + (s % NS) * STAGE + MATS * XBUF);
+    auto decode_a = [&](int slot, h8_t (&af)[4]) {
+        const uint32_t* tw = reinterpret_cast<const uint32_t*>(lds + slot * STAGE + MATS * XBUF);
         if constexpr (K == 4) {
 #pragma unroll
             for (int t4 = 0; t4 < 4; ++t4) af[t4] = a_fragment4(tw + (stile0 + t4) * 64, lane);
@@ -543,7 +544,7 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
     uint64_t tw = 0;
     const uint64_t tl0 = __builtin_amdgcn_s_memtime();
 #endif
-    auto step = [&](int s, const h8_t (&ac)[4], h8_t (&an)[4]) {
+    auto step = [&](int s, int slot, const h8_t (&ac)[4], h8_t (&an)[4]) {
         // stage s + 1 landed (at most the stages after it in flight) and every wave is done with stage s - 1
 #ifdef GFR_PF_TRACE
         const uint64_t w0 = __builtin_amdgcn_s_memtime();
@@ -554,18 +555,19 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
         tw += __builtin_amdgcn_s_memtime() - w0;
 #endif
         if (s + NS - 1 < S) issue(s + NS - 1);           // into stage s - 1's buffer, now free
-        const int sn = s + 1 < S ? s + 1 : s;             // the last step re-reads its own stage (unused)
+        const int sn = (slot + 1) % NS;                   // the next step's slot (the last step reads a stale one,
+                                                          // unused)
         if constexpr (K == 4) {
             // the next step's decode spread over this step's MFMA groups (sched_barrier keeps each group together,
             // so the VALU of the decode issues while the matrix core works)
-            const uint32_t* twn = reinterpret_cast<const uint32_t*>(lds + (sn % NS) * STAGE + MATS * XBUF);
+            const uint32_t* twn = reinterpret_cast<const uint32_t*>(lds + sn * STAGE + MATS * XBUF);
             uint32_t wp[4], w0[4], w1[4], st[4];
 #pragma unroll
             for (int t4 = 0; t4 < 4; ++t4) frag4_words(twn + (stile0 + t4) * 64, lane, wp[t4], w0[t4], w1[t4]);
 #pragma unroll
             for (int b = 0; b < RB; ++b) {
                 const h8_t bc = ring[b % D];
-                ring[b % D] = b + D < RB ? read_b(s, b + D) : read_b(sn, b + D - RB);
+                ring[b % D] = b + D < RB ? read_b(slot, b + D) : read_b(sn, b + D - RB);
                 if (b < nblk) {
 #pragma unroll
                     for (int t4 = 0; t4 < 4; ++t4)
@@ -586,7 +588,7 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
 #pragma unroll
             for (int b = 0; b < RB; ++b) {
                 const h8_t bc = ring[b % D];
-                ring[b % D] = b + D < RB ? read_b(s, b + D) : read_b(sn, b + D - RB);
+                ring[b % D] = b + D < RB ? read_b(slot, b + D) : read_b(sn, b + D - RB);
                 if (b < nblk) {
 #pragma unroll
                     for (int t4 = 0; t4 < 4; ++t4)
@@ -598,8 +600,19 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
 #pragma unroll
         for (int t4 = 0; t4 < 4; ++t4) __asm__ volatile("" : "+v"(an[t4]));
     };
-    for (int s = 0; s < S; ++s) {
-        step(s, a0, a1);
+    // UNR steps a trip (a multiple of NS and of 2): every stage slot is a constant, and the two fragment sets trade
+    // roles instead of being copied
+    constexpr int UNR = NS % 2 == 0 ? NS : 2 * NS;
+    int s = 0;
+    for (; s + UNR <= S; s += UNR) {
+#pragma unroll
+        for (int u = 0; u < UNR; u += 2) {
+            step(s + u, u % NS, a0, a1);
+            step(s + u + 1, (u + 1) % NS, a1, a0);
+        }
+    }
+    for (; s < S; ++s) {
+        step(s, s % NS, a0, a1);
 #pragma unroll
         for (int t4 = 0; t4 < 4; ++t4) a0[t4] = a1[t4];
     }
