@@ -134,9 +134,10 @@ def _moe_inputs(E_routed, D, N, bits, rows, topk, seed, zipf=False):
     return w, x, lg
 
 
-@pytest.mark.parametrize("rows,zipf", [(1, False), (4, True)])
+@pytest.mark.parametrize("rows,zipf", [(1, False), (4, True), (13, True)])
 def test_experts_run_rows_vs_oracle(gfr, oracle, rows, zipf):
-    """ExpertGpu::run_rows at the C2 / C3 shape (hidden 2048, inter 1536, 64 + 1 EXL3 experts, top-4 + shared)."""
+    """ExpertGpu::run_rows at the C2 / C3 shape (hidden 2048, inter 1536, 64 + 1 EXL3 experts, top-4 + shared); at 13
+    rows the shared expert's members take two programs (chunks of 8)."""
     E, D, N, bits, topk = 64, 2048, 1536, 4, 4
     slots = topk + 1
     w, x, lg = _moe_inputs(E, D, N, bits, rows, topk, 31 + rows, zipf)
