@@ -388,7 +388,7 @@ def test_single_launch_graph_replays(gfr):
     m.status()
 
 
-@pytest.mark.parametrize("bits", [2, 5])
+@pytest.mark.parametrize("bits", [2, 3, 5])
 def test_moe_layer_config5_decode_vs_oracle(gfr, oracle, bits):
     """Config 5's layer shape at bs = 1 (hidden 5120, 160 routed + 1 shared, top-8, inter 1536), K = 2 and 5, through
     the Moe entry point against the oracle (routing exact, output within tolerance)."""
