@@ -300,6 +300,7 @@ int gfr_exl3_grouped_gemv(hipStream_t stream, const uint16_t* x0, const uint16_t
     if (bits < 2 || bits > 5 || (mats != 1 && mats != 2)) return fail(GFR_EINVAL, "bits %d / mats %d", bits, mats);
     if (pairs <= 0 || maxm <= 0 || slots <= 0 || slots > 32 || experts <= 0 || maxu <= 0)
         return fail(GFR_EINVAL, "pairs %d maxm %d slots %d experts %d maxu %d", pairs, maxm, slots, experts, maxu);
+    if (maxm > 64) return fail(GFR_EINVAL, "maxm %d: an expert's members are read one a lane (at most 64)", maxm);
     hipError_t e = gfr::launch_gemv(stream, x0, x1 ? x1 : x0, t0, t1 ? t1 : t0, uids, ucount, members, z, kin, n,
                                     pairs, maxm, slots, experts, bits, mats, maxu);
     if (e != hipSuccess) return hip_fail(e, "grouped gemv");

@@ -153,7 +153,8 @@ int gfr_linear_destroy(gfr_linear* l);
  * Z[((mat * SK + split) * P + pair) * N + n] = sum over split's k of X_mat[pair][k] * W_mat[uids[u]][k][n] for every
  * member pair of every distinct expert u < *ucount with uids[u] < experts; mats = 2 (X0/T0 gate, X1/T1 up) or 1.
  * X [P][kin] fp16 (rotated rows), trellis [experts][kin/16][n/16][8*bits]. SK = gfr_exl3_gemv_splits(kin) is fixed
- * by kin, so a row's result never depends on the other rows. maxu = grid bound on distinct experts. */
+ * by kin, so a row's result never depends on the other rows. maxu = grid bound on distinct experts; members are
+ * read with stride maxm, 0 < maxm <= 64. */
 int gfr_exl3_gemv_splits(int kin);
 int gfr_exl3_grouped_gemv(hipStream_t stream, const uint16_t* x0, const uint16_t* x1, const uint32_t* t0,
                           const uint32_t* t1, const int32_t* uids, const int32_t* ucount, const int32_t* members,

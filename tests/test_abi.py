@@ -66,6 +66,16 @@ def test_run_rejects_null_engine():
     assert L.gfr_exl3_decode_tiles(None, None, 16, 16, 4, None) == gfr_moe.GFR_EINVAL
 
 
+def test_grouped_gemv_rejects_wide_member_stride():
+    # an expert's members are read one a lane: more than 64 would be dropped, so the call refuses them
+    import ctypes
+    import gfr_moe
+    L = gfr_moe.lib()
+    p = ctypes.c_void_p(16)   # never dereferenced: the arguments are checked first
+    rc = L.gfr_exl3_grouped_gemv(None, p, p, p, p, p, p, p, p, 256, 128, 4, 65, 2, 3, 4, 2, 2)
+    assert rc == gfr_moe.GFR_EINVAL and "maxm 65" in L.gfr_last_error().decode()
+
+
 def test_moe_create_rejects():
     import gfr_moe
     h = ctypes.c_void_p()
