@@ -311,7 +311,7 @@ def other_configs(args, copies, stream):
     out["loader"] = {"config": "prepared-weight load of config 2's 65 EXL3 experts (src/prepared.rs format, 16 MiB "
                                "chunks, each SHA-256-checked, file in the page cache)",
                      "bytes": nbytes, "seconds": round(secs, 4), "gbs": round(nbytes / secs / 1e9, 3),
-                     "hash_threads": min(16, os.cpu_count() or 1, nchunks)}
+                     "hash_tasks_in_flight_max": min(2 * min(16, os.cpu_count() or 1), nchunks)}
     return out
 
 

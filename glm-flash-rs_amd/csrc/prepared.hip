@@ -18,6 +18,8 @@
 
 #include <algorithm>
 #include <chrono>
+#include <deque>
+#include <future>
 #include <thread>
 #include <map>
 #include <memory>
@@ -566,11 +568,13 @@ int gfr_prepared_load(gfr_prepared* p, const char* const* prefixes, int nprefixe
             p->host[j].resize(p->storages[j].nbytes);
         }
     }
-    // staging for a batch of chunks, hashed in parallel (one thread a chunk); at most 1 GiB of pinned memory
+    // staging: a ring of pinned chunk slots (at most 1 GiB). The chunks are read in file order; each is hashed in a
+    // task of its own as soon as it is in, and the oldest is checked and copied out when the ring is full, so the
+    // reads, up to 2 * 16 hashes and the copies overlap.
     const unsigned hw = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
-    const uint64_t nbuf = std::max<uint64_t>(1, std::min<uint64_t>(hw, (1ull << 30) / p->chunk));
+    const uint64_t nslot = std::max<uint64_t>(1, std::min<uint64_t>(2 * hw, (1ull << 30) / p->chunk));
     uint8_t* staging = nullptr;
-    if ((e = hipHostMalloc((void**)&staging, nbuf * p->chunk, hipHostMallocDefault)) != hipSuccess) {
+    if ((e = hipHostMalloc((void**)&staging, nslot * p->chunk, hipHostMallocDefault)) != hipSuccess) {
         release(p);
         return gfr::set_error((int)e, std::string("hipHostMalloc: ") + hipGetErrorString(e));
     }
@@ -584,54 +588,55 @@ int gfr_prepared_load(gfr_prepared* p, const char* const* prefixes, int nprefixe
                 return true;
         return false;
     };
-    for (size_t i0 = 0; rc == 0 && i0 < p->chunk_sha256.size();) {
-        // the next batch: up to nbuf needed chunks, read in file order
-        std::vector<size_t> idx;
-        for (size_t i = i0; i < p->chunk_sha256.size() && idx.size() < nbuf; ++i) {
-            i0 = i + 1;
-            const uint64_t off = i * p->chunk, len = std::min(p->file_size - off, p->chunk);
-            if (!needed(off, len)) continue;
-            if (pos != off && fseeko(f, (off_t)off, SEEK_SET) != 0) { rc = err("seek in " + p->data_path); break; }
-            if (fread(staging + idx.size() * p->chunk, 1, len, f) != len) { rc = err("short read of " + p->data_path); break; }
-            pos = off + len;
-            idx.push_back(i);
-        }
-        if (rc) break;
-        std::vector<std::string> got(idx.size());
-        {
-            std::vector<std::thread> th;
-            for (size_t b = 0; b < idx.size(); ++b)
-                th.emplace_back([&, b] {
-                    const uint64_t off = idx[b] * p->chunk, len = std::min(p->file_size - off, p->chunk);
-                    Sha256 h;
-                    h.update(staging + b * p->chunk, len);
-                    got[b] = h.hex();
-                });
-            for (auto& t : th) t.join();
-        }
-        for (size_t b = 0; b < idx.size() && rc == 0; ++b) {
-            const size_t i = idx[b];
-            if (got[b] != p->chunk_sha256[i]) { rc = err("weight hash mismatch in chunk " + std::to_string(i)); break; }
-            const uint64_t offset = i * p->chunk, len = std::min(p->file_size - offset, p->chunk);
-            const uint8_t* data = staging + b * p->chunk;
-            while (first < p->storages.size() && p->storages[first].offset + p->storages[first].nbytes <= offset) ++first;
-            for (size_t j = first; j < p->storages.size(); ++j) {
-                const Storage& s = p->storages[j];
-                if (s.offset >= offset + len) break;
-                if (!sel[j]) continue;
-                const uint64_t lo = std::max(s.offset, offset), hi = std::min(s.offset + s.nbytes, offset + len);
-                if (hi <= lo) continue;
-                const uint8_t* src = data + (lo - offset);
-                if (s.cuda) {
-                    if ((e = hipMemcpy((uint8_t*)p->dev[j] + (lo - s.offset), src, hi - lo, hipMemcpyHostToDevice)) != hipSuccess) {
-                        rc = gfr::set_error((int)e, std::string("hipMemcpy: ") + hipGetErrorString(e));
-                        break;
-                    }
-                } else {
-                    memcpy(p->host[j].data() + (lo - s.offset), src, hi - lo);
-                }
+    struct Pending {
+        size_t chunk;
+        uint8_t* data;
+        std::future<std::string> hash;
+    };
+    std::deque<Pending> q;
+    // the oldest read chunk: its hash checked, then its bytes copied into the storages it overlaps
+    auto retire = [&]() -> int {
+        Pending pd = std::move(q.front());
+        q.pop_front();
+        const std::string got = pd.hash.get();
+        const size_t i = pd.chunk;
+        if (got != p->chunk_sha256[i]) return err("weight hash mismatch in chunk " + std::to_string(i));
+        const uint64_t offset = i * p->chunk, len = std::min(p->file_size - offset, p->chunk);
+        while (first < p->storages.size() && p->storages[first].offset + p->storages[first].nbytes <= offset) ++first;
+        for (size_t j = first; j < p->storages.size(); ++j) {
+            const Storage& s = p->storages[j];
+            if (s.offset >= offset + len) break;
+            if (!sel[j]) continue;
+            const uint64_t lo = std::max(s.offset, offset), hi = std::min(s.offset + s.nbytes, offset + len);
+            if (hi <= lo) continue;
+            const uint8_t* src = pd.data + (lo - offset);
+            if (s.cuda) {
+                const hipError_t ce = hipMemcpy((uint8_t*)p->dev[j] + (lo - s.offset), src, hi - lo, hipMemcpyHostToDevice);
+                if (ce != hipSuccess) return gfr::set_error((int)ce, std::string("hipMemcpy: ") + hipGetErrorString(ce));
+            } else {
+                memcpy(p->host[j].data() + (lo - s.offset), src, hi - lo);
             }
         }
+        return 0;
+    };
+    uint64_t nread = 0;
+    for (size_t i = 0; rc == 0 && i < p->chunk_sha256.size(); ++i) {
+        const uint64_t off = i * p->chunk, len = std::min(p->file_size - off, p->chunk);
+        if (!needed(off, len)) continue;
+        if (q.size() == nslot && (rc = retire())) break;   // slots are freed oldest first: the ring stays in order
+        uint8_t* buf = staging + (nread++ % nslot) * p->chunk;
+        if (pos != off && fseeko(f, (off_t)off, SEEK_SET) != 0) { rc = err("seek in " + p->data_path); break; }
+        if (fread(buf, 1, len, f) != len) { rc = err("short read of " + p->data_path); break; }
+        pos = off + len;
+        q.push_back({i, buf, std::async(std::launch::async, [buf, len] {
+                         Sha256 h;
+                         h.update(buf, len);
+                         return h.hex();
+                     })});
+    }
+    while (!q.empty()) {                        // every hash task is joined, also after an error
+        if (rc) { q.front().hash.wait(); q.pop_front(); continue; }
+        rc = retire();
     }
     if (f) fclose(f);
     (void)hipHostFree(staging);
