@@ -782,6 +782,12 @@ constexpr int PF_SPLIT_PAIRS = PF_SPLIT_PAIRS_MAX;
 constexpr int PF_SPLIT_K = 512;
 constexpr int PF_SPLIT_BM = 32;
 static bool split_ok(int hidden, int inter) { return hidden % PF_SPLIT_K == 0 && inter % PF_SPLIT_K == 0; }
+static_assert(PF_SPLIT_BM <= PF_BM && PF_SPLIT_BM <= PF_BM4, "items are bounded at the smallest item size");
+// The most items a window of P pairs over at most maxu distinct experts can plan, at any item size the engine uses.
+static size_t item_bound(size_t P, size_t maxu) {
+    const size_t b = P / PF_SPLIT_BM + maxu;
+    return b < P ? b : P;
+}
 
 hipError_t prefill_create(gfr_fast_experts** out, int hidden, int inter, int slots, int exl3_slots, int experts,
                           int max_rows) {
@@ -789,7 +795,9 @@ hipError_t prefill_create(gfr_fast_experts** out, int hidden, int inter, int slo
                                                 nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
                                                 nullptr, nullptr};
     const size_t P = (size_t)max_rows * slots;
-    const size_t max_items = P / PF_BM + PF_MAXU + 1;
+    // items = sum over experts of ceil(members / bm) <= min(P, P / bm + distinct experts), largest at the smallest
+    // item size (the split-K programs' PF_SPLIT_BM rows)
+    const size_t max_items = item_bound(P, PF_MAXU) + 1;
     hipError_t e;
     if ((e = hipMalloc(&fx->xg, P * hidden * 2)) != hipSuccess || (e = hipMalloc(&fx->xu, P * hidden * 2)) != hipSuccess ||
         (e = hipMalloc(&fx->xd, P * inter * 2)) != hipSuccess || (e = hipMalloc(&fx->out, P * hidden * 4)) != hipSuccess ||
@@ -881,7 +889,9 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
                                                fx->plan);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    const int max_items = P / bm + maxu;
+    // grid bound on the plan's items (sum of ceil(members / bm) <= min(P, P / bm + maxu)); the allocation holds
+    // item_bound(max P, PF_MAXU), which is at least this
+    const int max_items = P / bm + maxu < P ? P / bm + maxu : P;
     PrefillArgs a{};
 #ifdef GFR_PF_TRACE
     a.trace = fx->trace;

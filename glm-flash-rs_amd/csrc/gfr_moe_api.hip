@@ -103,14 +103,8 @@ struct gfr_moe {
     gfr_grouping* group_pre;   // member stride = max_rows (prefill chunks)
     gfr_experts* dec;
     gfr_fast_experts* pre;
-    uint32_t* tok_sync;        // the one-launch token layer's counters / flags (nullptr: shape not supported)
-    int tok_grid[6];           // its grid a bit width: min(units, resident workgroups)
     const float* route_bias;   // the router's gate (gfr_moe_set_router): nullptr = softmax
     float route_scale;
-    int single_launch;         // rows == 1 runs the one-launch layer (default on when the shape allows)
-#ifdef GFR_TOKEN_TRACE
-    uint64_t* tok_trace;
-#endif
 };
 
 extern "C" {
@@ -180,13 +174,14 @@ int experts_run(gfr_experts* ex, hipStream_t stream, const gfr_exl3_experts* w, 
                                        route)) !=
         hipSuccess)
         return hip_fail(e, "gate/up gemv");
-    if ((e = gfr::launch_expert_down(stream, ex->zgu, D, w->svh_g, w->svh_u, w->suh_d, 10.f, ex->xd, w->dt, ids,
-                                     count, members, ex->zd, N, P, rows, maxm, ex->slots, w->experts, w->bits,
-                                     maxu)) !=
-        hipSuccess)
+    const int skgu = gfr::gemv_gateup_splits(D);
+    if ((e = gfr::launch_expert_down(stream, ex->zgu, D, skgu, w->svh_g, w->svh_u, w->suh_d, 10.f, ex->xd, w->dt,
+                                     w->svh_d,
+                                     ids, count, members, ex->zd, N, P, rows, maxm, ex->slots, w->experts, w->bits,
+                                     maxu)) != hipSuccess)
         return hip_fail(e, "down gemv");
-    if ((e = gfr::launch_down_finish(stream, ex->zd, picks, w->svh_d, ex->y, rows, P, D, gfr::gemv_down_splits(N),
-                                     ex->slots, ex->exl3_slots, weights, out)) != hipSuccess)
+    if ((e = gfr::launch_sum_finish(stream, ex->zd, ex->y, rows, P, D, gfr::gemv_down_splits(N), ex->slots,
+                                    ex->exl3_slots, weights, out)) != hipSuccess)
         return hip_fail(e, "down epilogue");
     return 0;
 }
@@ -413,10 +408,9 @@ int gfr_moe_create(gfr_moe** out, int hidden, int inter, int routed, int topk, i
     const int dec_cap = 64 < max_rows ? 64 : max_rows;
     gfr_moe* m = new gfr_moe{hidden, inter, routed, topk, topk + 1, max_rows,
                              MOE_DECODE_ROWS < max_rows ? MOE_DECODE_ROWS : max_rows,
-                             nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, {0}, 0};
+                             nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 1.f};
     m->route_bias = nullptr;   // the softmax gate until gfr_moe_set_router
     m->route_scale = 1.f;
-    m->single_launch = 0;
     const size_t P = (size_t)max_rows * m->slots;
     if ((rc = alloc_zero(&m->weights, P, "moe weights")) || (rc = alloc_zero(&m->picks, P, "moe picks")) ||
         (rc = alloc_zero(&m->out, (size_t)max_rows * hidden, "moe output")) ||
@@ -424,33 +418,6 @@ int gfr_moe_create(gfr_moe** out, int hidden, int inter, int routed, int topk, i
         (rc = gfr_experts_create(&m->dec, hidden, inter, m->slots, m->slots, dec_cap))) {
         gfr_moe_destroy(m);
         return rc;
-    }
-    if (gfr::token_shape_ok(hidden, inter) && m->slots <= gfr::token_max_slots()) {
-        // one-launch token layer: grid = its work units, capped at the workgroups the GPU holds at once (a
-        // workgroup may wait for units of others, which must therefore all be resident)
-        int dev = 0, cus = 0;
-        hipError_t e;
-        if ((e = hipGetDevice(&dev)) != hipSuccess ||
-            (e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) {
-            gfr_moe_destroy(m);
-            return hip_fail(e, "device attributes");
-        }
-        const int units = gfr::token_units(m->slots, hidden, inter);
-        for (int b = 2; b <= 5; ++b) {
-            const int cap = gfr::token_blocks_per_cu(b) * cus;
-            m->tok_grid[b] = units < cap ? units : cap;
-        }
-        if ((rc = alloc_zero(&m->tok_sync, gfr::token_sync_words(m->slots, hidden, inter), "token sync"))) {
-            gfr_moe_destroy(m);
-            return rc;
-        }
-        m->single_launch = 0;      // measured slower than three launches on MI355X; kept selectable
-#ifdef GFR_TOKEN_TRACE
-        if ((rc = alloc_zero(&m->tok_trace, (size_t)units * 16, "token trace"))) {
-            gfr_moe_destroy(m);
-            return rc;
-        }
-#endif
     }
     if (max_rows > m->decode_rows &&
         ((rc = gfr_grouping_create(&m->group_pre, routed + 1, m->slots, max_rows)) ||
@@ -485,26 +452,6 @@ int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const
     hipError_t e;
     if (rows <= m->decode_rows) {
         gfr_grouping* g = m->group_dec;
-        if (rows == 1 && m->single_launch) {
-            // one launch: route, gate/up, gate/up epilogue, down, down epilogue, combine
-            gfr::TokenArgs a{};
-            gfr_experts* ex = m->dec;
-            a.x = input; a.logits = logits; a.route_bias = m->route_bias; a.route_scale = m->route_scale;
-            a.routed = m->routed; a.slots = m->slots; a.D = m->hidden;
-            a.N = m->inter; a.E = w->experts; a.limit = 10.f;
-            a.gt = w->gt; a.ut = w->ut; a.dt = w->dt;
-            a.suh_g = w->suh_g; a.suh_u = w->suh_u; a.suh_d = w->suh_d;
-            a.svh_g = w->svh_g; a.svh_u = w->svh_u; a.svh_d = w->svh_d;
-            a.zgu = ex->zgu; a.xd = ex->xd; a.zd = ex->zd; a.y = ex->y; a.out = m->out;
-            a.pick_out = m->picks; a.weight_out = m->weights; a.ids_out = g->ids; a.count_out = g->count;
-            a.members_out = g->members; a.maxm = g->max_rows; a.sync = m->tok_sync; a.grid = m->tok_grid[w->bits];
-            if (a.grid <= 0) return fail(GFR_EUNSUPPORTED, "one-launch token layer: no residency for %d bits", w->bits);
-#ifdef GFR_TOKEN_TRACE
-            a.trace = m->tok_trace;
-#endif
-            if ((e = gfr::launch_moe_token(stream, a, w->bits)) != hipSuccess) return hip_fail(e, "token layer");
-            return 0;
-        }
         if (rows == 1) {
             // three launches: gate/up (+ route, rotation), down (+ gate/up epilogue), down epilogue (+ combine)
             const gfr::RouteOne r{logits, m->route_bias, m->route_scale, m->routed, m->picks, m->weights, g->ids,
@@ -560,28 +507,6 @@ int gfr_moe_set_router(gfr_moe* m, const float* bias, float scale) {
     return 0;
 }
 
-int gfr_moe_set_single_launch(gfr_moe* m, int enable) {
-    if (!m) return fail(GFR_EINVAL, "null moe");
-    if (enable && !m->tok_sync)
-        return fail(GFR_EUNSUPPORTED, "one-launch token layer needs hidden %% 512 == 0, inter %% 256 == 0, slots <= 16");
-    m->single_launch = enable ? 1 : 0;
-    return 0;
-}
-
-int gfr_moe_status(gfr_moe* m) {
-    if (!m) return fail(GFR_EINVAL, "null moe");
-    if (!m->tok_sync) return 0;
-    uint32_t errw = 0;
-    hipError_t e = hipMemcpy(&errw, m->tok_sync + 3, 4, hipMemcpyDeviceToHost);
-    if (e != hipSuccess) return hip_fail(e, "status read");
-    if (errw) return fail(GFR_ESTALL, "one-launch token layer: a ready flag never came (error word %u)", errw);
-    return 0;
-}
-
-#ifdef GFR_TOKEN_TRACE
-uint64_t* gfr_moe_token_trace(const gfr_moe* m) { return m->tok_trace; }
-#endif
-
 float* gfr_moe_output(const gfr_moe* m) { return m ? m->out : nullptr; }
 int32_t* gfr_moe_picks(const gfr_moe* m) { return m ? m->picks : nullptr; }
 float* gfr_moe_weights(const gfr_moe* m) { return m ? m->weights : nullptr; }
@@ -592,7 +517,7 @@ int gfr_moe_destroy(gfr_moe* m) {
     gfr_grouping_destroy(m->group_pre);
     gfr_experts_destroy(m->dec);
     gfr_fast_experts_destroy(m->pre);
-    free_all({m->weights, m->picks, m->out, m->tok_sync});
+    free_all({m->weights, m->picks, m->out});
     delete m;
     return 0;
 }

@@ -29,9 +29,10 @@ hipError_t launch_gemv(hipStream_t s, const uint16_t* X0, const uint16_t* X1, co
                        const int* uids, const int* ucount, const int* members, float* Z, int Kin, int N, int P,
                        int maxm, int slots, int E, int bits, int mats, int maxu);
 int gemv_gateup_splits(int D);  // K splits of the decode gate/up GEMV (one 128-block a wave, 4 waves)
-int gemv_down_splits(int N);    // K splits of the decode down GEMV (one 128-block a wave, 2 waves)
+int gemv_down_splits(int N);    // k-block parts of the decode down GEMV (one a 128-k block)
 // Decode path: gate/up GEMV with rot_in fused (-> gate/up split partials Zgu [2][SK][P][N]); down GEMV with the
-// gate/up epilogue fused as its activation source (-> Zd [SK][P][D], xd [P][N]); down epilogue + combine.
+// gate/up epilogue fused as its activation source and the down epilogue's transform applied to each k-block part
+// (-> Zd [N / 128][P][D], xd [P][N]); the parts' sum + combine.
 // The gate/up GEMV needs gemv_gateup_splits(D) <= 4.
 // One-token windows can route inside the gate/up launch: the token's logits, and where to store its picks /
 // weights and the window's grouping (ids, count, members with stride maxm) for the later launches.
@@ -50,10 +51,16 @@ hipError_t launch_expert_gateup(hipStream_t s, const uint16_t* x, int x_stride, 
                                 const uint16_t* suh_u, const uint32_t* gt, const uint32_t* ut, const int* uids,
                                 const int* ucount, const int* members, float* Zgu, int D, int N, int P, int rows,
                                 int maxm, int slots, int E, int bits, int maxu, const RouteOne* route);
-hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, const uint16_t* svh_g, const uint16_t* svh_u,
-                              const uint16_t* suh_d, float limit, uint16_t* xd, const uint32_t* dt, const int* uids,
-                              const int* ucount, const int* members, float* Zd, int N, int P, int rows, int maxm,
-                              int slots, int E, int bits, int maxu);
+// SKgu: the gate/up partials' K splits (gemv_gateup_splits)
+hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, int SKgu, const uint16_t* svh_g,
+                              const uint16_t* svh_u, const uint16_t* suh_d, float limit, uint16_t* xd,
+                              const uint32_t* dt, const uint16_t* svh_d, const int* uids, const int* ucount,
+                              const int* members, float* Zd, int N, int P, int rows, int maxm, int slots, int E,
+                              int bits, int maxu);
+// Finish of the decode path: Zd's transformed k-block parts [N / 128][P][D] added in order -> y; with weights the
+// slot-ordered combine -> out
+hipError_t launch_sum_finish(hipStream_t s, const float* Zd, float* y, int rows, int P, int D, int SK, int slots,
+                             int exl3_slots, const float* weights, float* out);
 // one fp16 row through one linear with the input rotation fused (partials for down_epilogue)
 int gemv_linear_splits(int kin);
 hipError_t launch_linear_fused(hipStream_t s, const uint16_t* x, const uint16_t* suh, const uint32_t* trellis,
@@ -69,39 +76,6 @@ hipError_t launch_gateup_epilogue(hipStream_t s, const float* Z, const int* pick
 hipError_t launch_down_epilogue(hipStream_t s, const float* Z, const int* pick, const uint16_t* svh_d, float* y,
                                 int P, int D, int SK, int slots, int exl3_slots);
 
-// One-token MoE layer in one persistent launch (moe_token_kernel): the arguments, the sync words it needs (zero at
-// creation, never cleared by the host), its work units, the shapes it takes (hidden % 512, inter % 256) and its
-// residency (its grid must fit on the GPU at once: a workgroup may wait for another's results).
-struct TokenArgs {
-    const uint16_t* x;        // the token, bf16 [D]
-    const float* logits;      // [routed]
-    const float* route_bias;  // the gate (route.hpp RouteGate): nullptr = softmax
-    float route_scale;
-    int routed, slots, D, N, E;
-    float limit;
-    const uint32_t *gt, *ut, *dt;
-    const uint16_t *suh_g, *suh_u, *suh_d, *svh_g, *svh_u, *svh_d;
-    float* zgu;               // [2][SKgu][slots][N]
-    uint16_t* xd;             // [slots][N]
-    float* zd;                // [SKd][slots][D]
-    float* y;                 // [slots][D]
-    float* out;               // [D]
-    int* pick_out;            // picks / weights [slots]; the window's ids / count / members (stride maxm)
-    float* weight_out;
-    int* ids_out;
-    int* count_out;
-    int* members_out;
-    int maxm;
-    uint32_t* sync;           // token_sync_words(slots, D, N) words, zero at creation
-    int grid;                 // at most the workgroups the GPU holds at once (token_blocks_per_cu * CUs)
-    uint64_t* trace;          // GFR_TOKEN_TRACE builds only: per-workgroup timestamps [grid][16]
-};
-int token_sync_words(int slots, int D, int N);
-int token_units(int slots, int D, int N);
-bool token_shape_ok(int D, int N);
-int token_max_slots();
-int token_blocks_per_cu(int bits);   // resident 256-thread workgroups a CU (0: unknown width)
-hipError_t launch_moe_token(hipStream_t s, const TokenArgs& a, int bits);
 
 // router.hip
 // bias == nullptr: the softmax gate; else GLM's sigmoid + bias gate with weights times scale (route.hpp RouteGate)

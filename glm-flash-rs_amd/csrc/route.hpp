@@ -20,18 +20,39 @@ struct RouteGate {
 };
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
 
-// One wave (64 lanes) routes one token into registers: lane s < topk holds the s-th pick and its weight, lane topk
-// the shared expert (weight 1). Lane l holds logits l, l + 64, ... (PER of them); k rounds of a wave-wide max (DPP /
-// permlane, no LDS) whose winner is the lowest id holding it (a ballot per register, lowest set lane).
+// The router's inputs of one token in registers: lane l holds logits l, l + 64, ... (PER of them), and with GLM's gate
+// the matching biases. Loading them is split from the selection so that a caller can issue other loads in between.
 template <int PER>
-__device__ __forceinline__ void route_token_per(const float* __restrict__ l, int E, int topk, int shared_id,
-                                                int& pick, float& weight, RouteGate g) {
+struct RouteIn {
+    float l[PER];
+    float b[PER];
+};
+// Every load is issued by every lane (clamped index, the logits standing in for a missing bias), so that the number of
+// loads in flight is the same on every path and a caller's later waits need not be conservative.
+template <int PER>
+__device__ __forceinline__ void route_load(const float* __restrict__ l, int E, RouteGate g, RouteIn<PER>& in) {
+    const int lane = threadIdx.x & 63;
+    const float* bias = g.bias ? g.bias : l;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int e = j * 64 + lane < E ? j * 64 + lane : E - 1;
+        in.l[j] = l[e];
+        in.b[j] = bias[e];
+    }
+}
+
+// One wave (64 lanes) routes one token into registers: lane s < topk holds the s-th pick and its weight, lane topk
+// the shared expert (weight 1). k rounds of a wave-wide max (DPP / permlane, no LDS) whose winner is the lowest id
+// holding it (a ballot per register, lowest set lane).
+template <int PER>
+__device__ __forceinline__ void route_pick(const RouteIn<PER>& in, const float* __restrict__ l, int E, int topk,
+                                           int shared_id, int& pick, float& weight, RouteGate g) {
     const int lane = threadIdx.x & 63;
     float v[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
         const int e = j * 64 + lane;
-        v[j] = e < E ? (g.bias ? sigmoidf_(l[e]) + g.bias[e] : l[e]) : -__builtin_inff();
+        v[j] = e < E ? (g.bias ? sigmoidf_(in.l[j]) + in.b[j] : in.l[j]) : -__builtin_inff();
     }
     float my_v = 0.f;                                  // lane s < topk: the s-th pick's logit and id
     int my_e = 0;
@@ -70,6 +91,14 @@ __device__ __forceinline__ void route_token_per(const float* __restrict__ l, int
     float sum = 0.f;
     for (int s = 0; s < topk; ++s) sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), s));
     weight = lane < topk ? ex / sum : 1.f;
+}
+
+template <int PER>
+__device__ __forceinline__ void route_token_per(const float* __restrict__ l, int E, int topk, int shared_id,
+                                                int& pick, float& weight, RouteGate g) {
+    RouteIn<PER> in;
+    route_load<PER>(l, E, g, in);
+    route_pick<PER>(in, l, E, topk, shared_id, pick, weight, g);
 }
 
 __device__ __forceinline__ void route_token_regs(const float* __restrict__ l, int E, int topk, int shared_id,

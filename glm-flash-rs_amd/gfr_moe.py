@@ -58,7 +58,7 @@ def _load() -> ctypes.CDLL:
         "gfr_moe_picks": ([VP], P),
         "gfr_moe_weights": ([VP], P),
         "gfr_moe_set_decode_rows": ([VP, I], I),
-        "gfr_moe_set_single_launch": ([VP, I], I), "gfr_moe_status": ([VP], I),
+
         "gfr_moe_destroy": ([VP], I),
         "gfr_linear_create": ([ctypes.POINTER(VP), I, I, I], I),
         "gfr_linear_run": ([VP, P, P, P, P, P, P], I),
@@ -297,14 +297,6 @@ class Moe(_Engine):
         [routed]; None: back to the softmax gate. The tensor must outlive the runs."""
         self._router_bias = bias
         _check(lib().gfr_moe_set_router(self._h, _ptr(bias), float(scale) if bias is not None else 1.0))
-
-    def set_single_launch(self, enable: bool):
-        """rows == 1 as one persistent launch (default where the shape allows) or as three launches."""
-        _check(lib().gfr_moe_set_single_launch(self._h, int(enable)))
-
-    def status(self):
-        """Raises GfrError if a one-launch layer ever gave up waiting for an activation block (synchronous)."""
-        _check(lib().gfr_moe_status(self._h))
 
     def run(self, w: Exl3Experts, input: torch.Tensor, logits: torch.Tensor, rows: int, stream=None):
         ws = w.struct()

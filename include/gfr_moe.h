@@ -29,7 +29,6 @@ extern "C" {
 #define GFR_EINVAL (-1)   /* argument outside the engine's bounds (the reference's ensure!) */
 #define GFR_ENOMEM (-2)
 #define GFR_EUNSUPPORTED (-3)
-#define GFR_ESTALL (-4)        /* the one-launch token layer gave up waiting (see gfr_moe_status) */
 
 /* One layer's EXL3 expert tensors, the reference's weights.layers[L].moe.experts.{gt,ut,dt,suh_*,svh_*}
  * (experts.rs:146-156, prepared.rs:369-377), generalised to any shape and bit width:
@@ -117,16 +116,11 @@ float* gfr_moe_output(const gfr_moe* m);
 int32_t* gfr_moe_picks(const gfr_moe* m);        /* [rows][topk + 1] */
 float* gfr_moe_weights(const gfr_moe* m);        /* [rows][topk + 1] */
 int gfr_moe_set_decode_rows(gfr_moe* m, int decode_rows);  /* rows at or below run the decode path (default 4, max 64) */
-/* rows == 1 as one persistent launch (route .. combine; default on when hidden % 512 == 0 and inter % 256 == 0) or
- * as three launches (gate/up + route, down + gate/up epilogue, down epilogue + combine); both give the same bits.
- * No counterpart in the reference, whose decode layer is a captured graph of separate launches (model.rs:634). */
+/* rows == 1 runs three launches: gate/up GEMV (router and input rotation fused), down GEMV (gate/up epilogue fused),
+ * sum of the down parts + combine. */
 /* The layer's router gate: bias == NULL (default) the softmax gate of gfr_route_topk; else GLM's gate of
  * gfr_route_topk_biased with this bias [routed] (device, fp32; must outlive the runs) and scale (2.5 for GLM). */
 int gfr_moe_set_router(gfr_moe* m, const float* bias, float scale);
-int gfr_moe_set_single_launch(gfr_moe* m, int enable);
-/* Synchronous check of the one-launch layer's error word: GFR_ESTALL if a launch ever waited past its bound
- * for an activation block (results of that launch are invalid), else 0. */
-int gfr_moe_status(gfr_moe* m);
 int gfr_moe_destroy(gfr_moe* m);
 
 /* ---- The router alone (the reference's Triton topk, moe.rs:89-100; source absent, semantics of the benchmark):

@@ -323,71 +323,6 @@ def test_route_vs_oracle(gfr, oracle, rows, E, topk):
     np.testing.assert_allclose(w.cpu().numpy(), wt, rtol=2e-6, atol=1e-7)
 
 
-def _token_outputs(m, g_ids=None):
-    return (m.output[0].clone(), m.picks[0].clone(), m.weights[0].clone())
-
-
-@pytest.mark.parametrize("E,D,N,topk,bits", [(64, 2048, 1536, 4, 4), (16, 5120, 1536, 8, 2), (16, 5120, 1536, 8, 3),
-                                              (16, 5120, 1536, 8, 5), (8, 512, 768, 2, 4)])
-def test_single_launch_layer_equals_three_launches(gfr, E, D, N, topk, bits):
-    """The one-launch token layer gives the three-launch path's bits (same wave / split / slot order), at the C2
-    shape, C5's shape and bit widths, and an odd down-split count (inter 768: 3 splits)."""
-    import synth
-    w = synth.experts(E + 1, D, N, bits, seed=40 + bits)
-    xs = synth.activations(4, D, 41)
-    lgs = synth.logits(4, E, 42)
-    m = gfr.Moe(D, N, E, topk, 1)
-    for j in range(4):
-        m.set_single_launch(False)
-        m.run(w, xs[j:j + 1], lgs[j:j + 1], 1)
-        torch.cuda.synchronize()
-        three = _token_outputs(m)
-        m.output.fill_(float("nan"))
-        m.set_single_launch(True)
-        m.run(w, xs[j:j + 1], lgs[j:j + 1], 1)
-        torch.cuda.synchronize()
-        m.status()
-        one = _token_outputs(m)
-        assert torch.isfinite(one[0]).all()
-        for a, b in zip(one, three):
-            assert torch.equal(a, b), (j, D, bits)
-
-
-def test_single_launch_graph_replays(gfr):
-    """Captured one-launch layers replayed many times (its flags advance a generation each launch), interleaved
-    with eager launches, always give the eager bytes."""
-    import synth
-    E, D, N, bits, topk = 64, 2048, 1536, 4, 4
-    ws = [synth.experts(E + 1, D, N, bits, seed=s) for s in (5, 6)]
-    x = synth.activations(2, D, 7)
-    lg = synth.logits(2, E, 8)
-    m = gfr.Moe(D, N, E, topk, 1)
-    m.set_single_launch(True)
-    s = torch.cuda.Stream()
-    eager = []
-    with torch.cuda.stream(s):
-        for j in range(2):
-            m.run(ws[j], x[j:j + 1], lg[j:j + 1], 1, stream=s)
-            s.synchronize()
-            eager.append(m.output.clone())
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=s):
-            m.run(ws[0], x[0:1], lg[0:1], 1, stream=s)
-            m.run(ws[1], x[1:2], lg[1:2], 1, stream=s)
-    for rep in range(20):
-        m.output.zero_()
-        torch.cuda.synchronize()
-        with torch.cuda.stream(s):
-            graph.replay()
-        torch.cuda.synchronize()
-        assert torch.equal(m.output, eager[1]), rep
-        if rep % 5 == 4:
-            m.run(ws[0], x[0:1], lg[0:1], 1)
-            torch.cuda.synchronize()
-            assert torch.equal(m.output, eager[0]), rep
-    m.status()
-
-
 @pytest.mark.parametrize("bits", [2, 3, 5])
 def test_moe_layer_config5_decode_vs_oracle(gfr, oracle, bits):
     """Config 5's layer shape at bs = 1 (hidden 5120, 160 routed + 1 shared, top-8, inter 1536), K = 2 and 5, through
@@ -438,17 +373,15 @@ def test_route_biased_vs_oracle(gfr, oracle, rows, E, topk):
     _check_biased(oracle, picks, weights, logits, bias, topk, E)
 
 
-@pytest.mark.parametrize("rows,single", [(1, False), (1, True), (3, False), (32, False)])
-def test_moe_layer_biased_router_vs_oracle(gfr, oracle, rows, single):
-    """A Moe layer with GLM's gate on every routing path: the router fused into the bs = 1 gate/up GEMV, the one-launch
-    layer, the decode window's route + group launch and the split-K window's route + group + plan launch."""
+@pytest.mark.parametrize("rows", [1, 3, 32])
+def test_moe_layer_biased_router_vs_oracle(gfr, oracle, rows):
+    """A Moe layer with GLM's gate on every routing path: the router fused into the bs = 1 gate/up GEMV, the decode
+    window's route + group launch and the split-K window's route + group + plan launch."""
     E, D, N, bits, topk = 64, 2048, 1536, 4, 4
     w, x, _ = _moe_inputs(E, D, N, bits, rows, topk, 90 + rows)
     logits, bias = _biased_inputs(rows, E, 95 + rows)
     m = gfr.Moe(D, N, E, topk, rows)
     m.set_router(bias, 2.5)
-    if rows == 1:
-        m.set_single_launch(single)
     m.run(w, x, logits, rows)
     torch.cuda.synchronize()
     p, wt = _check_biased(oracle, m.picks[:rows], m.weights[:rows], logits, bias, topk, E)
