@@ -528,12 +528,26 @@ __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
     GEMV_MARK(1, tslot, 5);
 }
 
+// The combine's terms past the EXL3 slots (the reference's combine(y, shared, weights, out), moe.rs:171-181): the
+// caller's shared-expert output for each slot s >= exl3_slots, weighted, after the EXL3 slots (slot order).
+__device__ __forceinline__ void combine_shared(const float* __restrict__ w, int slots, int exl3_slots,
+                                               const float* __restrict__ shared, int shared_stride, int row, int n,
+                                               float& o0, float& o1) {
+    if (!shared) return;
+    for (int s = exl3_slots; s < slots; ++s) {
+        const float2 v = *reinterpret_cast<const float2*>(shared + (size_t)row * shared_stride + n);
+        o0 += w[s] * v.x;
+        o1 += w[s] * v.y;
+    }
+}
+
 // Finish of the decode path: y[p] = the k-block parts of the down epilogue (Zd, already transformed and scaled) added
 // in order; with weights, out[row] = the token's slots in order, weighted. Program (token row, 128-column block), one
 // wave a slot (up to 16 at a time).
 __global__ void __launch_bounds__(1024) sum_finish_kernel(const float* __restrict__ Z, float* __restrict__ y, int P,
                                                            int D, int SK, int slots, int exl3_slots,
                                                            const float* __restrict__ weights,
+                                                           const float* __restrict__ shared, int shared_stride,
                                                            float* __restrict__ out) {
     __shared__ float2 ys[16][64];
     const int row = blockIdx.x, blk = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -574,7 +588,10 @@ __global__ void __launch_bounds__(1024) sum_finish_kernel(const float* __restric
             __syncthreads();
         }
     }
-    if (weights && wave == 0) *reinterpret_cast<float2*>(out + (size_t)row * D + n) = make_float2(o0, o1);
+    if (weights && wave == 0) {
+        combine_shared(weights + (size_t)row * slots, slots, exl3_slots, shared, shared_stride, row, n, o0, o1);
+        *reinterpret_cast<float2*>(out + (size_t)row * D + n) = make_float2(o0, o1);
+    }
     GEMV_MARK(2, tslot, 5);
 }
 
@@ -585,6 +602,7 @@ __global__ void __launch_bounds__(1024) down_finish_kernel(const float* __restri
                                                             const uint16_t* __restrict__ svh_d, float* __restrict__ y,
                                                             int P, int D, int SK, int slots, int exl3_slots,
                                                             const float* __restrict__ weights,
+                                                            const float* __restrict__ shared, int shared_stride,
                                                             float* __restrict__ out) {
     __shared__ float2 ys[16][64];
     const int row = blockIdx.x, blk = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -630,7 +648,10 @@ __global__ void __launch_bounds__(1024) down_finish_kernel(const float* __restri
             __syncthreads();
         }
     }
-    if (weights && wave == 0) *reinterpret_cast<float2*>(out + (size_t)row * D + n) = make_float2(o0, o1);
+    if (weights && wave == 0) {
+        combine_shared(weights + (size_t)row * slots, slots, exl3_slots, shared, shared_stride, row, n, o0, o1);
+        *reinterpret_cast<float2*>(out + (size_t)row * D + n) = make_float2(o0, o1);
+    }
     GEMV_MARK(2, tslot, 5);
 }
 
@@ -848,9 +869,11 @@ hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, int SKgu, 
 }
 
 hipError_t launch_sum_finish(hipStream_t s, const float* Zd, float* y, int rows, int P, int D, int SK, int slots,
-                             int exl3_slots, const float* weights, float* out) {
+                             int exl3_slots, const float* weights, const float* shared, int shared_stride,
+                             float* out) {
     const int nwv = exl3_slots < 16 ? (exl3_slots > 0 ? exl3_slots : 1) : 16;
-    sum_finish_kernel<<<dim3(rows, D / 128), 64 * nwv, 0, s>>>(Zd, y, P, D, SK, slots, exl3_slots, weights, out);
+    sum_finish_kernel<<<dim3(rows, D / 128), 64 * nwv, 0, s>>>(Zd, y, P, D, SK, slots, exl3_slots, weights, shared,
+                                                               shared_stride, out);
     return hipGetLastError();
 }
 
@@ -882,10 +905,10 @@ hipError_t launch_linear_fused(hipStream_t s, const uint16_t* x, const uint16_t*
 
 hipError_t launch_down_finish(hipStream_t s, const float* Zd, const int* pick, const uint16_t* svh_d, float* y,
                               int rows, int P, int D, int SK, int slots, int exl3_slots, const float* weights,
-                              float* out) {
+                              const float* shared, int shared_stride, float* out) {
     const int nwv = exl3_slots < 16 ? (exl3_slots > 0 ? exl3_slots : 1) : 16;
     down_finish_kernel<<<dim3(rows, D / 128), 64 * nwv, 0, s>>>(Zd, pick, svh_d, y, P, D, SK, slots, exl3_slots,
-                                                                weights, out);
+                                                                weights, shared, shared_stride, out);
     return hipGetLastError();
 }
 

@@ -851,7 +851,7 @@ static hipError_t launch_gemm(int bits, dim3 grid, hipStream_t s, const PrefillA
 hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_experts* w, const uint16_t* input,
                        int input_stride, const int* picks, const int* ids, const int* count, const int* members,
                        int rows, int maxm, bool shared_x, const float* combine_weights, float* combine_out,
-                       bool* combined, bool planned) {
+                       bool* combined, bool planned, const float* combine_shared, int shared_stride) {
     const PrefillDims& d = fx->d;
     if (combined) *combined = false;
     if (w->bits < 2 || w->bits > 5) return hipErrorInvalidValue;
@@ -914,7 +914,7 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
             // the down epilogue and the layer's slot-ordered combine in one launch (the decode path's finish)
             if (combined) *combined = true;
             return launch_down_finish(s, fx->zd, picks, w->svh_d, fx->out, rows, P, d.hidden, skd, d.slots,
-                                      d.exl3_slots, combine_weights, combine_out);
+                                      d.exl3_slots, combine_weights, combine_shared, shared_stride, combine_out);
         }
         return launch_down_epilogue(s, fx->zd, picks, w->svh_d, fx->out, P, d.hidden, skd, d.slots, d.exl3_slots);
     }

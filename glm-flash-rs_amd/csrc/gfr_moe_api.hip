@@ -105,6 +105,9 @@ struct gfr_moe {
     gfr_fast_experts* pre;
     const float* route_bias;   // the router's gate (gfr_moe_set_router): nullptr = softmax
     float route_scale;
+    int shared_exl3;           // 1: the shared expert is EXL3 (weights hold routed + 1 experts); 0: its output is the
+                               // caller's (gfr_moe_run_shared), weights hold the routed experts only
+    float* logits;             // [max_rows][routed] router logits of gfr_moe_run_router
 };
 
 extern "C" {
@@ -116,7 +119,8 @@ const char* gfr_version(void) { return "gfr_moe 0.1 gfx950"; }
 int gfr_grouping_create(gfr_grouping** out, int experts, int slots, int max_rows) {
     if (!out) return fail(GFR_EINVAL, "null out");
     *out = nullptr;
-    if (experts <= 0 || experts > 4096) return fail(GFR_EINVAL, "grouping experts %d outside 1..4096", experts);
+    // the large path keeps an 8-word bitmap row per expert in LDS (64 KiB at 2048 experts)
+    if (experts <= 0 || experts > 2048) return fail(GFR_EINVAL, "grouping experts %d outside 1..2048", experts);
     if (slots <= 0 || slots > 32) return fail(GFR_EINVAL, "grouping slots %d outside 1..32", slots);
     if (max_rows <= 0 || max_rows > (1 << 20)) return fail(GFR_EINVAL, "grouping capacity %d", max_rows);
     gfr_grouping* g = new gfr_grouping{experts, slots, max_rows, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
@@ -138,7 +142,8 @@ int gfr_grouping_run(gfr_grouping* g, hipStream_t stream, const int32_t* picks, 
     if (!g || !picks) return fail(GFR_EINVAL, "null grouping or picks");
     if (rows <= 0 || rows > g->max_rows) return fail(GFR_EINVAL, "grouping rows %d exceed scratch %d", rows, g->max_rows);
     hipError_t e;
-    if (rows <= gfr::GROUP_SMALL_ROWS && g->experts <= 1024)
+    if (rows <= gfr::GROUP_SMALL_ROWS && g->experts <= 1024 &&
+        gfr::group_small_lds(rows, g->slots, g->experts) <= gfr::GROUP_LDS_MAX)
         e = gfr::launch_group_small(stream, picks, rows, g->slots, g->experts, g->ids, g->count, g->members,
                                     g->max_rows);
     else
@@ -165,7 +170,7 @@ namespace {
 int experts_run(gfr_experts* ex, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
                 int input_stride, const int32_t* picks, const int32_t* ids, const int32_t* count,
                 const int32_t* members, int rows, int maxm, const float* weights, float* out,
-                const gfr::RouteOne* route = nullptr) {
+                const gfr::RouteOne* route = nullptr, const float* shared = nullptr, int shared_stride = 0) {
     const int P = rows * ex->slots, D = ex->hidden, N = ex->inter;
     const int maxu = P < w->experts ? P : w->experts;
     hipError_t e;
@@ -181,7 +186,7 @@ int experts_run(gfr_experts* ex, hipStream_t stream, const gfr_exl3_experts* w, 
                                      maxu)) != hipSuccess)
         return hip_fail(e, "down gemv");
     if ((e = gfr::launch_sum_finish(stream, ex->zd, ex->y, rows, P, D, gfr::gemv_down_splits(N), ex->slots,
-                                    ex->exl3_slots, weights, out)) != hipSuccess)
+                                    ex->exl3_slots, weights, shared, shared_stride, out)) != hipSuccess)
         return hip_fail(e, "down epilogue");
     return 0;
 }
@@ -393,6 +398,10 @@ int gfr_fast_experts_destroy(gfr_fast_experts* fx) {
 
 // ---- one MoE layer ----------------------------------------------------------------------------------------------
 int gfr_moe_create(gfr_moe** out, int hidden, int inter, int routed, int topk, int max_rows) {
+    return gfr_moe_create_shared(out, hidden, inter, routed, topk, max_rows, 1);
+}
+
+int gfr_moe_create_shared(gfr_moe** out, int hidden, int inter, int routed, int topk, int max_rows, int shared_exl3) {
     if (!out) return fail(GFR_EINVAL, "null out");
     *out = nullptr;
     int rc = check_shape(hidden, inter);
@@ -408,20 +417,23 @@ int gfr_moe_create(gfr_moe** out, int hidden, int inter, int routed, int topk, i
     const int dec_cap = 64 < max_rows ? 64 : max_rows;
     gfr_moe* m = new gfr_moe{hidden, inter, routed, topk, topk + 1, max_rows,
                              MOE_DECODE_ROWS < max_rows ? MOE_DECODE_ROWS : max_rows,
-                             nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 1.f};
+                             nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 1.f,
+                             shared_exl3 ? 1 : 0, nullptr};
+    const int exl3_slots = shared_exl3 ? topk + 1 : topk, experts = shared_exl3 ? routed + 1 : routed;
     m->route_bias = nullptr;   // the softmax gate until gfr_moe_set_router
     m->route_scale = 1.f;
     const size_t P = (size_t)max_rows * m->slots;
     if ((rc = alloc_zero(&m->weights, P, "moe weights")) || (rc = alloc_zero(&m->picks, P, "moe picks")) ||
         (rc = alloc_zero(&m->out, (size_t)max_rows * hidden, "moe output")) ||
+        (rc = alloc_zero(&m->logits, (size_t)max_rows * routed, "moe logits")) ||
         (rc = gfr_grouping_create(&m->group_dec, routed + 1, m->slots, dec_cap)) ||
-        (rc = gfr_experts_create(&m->dec, hidden, inter, m->slots, m->slots, dec_cap))) {
+        (rc = gfr_experts_create(&m->dec, hidden, inter, m->slots, exl3_slots, dec_cap))) {
         gfr_moe_destroy(m);
         return rc;
     }
     if (max_rows > m->decode_rows &&
         ((rc = gfr_grouping_create(&m->group_pre, routed + 1, m->slots, max_rows)) ||
-         (rc = gfr_fast_experts_create(&m->pre, hidden, inter, m->slots, m->slots, routed + 1, max_rows)))) {
+         (rc = gfr_fast_experts_create(&m->pre, hidden, inter, m->slots, exl3_slots, experts, max_rows)))) {
         gfr_moe_destroy(m);
         return rc;
     }
@@ -440,15 +452,20 @@ int gfr_moe_set_decode_rows(gfr_moe* m, int decode_rows) {
     return 0;
 }
 
-int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
-                const float* logits, int rows) {
+namespace {
+int moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input, const float* logits,
+            const float* shared, int shared_stride, int rows) {
     if (!m) return fail(GFR_EINVAL, "null moe");
     int rc = check_weights(w, m->hidden, m->inter);
     if (rc) return rc;
-    if (w->experts != m->routed + 1)
-        return fail(GFR_EINVAL, "weights hold %d experts, layer needs %d routed + 1 shared", w->experts, m->routed);
+    if (w->experts != m->routed + m->shared_exl3)
+        return fail(GFR_EINVAL, "weights hold %d experts, layer needs %d routed%s", w->experts, m->routed,
+                    m->shared_exl3 ? " + 1 shared" : "");
     if (rows <= 0 || rows > m->max_rows) return fail(GFR_EINVAL, "rows %d outside 1..%d", rows, m->max_rows);
     if (!input || !logits) return fail(GFR_EINVAL, "null input");
+    if (shared && m->shared_exl3) return fail(GFR_EINVAL, "the layer's shared expert is EXL3: no shared output");
+    if (shared && shared_stride < m->hidden) return fail(GFR_EINVAL, "shared stride %d < hidden %d", shared_stride,
+                                                         m->hidden);
     hipError_t e;
     if (rows <= m->decode_rows) {
         gfr_grouping* g = m->group_dec;
@@ -457,7 +474,7 @@ int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const
             const gfr::RouteOne r{logits, m->route_bias, m->route_scale, m->routed, m->picks, m->weights, g->ids,
                                   g->count, g->members};
             return experts_run(m->dec, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members, 1,
-                               g->max_rows, m->weights, m->out, &r);
+                               g->max_rows, m->weights, m->out, &r, shared, shared_stride);
         }
         // four launches: route + group, gate/up (+ rotation), down (+ gate/up epilogue), down epilogue (+ combine)
         if ((e = gfr::launch_route_group(stream, logits, rows, m->routed, m->topk, m->picks, m->weights, g->ids,
@@ -465,12 +482,12 @@ int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const
                                          m->route_bias, m->route_scale)) != hipSuccess)
             return hip_fail(e, "route + group");
         return experts_run(m->dec, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members, rows,
-                           g->max_rows, m->weights, m->out);
+                           g->max_rows, m->weights, m->out, nullptr, shared, shared_stride);
     }
     gfr_grouping* g = m->group_pre;
     bool planned = false;
-    const size_t rg_lds = (2 * (size_t)rows * m->slots + (size_t)g->experts * ((rows + 31) / 32) + 2 * (size_t)g->experts) * 4;
-    if (rows <= gfr::GROUP_SMALL_ROWS && g->experts <= 1024 && rg_lds <= 65536) {
+    if (rows <= gfr::GROUP_SMALL_ROWS && g->experts <= 1024 &&
+        gfr::route_group_lds(rows, m->slots, g->experts) <= gfr::GROUP_LDS_MAX) {
         // route + group + the prefill engine's item plan in one launch (the same router, grouping and plan as the
         // separate launches below)
         int *pu, *pi, *pp;
@@ -490,12 +507,49 @@ int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const
     // windows on the split-K programs fold the combine into their down epilogue
     bool combined = false;
     if ((e = gfr::prefill_run(m->pre, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members, rows,
-                              g->max_rows, false, m->weights, m->out, &combined, planned)) != hipSuccess)
+                              g->max_rows, false, m->weights, m->out, &combined, planned, shared, shared_stride)) !=
+        hipSuccess)
         return hip_fail(e, "prefill run");
     if (!combined &&
-        (e = gfr::launch_combine(stream, gfr::prefill_output(m->pre), m->weights, rows, m->slots, m->hidden, m->out)) !=
-            hipSuccess)
+        (e = gfr::launch_combine(stream, gfr::prefill_output(m->pre), m->weights, rows, m->slots,
+                                 m->shared_exl3 ? m->slots : m->slots - 1, m->hidden, shared, shared_stride,
+                                 m->out)) != hipSuccess)
         return hip_fail(e, "combine");
+    return 0;
+}
+}  // namespace
+
+int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
+                const float* logits, int rows) {
+    return moe_run(m, stream, w, input, logits, nullptr, 0, rows);
+}
+
+int gfr_moe_run_shared(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
+                       const float* logits, const float* shared, int shared_stride, int rows) {
+    if (!shared) return fail(GFR_EINVAL, "null shared output");
+    return moe_run(m, stream, w, input, logits, shared, shared_stride, rows);
+}
+
+int gfr_moe_run_router(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
+                       const uint16_t* router_weight, const float* shared, int shared_stride, int rows) {
+    if (!m) return fail(GFR_EINVAL, "null moe");
+    if (!input || !router_weight) return fail(GFR_EINVAL, "null input or router weight");
+    if (rows <= 0 || rows > m->max_rows) return fail(GFR_EINVAL, "rows %d outside 1..%d", rows, m->max_rows);
+    int rc = gfr_router_logits(stream, input, m->hidden, router_weight, m->hidden, m->routed, rows, m->logits);
+    if (rc) return rc;
+    return moe_run(m, stream, w, input, m->logits, shared, shared_stride, rows);
+}
+
+int gfr_router_logits(hipStream_t stream, const uint16_t* input, int input_stride, const uint16_t* router_weight,
+                      int hidden, int routed, int rows, float* logits) {
+    if (!input || !router_weight || !logits) return fail(GFR_EINVAL, "null argument");
+    if (hidden <= 0 || hidden % 8 || hidden > gfr::router_logits_max_hidden())
+        return fail(GFR_EINVAL, "router hidden %d: a positive multiple of 8 up to %d", hidden,
+                    gfr::router_logits_max_hidden());
+    if (routed <= 0 || rows <= 0 || input_stride < hidden)
+        return fail(GFR_EINVAL, "routed %d rows %d stride %d", routed, rows, input_stride);
+    hipError_t e = gfr::launch_router_logits(stream, input, input_stride, router_weight, hidden, routed, rows, logits);
+    if (e != hipSuccess) return hip_fail(e, "router logits");
     return 0;
 }
 
@@ -517,7 +571,7 @@ int gfr_moe_destroy(gfr_moe* m) {
     gfr_grouping_destroy(m->group_pre);
     gfr_experts_destroy(m->dec);
     gfr_fast_experts_destroy(m->pre);
-    free_all({m->weights, m->picks, m->out});
+    free_all({m->weights, m->picks, m->out, m->logits});
     delete m;
     return 0;
 }

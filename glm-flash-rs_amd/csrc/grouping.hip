@@ -252,18 +252,28 @@ __global__ void __launch_bounds__(256) group_scatter_kernel(const int* __restric
 
 namespace gfr {
 
+size_t group_small_lds(int rows, int slots, int E) {
+    return ((size_t)rows * slots + (size_t)E * ((rows + 31) / 32) + 2 * (size_t)E) * 4;
+}
+
 hipError_t launch_group_small(hipStream_t s, const int* picks, int rows, int slots, int E, int* ids, int* count,
                               int* members, int maxm) {
-    const size_t lds = ((size_t)rows * slots + (size_t)E * ((rows + 31) / 32) + 2 * (size_t)E) * 4;
+    const size_t lds = group_small_lds(rows, slots, E);
+    if (lds > GROUP_LDS_MAX) return hipErrorInvalidValue;
     group_small_kernel<<<1, 1024, lds, s>>>(picks, rows, slots, E, ids, count, members, maxm);
     return hipGetLastError();
+}
+
+size_t route_group_lds(int rows, int slots, int E) {
+    return (2 * (size_t)rows * slots + (size_t)E * ((rows + 31) / 32) + 2 * (size_t)E) * 4;
 }
 
 hipError_t launch_route_group(hipStream_t s, const float* logits, int rows, int routed, int topk, int* picks,
                               float* weights, int* ids, int* count, int* members, int maxm, int bm, int* plan_ucnt,
                               int* plan_items, int* plan, const float* bias, float scale) {
     const int E = routed + 1, slots = topk + 1;
-    const size_t lds = (2 * (size_t)rows * slots + (size_t)E * ((rows + 31) / 32) + 2 * (size_t)E) * 4;
+    const size_t lds = route_group_lds(rows, slots, E);
+    if (lds > GROUP_LDS_MAX) return hipErrorInvalidValue;
     route_group_kernel<<<1, 1024, lds, s>>>(logits, rows, routed, topk, picks, weights, ids, count, members, maxm,
                                             bm, plan_ucnt, plan_items, plan, RouteGate{bias, scale});
     return hipGetLastError();
@@ -271,6 +281,7 @@ hipError_t launch_route_group(hipStream_t s, const float* logits, int rows, int 
 
 hipError_t launch_group_large(hipStream_t s, const int* picks, int rows, int slots, int E, uint32_t* bits,
                               int* prefix, int* counts, int* ids, int* count, int* members, int maxm) {
+    if ((size_t)E * 8 * 4 > GROUP_LDS_MAX) return hipErrorInvalidValue;
     group_mark_kernel<<<(rows + 255) / 256, 256, (size_t)E * 8 * 4, s>>>(picks, rows, slots, E, bits);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;

@@ -7,6 +7,9 @@ namespace gfr {
 
 // grouping.hip
 constexpr int GROUP_SMALL_ROWS = 256;
+constexpr size_t GROUP_LDS_MAX = 65536;   // dynamic LDS a grouping launch may ask for
+size_t group_small_lds(int rows, int slots, int E);   // LDS of launch_group_small
+size_t route_group_lds(int rows, int slots, int E);   // LDS of launch_route_group
 hipError_t launch_group_small(hipStream_t s, const int* picks, int rows, int slots, int E, int* ids, int* count,
                               int* members, int maxm);
 // route (route.hpp) + group_small in one launch; rows <= GROUP_SMALL_ROWS, routed + 1 <= 1024
@@ -60,7 +63,8 @@ hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, int SKgu, 
 // Finish of the decode path: Zd's transformed k-block parts [N / 128][P][D] added in order -> y; with weights the
 // slot-ordered combine -> out
 hipError_t launch_sum_finish(hipStream_t s, const float* Zd, float* y, int rows, int P, int D, int SK, int slots,
-                             int exl3_slots, const float* weights, float* out);
+                             int exl3_slots, const float* weights, const float* shared, int shared_stride,
+                             float* out);
 // one fp16 row through one linear with the input rotation fused (partials for down_epilogue)
 int gemv_linear_splits(int kin);
 hipError_t launch_linear_fused(hipStream_t s, const uint16_t* x, const uint16_t* suh, const uint32_t* trellis,
@@ -68,7 +72,7 @@ hipError_t launch_linear_fused(hipStream_t s, const uint16_t* x, const uint16_t*
                                int bits);
 hipError_t launch_down_finish(hipStream_t s, const float* Zd, const int* pick, const uint16_t* svh_d, float* y,
                               int rows, int P, int D, int SK, int slots, int exl3_slots, const float* weights,
-                              float* out);
+                              const float* shared, int shared_stride, float* out);
 // pair_order: xd in the MFMA path's pair order (x[m + 8], x[m] within each 16-value tile) instead of k order
 hipError_t launch_gateup_epilogue(hipStream_t s, const float* Z, const int* pick, const uint16_t* svh_g,
                                   const uint16_t* svh_u, const uint16_t* suh_d, uint16_t* xd, int P, int N, int SK,
@@ -81,7 +85,13 @@ hipError_t launch_down_epilogue(hipStream_t s, const float* Z, const int* pick, 
 // bias == nullptr: the softmax gate; else GLM's sigmoid + bias gate with weights times scale (route.hpp RouteGate)
 hipError_t launch_route(hipStream_t s, const float* logits, int rows, int E, int topk, int shared_id, int* picks,
                         float* weights, const float* bias = nullptr, float scale = 1.f);
-hipError_t launch_combine(hipStream_t s, const float* y, const float* weights, int rows, int slots, int D,
-                          float* out);
+// shared: the caller's output for the slots s >= exl3_slots ([rows][shared_stride] fp32), or null
+hipError_t launch_combine(hipStream_t s, const float* y, const float* weights, int rows, int slots, int exl3_slots,
+                          int D, const float* shared, int shared_stride, float* out);
+// logits [rows][E] fp32 = x [rows][x_stride] bf16 times W [E][D] bf16 (D a multiple of 8, at most
+// router_logits_max_hidden())
+int router_logits_max_hidden();
+hipError_t launch_router_logits(hipStream_t s, const uint16_t* x, int x_stride, const uint16_t* W, int D, int E,
+                                int rows, float* logits);
 
 }  // namespace gfr

@@ -58,7 +58,10 @@ def _load() -> ctypes.CDLL:
         "gfr_moe_picks": ([VP], P),
         "gfr_moe_weights": ([VP], P),
         "gfr_moe_set_decode_rows": ([VP, I], I),
-
+        "gfr_moe_create_shared": ([ctypes.POINTER(VP), I, I, I, I, I, I], I),
+        "gfr_moe_run_shared": ([VP, P, P, P, P, P, I, I], I),
+        "gfr_moe_run_router": ([VP, P, P, P, P, P, I, I], I),
+        "gfr_router_logits": ([P, P, I, P, I, I, I, P], I),
         "gfr_moe_destroy": ([VP], I),
         "gfr_linear_create": ([ctypes.POINTER(VP), I, I, I], I),
         "gfr_linear_run": ([VP, P, P, P, P, P, P], I),
@@ -276,13 +279,17 @@ class FastExperts(_Engine):
 
 class Moe(_Engine):
     """Moe::run_prefetched (moe.rs:66-182): router (the benchmark's softmax top-k, or GLM's sigmoid + bias gate via
-    set_router) -> grouping -> EXL3 experts (routed + shared) -> combine."""
+    set_router) -> grouping -> EXL3 experts -> combine. shared_exl3=True: the shared expert is the weights' last EXL3
+    expert (the benchmark configs); False: the reference's layout, whose shared expert is not EXL3 and whose output
+    the caller passes to run (the reference's combine(y, shared, weights, out), moe.rs:171-181)."""
 
     _destroy = "gfr_moe_destroy"
 
-    def __init__(self, hidden: int, inter: int, routed: int, topk: int, max_rows: int, device="cuda"):
+    def __init__(self, hidden: int, inter: int, routed: int, topk: int, max_rows: int, device="cuda",
+                 shared_exl3: bool = True):
         super().__init__()
-        _check(lib().gfr_moe_create(ctypes.byref(self._h), hidden, inter, routed, topk, max_rows))
+        _check(lib().gfr_moe_create_shared(ctypes.byref(self._h), hidden, inter, routed, topk, max_rows,
+                                           int(shared_exl3)))
         self.hidden, self.routed, self.topk, self.max_rows = hidden, routed, topk, max_rows
         L = lib()
         self.output = _view(L.gfr_moe_output(self._h), (max_rows, hidden), torch.float32, device)
@@ -298,9 +305,22 @@ class Moe(_Engine):
         self._router_bias = bias
         _check(lib().gfr_moe_set_router(self._h, _ptr(bias), float(scale) if bias is not None else 1.0))
 
-    def run(self, w: Exl3Experts, input: torch.Tensor, logits: torch.Tensor, rows: int, stream=None):
+    def run(self, w: Exl3Experts, input: torch.Tensor, logits: torch.Tensor, rows: int, stream=None,
+            shared: torch.Tensor = None):
+        """shared: the non-EXL3 shared expert's output [rows, >= hidden] fp32 (a layer made with shared_exl3=False)."""
         ws = w.struct()
-        _check(lib().gfr_moe_run(self._h, _stream(stream), ctypes.byref(ws), _ptr(input), _ptr(logits), rows))
+        if shared is None:
+            _check(lib().gfr_moe_run(self._h, _stream(stream), ctypes.byref(ws), _ptr(input), _ptr(logits), rows))
+        else:
+            _check(lib().gfr_moe_run_shared(self._h, _stream(stream), ctypes.byref(ws), _ptr(input), _ptr(logits),
+                                            _ptr(shared), shared.stride(0), rows))
+
+    def run_router(self, w: Exl3Experts, input: torch.Tensor, router_weight: torch.Tensor, rows: int, stream=None,
+                   shared: torch.Tensor = None):
+        """The layer from the hidden rows: router logits (router_weight [routed, hidden] bf16) then run."""
+        ws = w.struct()
+        _check(lib().gfr_moe_run_router(self._h, _stream(stream), ctypes.byref(ws), _ptr(input), _ptr(router_weight),
+                                        _ptr(shared), shared.stride(0) if shared is not None else 0, rows))
 
 
 class Linear(_Engine):
@@ -314,6 +334,18 @@ class Linear(_Engine):
 
     def run(self, x, trellis, suh, svh, y, stream=None):
         _check(lib().gfr_linear_run(self._h, _stream(stream), _ptr(x), _ptr(trellis), _ptr(suh), _ptr(svh), _ptr(y)))
+
+
+def router_logits(input: torch.Tensor, router_weight: torch.Tensor, stream=None) -> torch.Tensor:
+    """gfr_router_logits: [rows, routed] fp32 logits of bf16 rows [rows, hidden] and a bf16 weight [routed, hidden]."""
+    if input.dtype != torch.bfloat16 or router_weight.dtype != torch.bfloat16:
+        raise ValueError("router logits take bf16 rows and a bf16 weight")
+    rows, hidden = input.shape
+    routed = router_weight.shape[0]
+    out = torch.empty((rows, routed), dtype=torch.float32, device=input.device)
+    _check(lib().gfr_router_logits(_stream(stream), _ptr(input), input.stride(0), _ptr(router_weight), hidden, routed,
+                                   rows, _ptr(out)))
+    return out
 
 
 def route(logits: torch.Tensor, topk: int, stream=None):

@@ -105,13 +105,27 @@ uint16_t* gfr_fast_experts_rotated(const gfr_fast_experts* fx, int mat);
 int gfr_fast_experts_destroy(gfr_fast_experts* fx);
 
 /* ---- One MoE layer (Moe::run_prefetched, moe.rs:66-182) ------------------------------------------------------
- * logits [rows][routed] fp32 router logits -> softmax top-k (renormalised) + the shared expert (id `routed`, EXL3,
+ * logits [rows][routed] fp32 router logits -> softmax top-k (renormalised) + the shared expert (id `routed`,
  * weight 1) -> grouping -> experts (decode path for rows <= decode_rows, prefill path above) -> combine ->
- * output [rows][hidden] fp32. The weights hold routed + 1 experts. */
+ * output [rows][hidden] fp32, the slots added in order.
+ * gfr_moe_create: the shared expert is EXL3 (the benchmark configs); the weights hold routed + 1 experts.
+ * gfr_moe_create_shared with shared_exl3 = 0: the reference's layout, whose shared expert is FP8 and runs outside the
+ * EXL3 path (moe.rs:132-167); the weights hold the routed experts only, and the caller's shared-expert output enters
+ * the combine as the last slot (gfr_moe_run_shared: out = sum of the routed slots' weighted outputs + shared, the
+ * reference's combine(y, shared, weights, out), moe.rs:171-181). */
 typedef struct gfr_moe gfr_moe;
 int gfr_moe_create(gfr_moe** out, int hidden, int inter, int routed, int topk, int max_rows);  /* Moe::new :23-64 */
+int gfr_moe_create_shared(gfr_moe** out, int hidden, int inter, int routed, int topk, int max_rows, int shared_exl3);
 int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
                 const float* logits, int rows);                                 /* Moe::run_prefetched :66-182 */
+/* shared [rows][shared_stride] fp32: the shared expert's output (a layer made with shared_exl3 = 0 only) */
+int gfr_moe_run_shared(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
+                       const float* logits, const float* shared, int shared_stride, int rows);
+/* The whole layer from the hidden rows: router logits (gfr_router_logits, the reference's router_part + router_sum,
+ * moe.rs:77-87) into the layer's own buffer, then gfr_moe_run_shared (shared may be NULL: no shared term, or an
+ * EXL3 shared expert). router_weight [routed][hidden] bf16. */
+int gfr_moe_run_router(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
+                       const uint16_t* router_weight, const float* shared, int shared_stride, int rows);
 float* gfr_moe_output(const gfr_moe* m);
 int32_t* gfr_moe_picks(const gfr_moe* m);        /* [rows][topk + 1] */
 float* gfr_moe_weights(const gfr_moe* m);        /* [rows][topk + 1] */
@@ -134,6 +148,12 @@ int gfr_route_topk_biased(hipStream_t stream, const float* logits, const float* 
                           int routed, int topk, int32_t* picks, float* weights);
 int gfr_route_topk(hipStream_t stream, const float* logits, int rows, int routed, int topk, int32_t* picks,
                    float* weights);
+/* Router logits (moe.rs:77-87, router_part [1,9,8] + router_sum; Triton, source absent): logits[r][e] =
+ * sum over k of input[r][k] * router_weight[e][k], bf16 inputs, fp32 products and sums in a fixed order.
+ * input [rows][input_stride] bf16, router_weight [routed][hidden] bf16, logits [rows][routed] fp32; hidden a
+ * multiple of 8, at most 65536. */
+int gfr_router_logits(hipStream_t stream, const uint16_t* input, int input_stride, const uint16_t* router_weight,
+                      int hidden, int routed, int rows, float* logits);
 
 /* ---- Single EXL3 linear (benchmark config 1; the decode path's GEMV with rot_in / down-epilogue formulas) ----
  * y [n] fp32 = svh * had(W^T xh) / sqrt(128), xh = fp16(had(x * suh) / sqrt(128)), x [kin] fp16. */

@@ -323,10 +323,11 @@ def test_route_vs_oracle(gfr, oracle, rows, E, topk):
     np.testing.assert_allclose(w.cpu().numpy(), wt, rtol=2e-6, atol=1e-7)
 
 
-@pytest.mark.parametrize("bits", [2, 3, 5])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5])
 def test_moe_layer_config5_decode_vs_oracle(gfr, oracle, bits):
-    """Config 5's layer shape at bs = 1 (hidden 5120, 160 routed + 1 shared, top-8, inter 1536), K = 2 and 5, through
-    the Moe entry point against the oracle (routing exact, output within tolerance)."""
+    """Config 5's layer shape at bs = 1 (hidden 5120, 160 routed + 1 shared, top-8, inter 1536), each of the stack's
+    bit widths K = 2, 3, 4, 5, through the Moe entry point against the oracle (routing exact, output within
+    tolerance)."""
     import synth
     E, D, N, topk = 160, 5120, 1536, 8
     w = synth.experts(E + 1, D, N, bits, seed=60 + bits)

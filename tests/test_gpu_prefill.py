@@ -115,12 +115,13 @@ def test_moe_prefill_config4_tokens(gfr, oracle):
         assert_close(out[r], want[0], what=f"token {r}")
 
 
-@pytest.mark.parametrize("bits", [2, 3, 5])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5])
 @pytest.mark.parametrize("rows", [40, 320])
 def test_fast_experts_bit_widths(gfr, oracle, bits, rows):
-    """K = 2, 3, 5 (config 5's mixed bit rates): the MFMA path's generic decode (one trellis lane a thread, pieces
-    handed to their MFMA lanes through LDS) against the oracle, at C5's hidden size. 40 rows (360 pairs) run the
-    split-K programs, 320 rows (2880 pairs) the full-K items with the fused epilogues."""
+    """K = 2, 3, 4, 5 (config 5's mixed bit rates) at C5's hidden size against the oracle: K = 4's decode straight
+    into MFMA fragments, the others' generic decode (one trellis lane a thread, pieces handed to their MFMA lanes
+    through LDS). 40 rows (360 pairs) run the split-K programs, 320 rows (2880 pairs) the full-K items with the fused
+    epilogues."""
     import synth
     Dk, Nk, E, slots, maxm = 5120, 1536, 9, 9, rows
     w = synth.experts(E, Dk, Nk, bits, seed=90 + bits)
@@ -205,3 +206,30 @@ def test_prefill_rotation_bitexact(gfr, oracle, hidden, slots, rows, shared_x):
                 want = oracle.rot(xs[r], suh[picks_np[r, s]])
                 assert np.array_equal(got[r * slots + s], want), \
                     f"matrix {m} row {r} slot {s}: {np.sum(got[r * slots + s] != want)} values differ"
+
+
+def test_split_window_with_many_experts(gfr, oracle):
+    """A split-K window (at most 2048 pairs, 32-row items) whose routing spreads over 1023 experts with one member each
+    plus a shared expert with every row: the plan holds 1023 + 32 items, more than an item count sized for 128-row
+    items would hold. Sampled tokens against the oracle."""
+    import synth
+    routed, topk, rows, Dk, Nk, bits = 1023, 1, 1024, 512, 512, 4
+    w = synth.experts(routed + 1, Dk, Nk, bits, seed=1023)
+    x = synth.activations(rows, Dk, 11)
+    lg = torch.randn((rows, routed), generator=torch.Generator(device="cuda").manual_seed(12), device="cuda")
+    target = torch.arange(rows, device="cuda") % routed
+    lg[torch.arange(rows, device="cuda"), target] = 10.0
+    m = gfr.Moe(Dk, Nk, routed, topk, rows)
+    m.run(w, x, lg, rows)
+    torch.cuda.synchronize()
+    out = m.output[:rows].cpu().numpy()
+    assert np.all(np.isfinite(out))
+    p, wt = oracle.route(lg.cpu().numpy(), topk, routed)
+    assert np.array_equal(m.picks[:rows].cpu().numpy(), p)
+    assert len(set(p[:, 0].tolist())) == routed
+    dec = DecodedExperts(oracle, w)
+    xb = np_u16(x)
+    for r in (0, 511, 1022, 1023):
+        ys = np.stack([dec.row(xb[r], int(e), sk_gu=1, sk_d=1, warps=1)[0] for e in p[r]])
+        want = oracle.combine(ys, wt[r:r + 1], 1, topk + 1)
+        assert_close(out[r], want[0], what=f"token {r}")

@@ -343,3 +343,31 @@ def test_combine(oracle):
     w = rng.random((3, 5)).astype(np.float32)
     out = oracle.combine(y, w, 3, 5)
     np.testing.assert_allclose(out, np.einsum("rs,rsn->rn", w, y.reshape(3, 5, 32)), rtol=1e-6, atol=1e-6)
+
+
+def test_linear_vs_float64(oracle):
+    """gfro_linear (config 1's checker: rot_in on an fp16 token, one GEMV, the down epilogue, exl3.cu:224-241 and
+    :300-321) against the same composition in float64 with the dense Sylvester Hadamard of each 128-block. The only
+    rounding of the oracle, fp16 of the rotated activations, is applied at the same point, so the two agree to fp32
+    accumulation error; a kin != n shape catches a transposed weight, and a dropped scale, 1/sqrt(128) or block
+    transform fails by orders of magnitude."""
+    rng = np.random.default_rng(21)
+    H = np.array([[1.0]])
+    for _ in range(7):
+        H = np.block([[H, H], [H, -H]])
+    Hb = lambda v: np.concatenate([H @ v[i:i + 128] for i in range(0, len(v), 128)]) / np.sqrt(128)
+    for kin, n in ((384, 256), (2048, 1536)):
+        words = rng.integers(0, 2 ** 32, (kin // 16, n // 16, 32), dtype=np.uint64).astype(np.uint32)
+        w = oracle.unpack_f32(words, kin, n, 4)
+        sc = lambda m: ((rng.integers(0, 2, m) * 2 - 1) * (rng.random(m) + 0.5)).astype(np.float16)
+        suh, svh = sc(kin), sc(n)
+        x = rng.standard_normal(kin).astype(np.float16)
+        y = oracle.linear(x.view(np.uint16), w, suh.view(np.uint16), svh.view(np.uint16))
+        xh = Hb(x.astype(np.float64) * suh.astype(np.float64)).astype(np.float16).astype(np.float64)
+        want = Hb(xh @ w.astype(np.float64)) * svh.astype(np.float64)
+        err = np.sqrt(np.mean((y - want) ** 2) / np.mean(want ** 2))
+        assert err < 5e-5, (kin, n, err)
+        # the same without the fp16 rounding of the activations: within fp16 rounding of the result
+        want_exact = Hb(Hb(x.astype(np.float64) * suh.astype(np.float64)) @ w.astype(np.float64)) * svh.astype(np.float64)
+        err2 = np.sqrt(np.mean((y - want_exact) ** 2) / np.mean(want_exact ** 2))
+        assert err2 < 2e-3, (kin, n, err2)
