@@ -6,6 +6,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
+#include <mutex>
 #include <string>
 
 #include "../../include/gfr_moe.h"
@@ -522,6 +523,95 @@ int moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uin
 int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
                 const float* logits, int rows) {
     return moe_run(m, stream, w, input, logits, nullptr, 0, rows);
+}
+
+// ---- the bs = 1 layer without allocation ----------------------------------------------------------------------
+// Every scratch buffer of gfr_moe_token_static lives in this fixed device array (one per GPU, held until the process
+// ends). Host code uses the per-device address from hipGetSymbolAddress, never the array's name.
+}  // extern "C"
+namespace {
+constexpr size_t STATIC_SCRATCH_BYTES = (size_t)8 << 20;
+static __device__ __align__(256) unsigned char scratch[STATIC_SCRATCH_BYTES];
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch[MAX_DEVICES];
+
+// this device's address of `scratch` (looked up once per device, with that device current)
+int scratch_ptr(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "static scratch: current device");
+    if (dev < 0 || dev >= MAX_DEVICES) return fail(GFR_EUNSUPPORTED, "static scratch: device %d", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "static scratch address");
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return 0;
+}
+
+// carve 256-byte aligned pieces off the array
+struct Carver {
+    unsigned char* base;
+    size_t off;
+    template <typename T>
+    T* take(size_t count) {
+        T* p = reinterpret_cast<T*>(base + off);
+        off += (count * sizeof(T) + 255) & ~(size_t)255;
+        return p;
+    }
+};
+}  // namespace
+extern "C" {
+
+int gfr_moe_token_static(hipStream_t stream, const gfr_exl3_experts* w, int routed, int topk, const uint16_t* input,
+                         const float* logits, float* out, int32_t* picks, float* weights) {
+    if (!w) return fail(GFR_EINVAL, "null weights");
+    int rc = check_shape(w->hidden, w->inter);
+    if (rc) return rc;
+    rc = check_weights(w, w->hidden, w->inter);
+    if (rc) return rc;
+    if (routed <= 0 || routed > 1023 || topk <= 0 || topk > 31 || topk > routed)
+        return fail(GFR_EINVAL, "routed %d / topk %d", routed, topk);
+    if (w->experts != routed + 1)
+        return fail(GFR_EINVAL, "weights hold %d experts, layer needs %d routed + 1 shared", w->experts, routed);
+    if (!input || !logits || !out) return fail(GFR_EINVAL, "null input, logits or output");
+    const int slots = topk + 1, D = w->hidden, N = w->inter;
+    // the layout, sized first on a null base, then placed on this device's array
+    int32_t *pk, *ids, *count, *members;
+    float* wt;
+    gfr_experts ex{D, N, slots, slots, 1, nullptr, nullptr, nullptr, nullptr};
+    auto carve = [&](Carver& c) {
+        pk = c.take<int32_t>(slots);
+        wt = c.take<float>(slots);
+        ids = c.take<int32_t>(slots);
+        count = c.take<int32_t>(1);
+        members = c.take<int32_t>(slots);
+        ex.zgu = c.take<float>((size_t)2 * gfr::gemv_gateup_splits(D) * slots * N);
+        ex.xd = c.take<uint16_t>((size_t)slots * N);
+        ex.zd = c.take<float>((size_t)gfr::gemv_down_splits(N) * slots * D);
+        ex.y = c.take<float>((size_t)slots * D);
+    };
+    Carver size{nullptr, 0};
+    carve(size);
+    if (size.off > STATIC_SCRATCH_BYTES)
+        return fail(GFR_EINVAL, "layer hidden %d inter %d top-%d needs %zu bytes of scratch, the static array holds %zu",
+                    D, N, topk, size.off, STATIC_SCRATCH_BYTES);
+    void* base = nullptr;
+    if ((rc = scratch_ptr(&base))) return rc;
+    Carver c{static_cast<unsigned char*>(base), 0};
+    carve(c);
+    const gfr::RouteOne r{logits, nullptr, 1.f, routed, pk, wt, ids, count, members};
+    if ((rc = experts_run(&ex, stream, w, input, D, pk, ids, count, members, 1, 1, wt, out, &r))) return rc;
+    hipError_t e;
+    if (picks && (e = hipMemcpyAsync(picks, pk, slots * 4, hipMemcpyDeviceToDevice, stream)) != hipSuccess)
+        return hip_fail(e, "picks copy");
+    if (weights && (e = hipMemcpyAsync(weights, wt, slots * 4, hipMemcpyDeviceToDevice, stream)) != hipSuccess)
+        return hip_fail(e, "weights copy");
+    return 0;
 }
 
 int gfr_moe_run_shared(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,

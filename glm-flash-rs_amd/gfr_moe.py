@@ -62,6 +62,7 @@ def _load() -> ctypes.CDLL:
         "gfr_moe_run_shared": ([VP, P, P, P, P, P, I, I], I),
         "gfr_moe_run_router": ([VP, P, P, P, P, P, I, I], I),
         "gfr_router_logits": ([P, P, I, P, I, I, I, P], I),
+        "gfr_moe_token_static": ([P, ctypes.POINTER(_Exl3Struct), I, I, P, P, P, P, P], I),
         "gfr_moe_destroy": ([VP], I),
         "gfr_linear_create": ([ctypes.POINTER(VP), I, I, I], I),
         "gfr_linear_run": ([VP, P, P, P, P, P, P], I),
@@ -334,6 +335,14 @@ class Linear(_Engine):
 
     def run(self, x, trellis, suh, svh, y, stream=None):
         _check(lib().gfr_linear_run(self._h, _stream(stream), _ptr(x), _ptr(trellis), _ptr(suh), _ptr(svh), _ptr(y)))
+
+
+def moe_token_static(w: Exl3Experts, routed: int, topk: int, input: torch.Tensor, logits: torch.Tensor,
+                     out: torch.Tensor, picks: torch.Tensor = None, weights: torch.Tensor = None, stream=None):
+    """gfr_moe_token_static: one token through the bs = 1 layer with the library's fixed scratch (no allocation)."""
+    ws = w.struct()
+    _check(lib().gfr_moe_token_static(_stream(stream), ctypes.byref(ws), routed, topk, _ptr(input), _ptr(logits),
+                                      _ptr(out), _ptr(picks), _ptr(weights)))
 
 
 def router_logits(input: torch.Tensor, router_weight: torch.Tensor, stream=None) -> torch.Tensor:

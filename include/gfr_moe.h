@@ -129,7 +129,16 @@ int gfr_moe_run_router(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w
 float* gfr_moe_output(const gfr_moe* m);
 int32_t* gfr_moe_picks(const gfr_moe* m);        /* [rows][topk + 1] */
 float* gfr_moe_weights(const gfr_moe* m);        /* [rows][topk + 1] */
-int gfr_moe_set_decode_rows(gfr_moe* m, int decode_rows);  /* rows at or below run the decode path (default 4, max 64) */
+int gfr_moe_set_decode_rows(gfr_moe* m, int decode_rows);
+/* No counterpart in the reference: for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). One token through the bs = 1 layer of gfr_moe_run (the
+ * router's softmax gate over `routed` experts, top-k, the EXL3 shared expert last: w holds routed + 1 experts), the
+ * same kernels and arithmetic, with every scratch buffer in a fixed 8 MiB device array of the library (one a GPU,
+ * held until the process ends); a shape whose scratch exceeds it (about 2 slots x hidden x inter / 32 bytes plus
+ * 50 slots x hidden bytes) returns GFR_EINVAL. Allocates nothing. The array keeps the last call's contents; calls that
+ * overlap on one GPU race on it. out [hidden] fp32; picks / weights [topk + 1] copies of the routing (may be NULL). */
+int gfr_moe_token_static(hipStream_t stream, const gfr_exl3_experts* w, int routed, int topk, const uint16_t* input,
+                         const float* logits, float* out, int32_t* picks, float* weights);  /* rows at or below run the decode path (default 4, max 64) */
 /* rows == 1 runs three launches: gate/up GEMV (router and input rotation fused), down GEMV (gate/up epilogue fused),
  * sum of the down parts + combine. */
 /* The layer's router gate: bias == NULL (default) the softmax gate of gfr_route_topk; else GLM's gate of
