@@ -4,12 +4,14 @@
 A step is one MoE layer on one token: router (softmax top-4) -> grouping -> rotated gate/up trellis GEMV -> limited
 SwiGLU epilogue -> down GEMV -> epilogue -> weighted combine, with hidden 2048, 64 routed + 1 shared EXL3 expert,
 intermediate 1536, K = 4 bits. Inputs are seeded synthetic tensors already resident in HBM. Steps run as HIP-graph
-replays; each step uses one of `--copies` distinct copies of the layer's expert weights (8 x 308 MB > the 256 MB
-Infinity Cache) and a fresh routing, so weights stream from HBM.
+replays; each step uses one of `--copies` distinct copies of the layer's expert weights (16 x 308 MB; a copy comes
+back after 15 other token-layers, about 356 MB of other traffic, more than the 256 MB Infinity Cache holds) and a
+fresh routing, so weights stream from HBM.
 
 Also measured in the same run:
-  roofline      the dominant kernel (the gate/up grouped GEMV) timed alone with HIP events on its stream, its
-                algorithmic bytes per launch / average launch time against the 8 TB/s HBM peak;
+  roofline      the dominant kernel (the layer's gate/up launch) timed inside the layer's own launch sequence with
+                HIP events on its stream, its algorithmic bytes per launch / average launch time against the 8 TB/s
+                HBM peak, with the down launch and the whole layer beside it;
   cpu_baseline  the scalar CPU oracle (decode + fp32 matvec of the token's 5 experts, oracle/gfr_oracle.c) on a
                 bounded sample of tokens, 1 thread;
   prefill       config 4 (8192 tokens, uniform top-4) through the prefill path, against the fp16 MFMA peak;
@@ -69,17 +71,20 @@ def replay_plan(steps, glen, full, rest):
 
 
 def decode_bench(args):
+    """Config 2: `args.steps` bs=1 layer steps as graph replays. Step j uses weight copy j % copies and routing
+    j % routings; the warm-up replays steps from the middle of the cycle, so the timed replay does not start on the
+    copies it just touched. Also times the layer's first launch alone and its first two launches (the same steps,
+    gfr_moe_set_launches), which gives each launch's share of a step inside the layer's own sequence."""
     import torch
     import gfr_moe
     import synth
-    dev = "cuda"
     stream = torch.cuda.Stream()
     copies = [synth.experts(E + 1, D, N, BITS, seed=1000 + 17 * c) for c in range(args.copies)]
     R = args.routings
     xs = synth.activations(R, D, 5)
     logits = synth.logits(R, E, 6)
     moe = gfr_moe.Moe(D, N, E, TOPK, 1)
-    glen = min(args.steps, R)
+    glen = min(args.steps, 8 * args.copies)
 
     def step(j):
         return lambda: moe.run(copies[j % len(copies)], xs[j % R:j % R + 1], logits[j % R:j % R + 1], 1,
@@ -89,12 +94,19 @@ def decode_bench(args):
         for j in range(len(copies)):
             step(j)()
     stream.synchronize()
-    full = graph_of([step(j) for j in range(glen)], stream)
-    rest = graph_of([step(j) for j in range(args.steps % glen)], stream) if args.steps % glen else None
-    wplan = replay_plan(max(args.warmup, 1), glen, full, graph_of([step(j) for j in range(max(args.warmup, 1) % glen)],
-                                                                  stream) if max(args.warmup, 1) % glen else None)
-    time_graphs(wplan, stream)
-    secs = time_graphs(replay_plan(args.steps, glen, full, rest), stream)
+    warm0 = glen // 2
+    per_launch = {}
+    for launches in (1, 2, 0):
+        moe.set_launches(launches)
+        full = graph_of([step(j) for j in range(glen)], stream)
+        rest = graph_of([step(j) for j in range(args.steps % glen)], stream) if args.steps % glen else None
+        nw = max(args.warmup, 1)
+        warm = graph_of([step(warm0 + j) for j in range(min(nw, glen))], stream)
+        time_graphs([warm] * max(nw // glen, 1), stream)
+        per_launch[launches] = time_graphs(replay_plan(args.steps, glen, full, rest), stream)
+        del full, rest, warm
+    moe.set_launches(0)
+    secs = per_launch[0]
     # the replayed layer computed what an eager run of the last replayed step computes
     replayed = moe.output[0].clone()
     with torch.cuda.stream(stream):
@@ -102,60 +114,34 @@ def decode_bench(args):
     stream.synchronize()
     if not (torch.isfinite(replayed).all() and torch.equal(replayed, moe.output[0])):
         raise RuntimeError("graph-replayed MoE layer differs from the eager run")
-    return secs, copies, xs, logits, stream
+    launches_us = {"gate_up": per_launch[1] / args.steps * 1e6,
+                   "down": (per_launch[2] - per_launch[1]) / args.steps * 1e6,
+                   "finish": (per_launch[0] - per_launch[2]) / args.steps * 1e6}
+    return secs, copies, xs, logits, stream, launches_us
 
 
-def gemv_roofline(args, copies, stream):
-    """The gate/up grouped GEMV of the bs=1 layer, alone: 5 distinct experts x 2 matrices x 2048 x 1536 at 4 bits."""
-    import numpy as np
-    import torch
-    import gfr_moe
-    import synth
-    L = gfr_moe.lib()
-    R = args.routings
-    rng = np.random.default_rng(11)
-    groups = []
-    g = gfr_moe.Grouping(E + 1, SLOTS, 1)
-    for j in range(R):
-        p = np.append(rng.choice(E, TOPK, replace=False), E).astype(np.int32)[None]
-        g.run(torch.from_numpy(p).cuda(), 1)
-        groups.append((g.ids.clone(), g.count.clone(), g.members.clone()))
-    torch.cuda.synchronize()
-    X = torch.randn((2, SLOTS, D), device="cuda").half()
-    Z = torch.empty((2 * L.gfr_exl3_gemv_splits(D) * SLOTS * N,), device="cuda")
-    glen = min(args.kernel_launches, R)
-
-    def launch(j):
-        w = copies[j % len(copies)]
-        ids, count, members = groups[j % R]
-        return lambda: gfr_moe._check(L.gfr_exl3_grouped_gemv(
-            stream.cuda_stream, X[0].data_ptr(), X[1].data_ptr(), w.gt.data_ptr(), w.ut.data_ptr(), ids.data_ptr(),
-            count.data_ptr(), members.data_ptr(), Z.data_ptr(), D, N, SLOTS, 1, SLOTS, E + 1, BITS, 2, SLOTS))
-
-    full = graph_of([launch(j) for j in range(glen)], stream)
-    time_graphs([full], stream)
-    n = args.kernel_launches - args.kernel_launches % glen
-    secs = time_graphs([full] * (n // glen), stream)
-    per = secs / n
-    weight_bytes = SLOTS * 2 * D * N * BITS // 8
-    act_bytes = SLOTS * 2 * D * 2 + SLOTS * 2 * N * 4           # rotated fp16 rows in, fp32 gate/up rows out
-    algo = weight_bytes + act_bytes
-    achieved = algo / per / 1e9
-    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-            "kernel": "expert_gemv_kernel<4,4,4,2,0,1,false> (gate/up grouped trellis GEMV)", "bytes_per_launch": algo,
-            "us_per_launch": round(per * 1e6, 3)}
+def layer_bytes():
+    """Algorithmic HBM bytes of one config-2 token-layer, per launch (each input read once, each output written once):
+    gate/up: 5 experts' gate and up trellis, their input scales, the token, the router logits, the gate/up K-split
+    partials written; down: 5 down trellis, the epilogue's scales, the partials read, the transformed k-block parts
+    written, the down input xd written; finish: the parts read, y and the output written, the routing weights."""
+    slots, skgu, skd = SLOTS, D // 512, N // 128
+    trellis = D * N * BITS // 8
+    gate_up = slots * 2 * trellis + slots * 2 * D * 2 + D * 2 + E * 4 + 2 * skgu * slots * N * 4
+    down = slots * trellis + slots * (3 * N * 2 + D * 2) + 2 * skgu * slots * N * 4 + skd * slots * D * 4 + slots * N * 2
+    finish = skd * slots * D * 4 + slots * D * 4 + D * 4 + slots * 4
+    return {"gate_up": gate_up, "down": down, "finish": finish}
 
 
 def measured_traffic():
     """HBM bytes per launch of the roofline kernel from the committed rocprofv3 --pmc summary (FETCH_SIZE and
     WRITE_SIZE per dispatch, each scaled by the same counter's reading on a plain copy of known size)."""
-    path = os.path.join(ROOT, "profiles", "gemv_c2_traffic.json")
+    path = os.path.join(ROOT, "profiles", "decode_layer_traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         t = json.load(f)
-    return t.get("hbm_bytes_per_launch")
+    return t.get("gate_up_hbm_bytes_per_launch")
 
 
 def calibrate_copy():
@@ -371,14 +357,30 @@ def cpu_baseline(args, copies, xs, logits):
     return one, many
 
 
+def counter_summary(path):
+    """Per-kernel averages of every counter in a rocprofv3 --pmc ... --output-format csv counter_collection.csv (one
+    line per kernel of this library: dispatches, counter = mean value per dispatch)."""
+    import csv
+    import collections
+    sums = collections.defaultdict(lambda: collections.defaultdict(float))
+    disp = collections.defaultdict(set)
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            k = r["Kernel_Name"]
+            sums[k][r["Counter_Name"]] += float(r["Counter_Value"])
+            disp[k].add(r["Dispatch_Id"])
+    for k in sorted(sums, key=lambda k: -len(disp[k])):
+        n = len(disp[k])
+        print(json.dumps({"kernel": k, "dispatches": n, **{c: round(v / n, 1) for c, v in sums[k].items()}}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--copies", type=int, default=8)
+    ap.add_argument("--copies", type=int, default=16)
     ap.add_argument("--routings", type=int, default=64)
-    ap.add_argument("--kernel-launches", type=int, default=2048)
     ap.add_argument("--cpu-tokens", type=int, default=6)
     ap.add_argument("--cpu-threads", type=int, default=16, help="threads of the all-cores CPU baseline (capped "
                     "at the cores this process may use)")
@@ -390,17 +392,41 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary config 1 / 3 / 5 lines")
     ap.add_argument("--extra-launches", type=int, default=4096)
     ap.add_argument("--c5-prefill-rows", type=int, default=16384)
+    ap.add_argument("--counter-summary", metavar="CSV", help="print per-kernel counter averages of a rocprofv3 "
+                    "counter_collection.csv and exit (no GPU work)")
     args = ap.parse_args()
+    if args.counter_summary:
+        counter_summary(args.counter_summary)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     if args.calibrate_copy:
         calibrate_copy()
-    secs, copies, xs, logits, stream = decode_bench(args)
-    log(f"decode: {args.steps} steps in {secs * 1e3:.2f} ms")
-    roof = gemv_roofline(args, copies, stream)
-    log(f"gate/up gemv alone: {roof['us_per_launch']} us, {roof['achieved']} GB/s")
+    secs, copies, xs, logits, stream, launches_us = decode_bench(args)
+    log(f"decode: {args.steps} steps in {secs * 1e3:.2f} ms; per launch (us): {launches_us}")
+    nbytes = layer_bytes()
+    layer_total = sum(nbytes.values())
+    us_step = secs * 1e6 / args.steps
+    gu_gbs = nbytes["gate_up"] / launches_us["gate_up"] / 1e3
+    roof = {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+            "kernel": "expert_gemv_kernel<4,8,4,2,1,1,true> (the layer's gate/up launch: router, input rotation, "
+                      "gate and up trellis GEMV)",
+            "bytes_per_launch": nbytes["gate_up"], "us_per_launch": round(launches_us["gate_up"], 3),
+            "timing": "HIP events on the layer's stream around graph replays of the layer cut after its first launch "
+                      "(gfr_moe_set_launches(1)); includes the launch's share of the inter-kernel gaps",
+            "down": {"kernel": "down_gemv_kernel<4,1>", "bytes_per_launch": nbytes["down"],
+                     "us_per_launch": round(launches_us["down"], 3),
+                     "gbs": round(nbytes["down"] / launches_us["down"] / 1e3, 1),
+                     "frac": round(nbytes["down"] / launches_us["down"] / 1e3 / HBM_PEAK_GBS, 4)},
+            "finish": {"kernel": "sum_finish_kernel", "bytes_per_launch": nbytes["finish"],
+                       "us_per_launch": round(launches_us["finish"], 3)},
+            "layer": {"bytes_per_step": layer_total, "us_per_step": round(us_step, 3),
+                      "gbs": round(layer_total / us_step / 1e3, 1),
+                      "frac": round(layer_total / us_step / 1e3 / HBM_PEAK_GBS, 4)}}
+    log(f"gate/up launch: {roof['us_per_launch']} us, {roof['achieved']} GB/s; layer {roof['layer']['gbs']} GB/s")
     prefill = None
     if not args.no_prefill:
         prefill = prefill_bench(args, copies, stream)
@@ -420,7 +446,8 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
         "config": {"workload": "config 2: one MoE layer, bs=1 decode, hidden 2048, 64 routed + 1 shared EXL3 "
                                "experts, inter 1536, top-4, K=4", "global_batch": 1, "seq_len": 1,
-                   "parallelism": "single-gpu", "weight_copies": args.copies, "routings": args.routings},
+                   "parallelism": "single-gpu", "weight_copies": args.copies, "routings": args.routings,
+                   "weight_bytes_cycled": int(args.copies * (E + 1) * 3 * D * N * BITS // 8)},
         "roofline": roof, "cpu_baseline": cpu, "cpu_baseline_all_cores": cpu_all, "prefill": prefill,
         "other_configs": extra,
     }

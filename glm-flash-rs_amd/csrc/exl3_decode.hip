@@ -178,7 +178,8 @@ __device__ __forceinline__ void load_tile_acts(const uint32_t* tile, uint32_t (&
 template <int K, int KTW, int NW, int MATS, int XSRC, int RB, bool ROUTE1>
 __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) {
     constexpr int KC = NW * KTW;
-    static_assert(XSRC == 0 || KTW == 8, "a wave that builds its activations covers one 128-point block");
+    static_assert(XSRC == 0 || KTW == 8 || KTW == 4 || KTW == 2,
+                  "a wave that builds its activations covers one 128-point block or a part of one");
     static_assert(XSRC != 0 || RB * KTW <= 64, "one lane a (member, k tile) when staging rotated rows");
     __shared__ __attribute__((aligned(16))) uint32_t xs[NW][RB][KTW * 16];   // activations, each twice
     __shared__ float red[NW][RB][128];
@@ -196,7 +197,7 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
     uint32_t xearly = 0;   // ROUTE1 with the fused rotation: the token's input pair, loaded while it is routed
     if constexpr (ROUTE1) {
         if constexpr (XSRC == 1)
-            xearly = *reinterpret_cast<const uint32_t*>(a.x0 + kt0 * 16 + 2 * lane);
+            xearly = *reinterpret_cast<const uint32_t*>(a.x0 + (kt0 & ~7) * 16 + 2 * lane);
         int pick;
         float weight;
         route_token_regs(a.logits, a.routed, a.slots - 1, a.routed, pick, weight, RouteGate{a.route_bias, a.route_scale});
@@ -233,14 +234,15 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
     uint4 va = {0, 0, 0, 0}, vb = {0, 0, 0, 0};           // XSRC 0: this lane's k tile of one member
     auto load_acts = [&](int r0, int nr) {
         if constexpr (XSRC == 1) {
-            sv = *reinterpret_cast<const uint32_t*>((mat ? a.suh1 : a.suh0) + (size_t)e * a.Kin + kt0 * 16 + 2 * lane);
+            // the whole 128-point block of the wave's k tiles (the transform needs all of it)
+            sv = *reinterpret_cast<const uint32_t*>((mat ? a.suh1 : a.suh0) + (size_t)e * a.Kin + (kt0 & ~7) * 16 + 2 * lane);
             if constexpr (ROUTE1) {
                 xv[0] = xearly;
             } else {
 #pragma unroll
                 for (int m = 0; m < RB; ++m) {
                     const int row = __builtin_amdgcn_readlane(code, r0 + (m < nr ? m : 0)) >> 5;
-                    xv[m] = *reinterpret_cast<const uint32_t*>(a.x0 + (size_t)row * a.x_stride + kt0 * 16 + 2 * lane);
+                    xv[m] = *reinterpret_cast<const uint32_t*>(a.x0 + (size_t)row * a.x_stride + (kt0 & ~7) * 16 + 2 * lane);
                 }
             }
         } else {
@@ -271,7 +273,10 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
             for (int m = 0; m < RB; ++m)
                 if (m < nr) {
                     fwht128_w64(v[m], lane);
-                    store_block(&xs[wave][m][0], v[m], lane);
+                    // this wave's k tiles of the block: its lanes [8 sub, 8 (sub + KTW)), at slot 0 onwards
+                    const int sub = kt0 & 7;
+                    if (KTW == 8 || (lane >= 8 * sub && lane < 8 * (sub + KTW)))
+                        store_block(&xs[wave][m][0] - 16 * sub, v[m], lane);
                 }
             __builtin_amdgcn_sched_barrier(0);
             issue();
@@ -388,12 +393,31 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
 // order. Every sum has a fixed order, and a row's result never depends on the other rows.
 //   a.Kin = intermediate size (the down input), a.N = hidden size; a.suh0 = suh_d, a.svh_g / svh_u the gate / up
 //   output scales, a.t0 the down trellis, a.zgu / SKgu the gate/up partials, a.z = Zd, a.x1 (reused) = svh_d.
+#ifndef GFR_DOWN_XCD
+#define GFR_DOWN_XCD 1
+#endif
+// The dispatcher hands workgroup L (linear launch order) to XCD L % 8, and each XCD has its own L2. Renumber the grid
+// so that XCD x runs the logical range [x T/8, (x+1) T/8) with y (the output row block) fastest, then x, then z: the
+// row blocks of one (unit, k block) then share one L2 for the partials and scales they all read. Grids whose size
+// is not a multiple of 8 keep the launch order.
+__device__ inline void xcd_grouped(int& bx, int& by, int& bz) {
+    bx = blockIdx.x; by = blockIdx.y; bz = blockIdx.z;
+    const int gx = gridDim.x, gy = gridDim.y, T = gx * gy * gridDim.z;
+    if (!GFR_DOWN_XCD || (T & 7)) return;
+    const int L = bx + gx * (by + gy * bz), g = (L & 7) * (T >> 3) + (L >> 3);
+    by = g % gy;
+    bx = (g / gy) % gx;
+    bz = g / (gy * gx);
+}
+
 template <int K, int RB>
 __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t xs[RB][128];   // the k block's activations, each twice
     __shared__ float red[4][RB][128];
     __shared__ float2 psum[4][RB][2][64];                            // each wave's quarter of the gate / up splits
-    const int u = blockIdx.x % a.ucap, hb = blockIdx.y, kb = blockIdx.z, c0 = (int)(blockIdx.x / a.ucap) * RB;
+    int bx, hb, kb;
+    xcd_grouped(bx, hb, kb);
+    const int u = bx % a.ucap, c0 = (bx / a.ucap) * RB;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, t = lane >> 3, i = lane & 7;
     const int KT = a.Kin >> 4, NT = a.N >> 4;
     const size_t tslot = (((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * 4 + wave;
@@ -878,9 +902,16 @@ hipError_t launch_sum_finish(hipStream_t s, const float* Zd, float* y, int rows,
 }
 
 // One linear with its input rotation fused (XSRC 1, fp16 input): Z[split][n] partials of
-// W_q[0] over one row, SK = kin / 128 / NW splits in fixed order (gemv_linear_splits).
-static int nw_linear(int kin) { return (kin / 128) % 4 == 0 ? 4 : 2; }
-int gemv_linear_splits(int kin) { return kin / 128 / nw_linear(kin); }
+// W_q[0] over one row, one split a 256-k pair of blocks (gemv_linear_splits), added in order by the epilogue launch.
+// Four waves a split, four k tiles each: (kin / 256) x (n / 128) workgroups, 384 waves at config 1 (measured
+// against 192, 768 and other shapes on MI355X: 6.8 against 7.1-8.7 us).
+#ifndef GFR_LIN_KTW
+#define GFR_LIN_KTW 4
+#endif
+#ifndef GFR_LIN_NW
+#define GFR_LIN_NW 4
+#endif
+int gemv_linear_splits(int kin) { return kin / 16 / (GFR_LIN_KTW * GFR_LIN_NW); }
 hipError_t launch_linear_fused(hipStream_t s, const uint16_t* x, const uint16_t* suh, const uint32_t* trellis,
                                const int* uids, const int* ucount, const int* members, float* z, int kin, int n,
                                int bits) {
@@ -889,12 +920,10 @@ hipError_t launch_linear_fused(hipStream_t s, const uint16_t* x, const uint16_t*
     a.uids = uids; a.ucount = ucount; a.members = members; a.z = z; a.Kin = kin; a.N = n; a.P = 1;
     a.SK = gemv_linear_splits(kin); a.maxm = 1; a.slots = 1; a.E = 1; a.ucap = 1;
     const dim3 grid(1, n / 128, a.SK);
-    const bool four = nw_linear(kin) == 4;
     switch (bits) {
 #define GFR_LIN(KB)                                                                                                 \
         case KB:                                                                                                  \
-            if (four) expert_gemv_kernel<KB, 8, 4, 1, 1, 1, false><<<grid, 256, 0, s>>>(a);                         \
-            else expert_gemv_kernel<KB, 8, 2, 1, 1, 1, false><<<grid, 128, 0, s>>>(a);                              \
+            expert_gemv_kernel<KB, GFR_LIN_KTW, GFR_LIN_NW, 1, 1, 1, false><<<grid, 64 * GFR_LIN_NW, 0, s>>>(a);   \
             break;
         GFR_LIN(2) GFR_LIN(3) GFR_LIN(4) GFR_LIN(5)
 #undef GFR_LIN

@@ -109,6 +109,7 @@ struct gfr_moe {
     int shared_exl3;           // 1: the shared expert is EXL3 (weights hold routed + 1 experts); 0: its output is the
                                // caller's (gfr_moe_run_shared), weights hold the routed experts only
     float* logits;             // [max_rows][routed] router logits of gfr_moe_run_router
+    int launches;              // measurement: rows == 1 issues only the first `launches` launches (0: all)
 };
 
 extern "C" {
@@ -171,7 +172,8 @@ namespace {
 int experts_run(gfr_experts* ex, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
                 int input_stride, const int32_t* picks, const int32_t* ids, const int32_t* count,
                 const int32_t* members, int rows, int maxm, const float* weights, float* out,
-                const gfr::RouteOne* route = nullptr, const float* shared = nullptr, int shared_stride = 0) {
+                const gfr::RouteOne* route = nullptr, const float* shared = nullptr, int shared_stride = 0,
+                int launches = 0) {
     const int P = rows * ex->slots, D = ex->hidden, N = ex->inter;
     const int maxu = P < w->experts ? P : w->experts;
     hipError_t e;
@@ -180,12 +182,14 @@ int experts_run(gfr_experts* ex, hipStream_t stream, const gfr_exl3_experts* w, 
                                        route)) !=
         hipSuccess)
         return hip_fail(e, "gate/up gemv");
+    if (launches == 1) return 0;
     const int skgu = gfr::gemv_gateup_splits(D);
     if ((e = gfr::launch_expert_down(stream, ex->zgu, D, skgu, w->svh_g, w->svh_u, w->suh_d, 10.f, ex->xd, w->dt,
                                      w->svh_d,
                                      ids, count, members, ex->zd, N, P, rows, maxm, ex->slots, w->experts, w->bits,
                                      maxu)) != hipSuccess)
         return hip_fail(e, "down gemv");
+    if (launches == 2) return 0;
     if ((e = gfr::launch_sum_finish(stream, ex->zd, ex->y, rows, P, D, gfr::gemv_down_splits(N), ex->slots,
                                     ex->exl3_slots, weights, shared, shared_stride, out)) != hipSuccess)
         return hip_fail(e, "down epilogue");
@@ -419,7 +423,7 @@ int gfr_moe_create_shared(gfr_moe** out, int hidden, int inter, int routed, int 
     gfr_moe* m = new gfr_moe{hidden, inter, routed, topk, topk + 1, max_rows,
                              MOE_DECODE_ROWS < max_rows ? MOE_DECODE_ROWS : max_rows,
                              nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 1.f,
-                             shared_exl3 ? 1 : 0, nullptr};
+                             shared_exl3 ? 1 : 0, nullptr, 0};
     const int exl3_slots = shared_exl3 ? topk + 1 : topk, experts = shared_exl3 ? routed + 1 : routed;
     m->route_bias = nullptr;   // the softmax gate until gfr_moe_set_router
     m->route_scale = 1.f;
@@ -475,7 +479,7 @@ int moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uin
             const gfr::RouteOne r{logits, m->route_bias, m->route_scale, m->routed, m->picks, m->weights, g->ids,
                                   g->count, g->members};
             return experts_run(m->dec, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members, 1,
-                               g->max_rows, m->weights, m->out, &r, shared, shared_stride);
+                               g->max_rows, m->weights, m->out, &r, shared, shared_stride, m->launches);
         }
         // four launches: route + group, gate/up (+ rotation), down (+ gate/up epilogue), down epilogue (+ combine)
         if ((e = gfr::launch_route_group(stream, logits, rows, m->routed, m->topk, m->picks, m->weights, g->ids,
@@ -640,6 +644,13 @@ int gfr_router_logits(hipStream_t stream, const uint16_t* input, int input_strid
         return fail(GFR_EINVAL, "routed %d rows %d stride %d", routed, rows, input_stride);
     hipError_t e = gfr::launch_router_logits(stream, input, input_stride, router_weight, hidden, routed, rows, logits);
     if (e != hipSuccess) return hip_fail(e, "router logits");
+    return 0;
+}
+
+int gfr_moe_set_launches(gfr_moe* m, int launches) {
+    if (!m) return fail(GFR_EINVAL, "null moe");
+    if (launches < 0 || launches > 3) return fail(GFR_EINVAL, "launches %d outside 0..3", launches);
+    m->launches = launches == 3 ? 0 : launches;
     return 0;
 }
 

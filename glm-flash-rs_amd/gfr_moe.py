@@ -62,6 +62,7 @@ def _load() -> ctypes.CDLL:
         "gfr_moe_run_shared": ([VP, P, P, P, P, P, I, I], I),
         "gfr_moe_run_router": ([VP, P, P, P, P, P, I, I], I),
         "gfr_router_logits": ([P, P, I, P, I, I, I, P], I),
+        "gfr_moe_set_launches": ([VP, I], I),
         "gfr_moe_token_static": ([P, ctypes.POINTER(_Exl3Struct), I, I, P, P, P, P, P], I),
         "gfr_moe_destroy": ([VP], I),
         "gfr_linear_create": ([ctypes.POINTER(VP), I, I, I], I),
@@ -299,6 +300,10 @@ class Moe(_Engine):
 
     def set_decode_rows(self, n: int):
         _check(lib().gfr_moe_set_decode_rows(self._h, n))
+
+    def set_launches(self, n: int):
+        """Measurement aid (gfr_moe_set_launches): a one-row run issues only its first n launches (0: all)."""
+        _check(lib().gfr_moe_set_launches(self._h, n))
 
     def set_router(self, bias: torch.Tensor = None, scale: float = 2.5):
         """GLM's gate (the reference's topk(logits, bias, picks, weights, 2.5), moe.rs:89-99) with this fp32 bias

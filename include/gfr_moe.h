@@ -144,6 +144,10 @@ int gfr_moe_token_static(hipStream_t stream, const gfr_exl3_experts* w, int rout
 /* The layer's router gate: bias == NULL (default) the softmax gate of gfr_route_topk; else GLM's gate of
  * gfr_route_topk_biased with this bias [routed] (device, fp32; must outlive the runs) and scale (2.5 for GLM). */
 int gfr_moe_set_router(gfr_moe* m, const float* bias, float scale);
+/* Measurement aid, no reference counterpart: a one-row run issues only its first `launches` launches (1: the gate/up
+ * GEMV with the router; 2: and the down GEMV; 0 or 3: all three), so that a caller can time each launch inside the
+ * layer's own sequence. Outputs of a shortened run are incomplete. */
+int gfr_moe_set_launches(gfr_moe* m, int launches);
 int gfr_moe_destroy(gfr_moe* m);
 
 /* ---- The router alone (the reference's Triton topk, moe.rs:89-100; source absent, semantics of the benchmark):
