@@ -36,7 +36,7 @@ namespace gfr {
 #endif
 constexpr int PF_BM = PF_BM_ROWS;   // member rows an item (256: one workgroup a CU; 128: two)
 #ifndef PF_BM4_ROWS
-#define PF_BM4_ROWS 160
+#define PF_BM4_ROWS 176
 #endif
 constexpr int PF_BM4 = PF_BM4_ROWS;  // member rows an item for K = 4 (fits two workgroups a CU in LDS)
 static_assert(PF_BM4 >= PF_BM, "allocation bound");
@@ -373,7 +373,7 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
     constexpr int XLOADS = (MATS * RB + 3) / 4;          // direct loads of rows a wave a step (the last repeated)
     constexpr int TL = (K + 3) / 4;                      // direct loads of trellis words a wave a step
     constexpr int LOADS = XLOADS + TL;
-    static_assert((BM == 256 || BM == 160 || BM == 128 || BM == 32) && NS <= 8, "tile shape");
+    static_assert((BM == 256 || BM == 176 || BM == 160 || BM == 128 || BM == 32) && NS <= 8, "tile shape");
     __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
     __shared__ int rows_sh[BM];
     // K != 4: each lane decodes one trellis lane's 32 values of one tile and the fragments are exchanged here
@@ -683,11 +683,13 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
         if (c * ER >= nrows) return;
 #pragma unroll
         for (int bb = 0; bb < ER / 16; ++bb)
+            if (c * (ER / 16) + bb < RB)                // the last chunk of a BM that is not a multiple of ER
 #pragma unroll
-            for (int t4 = 0; t4 < 4; ++t4) {
-                const int row = 16 * bb + (lane & 15);
-                *reinterpret_cast<f4_t*>(ep + row * EPITCH + ncol + t4 * 16) = acc[t4][c * (ER / 16) + bb];
-            }
+                for (int t4 = 0; t4 < 4; ++t4) {
+                    const int row = 16 * bb + (lane & 15);
+                    *reinterpret_cast<f4_t*>(ep + row * EPITCH + ncol + t4 * 16) =
+                        acc[t4][min(c * (ER / 16) + bb, RB - 1)];
+                }
         __syncthreads();
 #pragma unroll
         for (int g = 0; g < ER / 16; ++g) {
@@ -742,12 +744,13 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
         }
         __syncthreads();
     };
-    static_assert(BM % ER == 0 && ER % 16 == 0 && BM / ER <= 5, "epilogue chunks");
+    static_assert(ER % 16 == 0 && (BM + ER - 1) / ER <= 6, "epilogue chunks");
     chunk(std::integral_constant<int, 0>{});
     chunk(std::integral_constant<int, 1>{});
     chunk(std::integral_constant<int, 2>{});
     chunk(std::integral_constant<int, 3>{});
     chunk(std::integral_constant<int, 4>{});
+    chunk(std::integral_constant<int, 5>{});
 #ifdef GFR_PF_TRACE
     if (tid == 0) {
         uint64_t* o = a.trace + (size_t)(MATS == 2 ? 0 : 16384) * 8 + (size_t)blockIdx.x * 8;
