@@ -81,6 +81,7 @@ struct gfr_grouping {
     int experts, slots, max_rows;
     uint32_t* bits;
     int *prefix, *counts, *ids, *count, *members;
+    uint8_t* first;            // [experts][max_rows]: the first slot of row r that holds expert e (large windows)
 };
 
 struct gfr_experts {
@@ -125,11 +126,12 @@ int gfr_grouping_create(gfr_grouping** out, int experts, int slots, int max_rows
     if (experts <= 0 || experts > 2048) return fail(GFR_EINVAL, "grouping experts %d outside 1..2048", experts);
     if (slots <= 0 || slots > 32) return fail(GFR_EINVAL, "grouping slots %d outside 1..32", slots);
     if (max_rows <= 0 || max_rows > (1 << 20)) return fail(GFR_EINVAL, "grouping capacity %d", max_rows);
-    gfr_grouping* g = new gfr_grouping{experts, slots, max_rows, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    gfr_grouping* g = new gfr_grouping{experts, slots, max_rows, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
     const size_t nwd = (size_t)(max_rows + 31) / 32;
     int rc;
     if ((rc = alloc_zero(&g->bits, (size_t)experts * nwd, "grouping bits")) ||
         (rc = alloc_zero(&g->prefix, (size_t)experts * nwd, "grouping prefix")) ||
+        (rc = alloc_zero(&g->first, (size_t)experts * max_rows, "grouping first slots")) ||
         (rc = alloc_zero(&g->counts, (size_t)experts, "grouping counts")) ||
         (rc = alloc_zero(&g->ids, (size_t)experts, "grouping ids")) || (rc = alloc_zero(&g->count, 1, "count")) ||
         (rc = alloc_zero(&g->members, (size_t)experts * max_rows, "grouping members"))) {
@@ -149,8 +151,8 @@ int gfr_grouping_run(gfr_grouping* g, hipStream_t stream, const int32_t* picks, 
         e = gfr::launch_group_small(stream, picks, rows, g->slots, g->experts, g->ids, g->count, g->members,
                                     g->max_rows);
     else
-        e = gfr::launch_group_large(stream, picks, rows, g->slots, g->experts, g->bits, g->prefix, g->counts, g->ids,
-                                    g->count, g->members, g->max_rows);
+        e = gfr::launch_group_large(stream, picks, rows, g->slots, g->experts, g->bits, g->first, g->prefix, g->counts,
+                                    g->ids, g->count, g->members, g->max_rows);
     if (e != hipSuccess) return hip_fail(e, "grouping launch");
     return 0;
 }
@@ -161,7 +163,7 @@ int32_t* gfr_grouping_members(const gfr_grouping* g) { return g ? g->members : n
 
 int gfr_grouping_destroy(gfr_grouping* g) {
     if (!g) return 0;
-    free_all({g->bits, g->prefix, g->counts, g->ids, g->count, g->members});
+    free_all({g->bits, g->prefix, g->counts, g->ids, g->count, g->members, g->first});
     delete g;
     return 0;
 }
@@ -507,7 +509,19 @@ int moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uin
         if ((e = gfr::launch_route(stream, logits, rows, m->routed, m->topk, m->routed, m->picks, m->weights,
                                    m->route_bias, m->route_scale)) != hipSuccess)
             return hip_fail(e, "route");
-        if ((rc = gfr_grouping_run(g, stream, m->picks, rows))) return rc;
+        if (rows <= gfr::GROUP_SMALL_ROWS) {
+            if ((rc = gfr_grouping_run(g, stream, m->picks, rows))) return rc;
+        } else {
+            // the three grouping launches, the last of which also writes the item plan
+            int *pu, *pi, *pp;
+            gfr::prefill_plan_buffers(m->pre, &pu, &pi, &pp);
+            if ((e = gfr::launch_group_large(stream, m->picks, rows, g->slots, g->experts, g->bits, g->first, g->prefix,
+                                             g->counts, g->ids, g->count, g->members, g->max_rows,
+                                             gfr::prefill_item_rows(m->pre, rows, w->bits), pu, pi, pp)) !=
+                hipSuccess)
+                return hip_fail(e, "grouping launch");
+            planned = true;
+        }
     }
     // windows on the split-K programs fold the combine into their down epilogue
     bool combined = false;

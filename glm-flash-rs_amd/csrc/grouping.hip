@@ -38,13 +38,6 @@ __device__ __forceinline__ int block_scan(int x, int* scratch, int* total) {
     return x + off;
 }
 
-// First slot of row r that holds expert e (the row is known to hold it).
-__device__ __forceinline__ int first_slot(const int* __restrict__ picks, int r, int slots, int e) {
-    int s = 0;
-    while (s < slots - 1 && picks[r * slots + s] != e) ++s;
-    return s;
-}
-
 // One workgroup (blockDim.x a multiple of 64, <= 1024). lds: E * ceil(rows / 32) bitmap words + 2 E ints.
 // picks may live in LDS or global memory.
 // With `plan` (the prefill engine's item plan, bm rows an item): plan_ucnt[u] = members of used expert u,
@@ -161,18 +154,22 @@ __global__ void __launch_bounds__(1024) route_group_kernel(const float* __restri
 }
 
 // Large windows, launch 1: the 256 rows of this workgroup marked in an LDS bitmap [E][8], stored to
-// bits[e][NWD] (each global word is owned by exactly one workgroup, so no clear launch is needed).
+// bits[e][NWD] (each global word is owned by exactly one workgroup, so no clear launch is needed), and
+// first[e][r] = the first slot of row r that holds e (the slots stored last to first, so the first one stays).
 __global__ void __launch_bounds__(256) group_mark_kernel(const int* __restrict__ picks, int rows, int slots, int E,
-                                                         uint32_t* __restrict__ bits) {
+                                                         uint32_t* __restrict__ bits, uint8_t* __restrict__ first) {
     extern __shared__ uint32_t lb[];                         // [E][8]
     const int NWD = (rows + 31) >> 5;
     for (int i = threadIdx.x; i < E * 8; i += blockDim.x) lb[i] = 0;
     __syncthreads();
     const int r = blockIdx.x * 256 + threadIdx.x;
     if (r < rows)
-        for (int s = 0; s < slots; ++s) {
+        for (int s = slots - 1; s >= 0; --s) {
             const int e = picks[r * slots + s];
-            if (e >= 0 && e < E) atomicOr(&lb[e * 8 + (threadIdx.x >> 5)], 1u << (r & 31));
+            if (e >= 0 && e < E) {
+                atomicOr(&lb[e * 8 + (threadIdx.x >> 5)], 1u << (r & 31));
+                first[(size_t)e * rows + r] = (uint8_t)s;
+            }
         }
     __syncthreads();
     for (int i = threadIdx.x; i < E * 8; i += blockDim.x) {
@@ -199,44 +196,79 @@ __global__ void __launch_bounds__(256) group_prefix_kernel(const uint32_t* __res
     if (threadIdx.x == 0) counts[e] = total;
 }
 
-// Launch 3, workgroup per expert: its place among the used experts, ids / count, its members and its -1 tail.
+// Launch 3, workgroup per expert: its place among the used experts, ids / count, its members and its -1 tail. A
+// thread per row: a member's position is the popcount prefix of its bitmap word plus the set bits below it in the
+// word, so no thread walks an expert's rows in sequence. With `plan` (bm rows an item) it also writes the prefill
+// engine's item plan, as prefill_plan_kernel would from the finished table: plan_ucnt[u] = members of used expert
+// u, plan_items = (u << 16) | pass for the ceil(members / bm) passes of each u in u order, plan[0] = item count.
 __global__ void __launch_bounds__(256) group_scatter_kernel(const int* __restrict__ picks, int rows, int slots,
                                                             int E, const uint32_t* __restrict__ bits,
+                                                            const uint8_t* __restrict__ first,
                                                             const int* __restrict__ prefix,
                                                             const int* __restrict__ counts, int* __restrict__ ids,
                                                             int* __restrict__ count, int* __restrict__ members,
-                                                            int maxm) {
+                                                            int maxm, int bm, int* __restrict__ plan_ucnt,
+                                                            int* __restrict__ plan_items, int* __restrict__ plan) {
     __shared__ int scan_scratch[16];
-    __shared__ int below_sh, used_sh;
+    __shared__ int tot_sh[4];
     const int e = blockIdx.x, NWD = (rows + 31) >> 5;
-    int below = 0, used = 0;
+    int below = 0, used = 0, ibelow = 0, itotal = 0;
     for (int q = threadIdx.x; q < E; q += blockDim.x) {
-        const int c = counts[q] > 0;
-        used += c;
-        below += (q < e) & c;
+        const int c = counts[q], np = plan ? (c + bm - 1) / bm : 0;
+        used += c > 0;
+        below += (q < e) & (c > 0);
+        itotal += np;
+        ibelow += q < e ? np : 0;
     }
-    int t1, t2;
-    block_scan(below, scan_scratch, &t1);
-    block_scan(used, scan_scratch, &t2);
-    if (threadIdx.x == 0) {
-        below_sh = t1;
-        used_sh = t2;
+    int t[4];
+    block_scan(below, scan_scratch, &t[0]);
+    block_scan(used, scan_scratch, &t[1]);
+    if (plan) {
+        block_scan(ibelow, scan_scratch, &t[2]);
+        block_scan(itotal, scan_scratch, &t[3]);
     }
+    if (threadIdx.x == 0)
+        for (int i = 0; i < 4; ++i) tot_sh[i] = t[i];
     __syncthreads();
-    below = below_sh;
-    used = used_sh;
+    below = tot_sh[0];
+    used = tot_sh[1];
     const int ce = counts[e];
-    if (e == 0 && threadIdx.x == 0) *count = used;
+    if (e == 0 && threadIdx.x == 0) {
+        *count = used;
+        if (plan) plan[0] = tot_sh[3];
+    }
     if (ce > 0) {
         const int u = below;
         if (threadIdx.x == 0) ids[u] = e;
-        for (int w = threadIdx.x; w < NWD; w += blockDim.x) {
-            uint32_t b = bits[(size_t)e * NWD + w];
-            int off = prefix[(size_t)e * NWD + w];
-            while (b) {
-                const int r = w * 32 + __builtin_ctz(b);
-                members[(size_t)u * maxm + off++] = r * 32 + first_slot(picks, r, slots, e);
-                b &= b - 1;
+        if (plan) {
+            const int np = (ce + bm - 1) / bm, first = tot_sh[2];
+            if (threadIdx.x == 0) plan_ucnt[u] = ce;
+            for (int k = threadIdx.x; k < np; k += blockDim.x) plan_items[first + k] = (u << 16) | k;
+        }
+        // rows in batches of UB a thread: every load of a batch is issued before any of its values is used (the
+        // empty asm keeps the compiler from sinking a load into the branch that uses it), so a batch costs one
+        // round trip; first[] of a row outside the expert is loaded and never used
+        constexpr int UB = 8;
+        const uint32_t* be = bits + (size_t)e * NWD;
+        const int* pe = prefix + (size_t)e * NWD;
+        const uint8_t* fe = first + (size_t)e * rows;
+        for (int r0 = threadIdx.x; r0 < rows; r0 += UB * blockDim.x) {
+            uint32_t b[UB];
+            int pos[UB], sl[UB];
+#pragma unroll
+            for (int k = 0; k < UB; ++k) {
+                const int r = min(r0 + k * (int)blockDim.x, rows - 1);
+                b[k] = be[r >> 5];
+                pos[k] = pe[r >> 5];
+                sl[k] = fe[r];
+            }
+#pragma unroll
+            for (int k = 0; k < UB; ++k) __asm__ volatile("" : "+v"(b[k]), "+v"(pos[k]), "+v"(sl[k]));
+#pragma unroll
+            for (int k = 0; k < UB; ++k) {
+                const int r = r0 + k * (int)blockDim.x;
+                if (r < rows && ((b[k] >> (r & 31)) & 1u))
+                    members[(size_t)u * maxm + pos[k] + __popc(b[k] & ((1u << (r & 31)) - 1u))] = r * 32 + sl[k];
             }
         }
         for (int j = ce + threadIdx.x; j < maxm; j += blockDim.x) members[(size_t)u * maxm + j] = -1;
@@ -280,14 +312,16 @@ hipError_t launch_route_group(hipStream_t s, const float* logits, int rows, int 
 }
 
 hipError_t launch_group_large(hipStream_t s, const int* picks, int rows, int slots, int E, uint32_t* bits,
-                              int* prefix, int* counts, int* ids, int* count, int* members, int maxm) {
+                              uint8_t* first, int* prefix, int* counts, int* ids, int* count, int* members, int maxm, int bm,
+                              int* plan_ucnt, int* plan_items, int* plan) {
     if ((size_t)E * 8 * 4 > GROUP_LDS_MAX) return hipErrorInvalidValue;
-    group_mark_kernel<<<(rows + 255) / 256, 256, (size_t)E * 8 * 4, s>>>(picks, rows, slots, E, bits);
+    group_mark_kernel<<<(rows + 255) / 256, 256, (size_t)E * 8 * 4, s>>>(picks, rows, slots, E, bits, first);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     group_prefix_kernel<<<E, 256, 0, s>>>(bits, rows, prefix, counts);
     if ((err = hipGetLastError()) != hipSuccess) return err;
-    group_scatter_kernel<<<E, 256, 0, s>>>(picks, rows, slots, E, bits, prefix, counts, ids, count, members, maxm);
+    group_scatter_kernel<<<E, 256, 0, s>>>(picks, rows, slots, E, bits, first, prefix, counts, ids, count, members, maxm,
+                                            bm, plan_ucnt, plan_items, plan);
     return hipGetLastError();
 }
 

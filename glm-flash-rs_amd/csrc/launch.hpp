@@ -18,8 +18,10 @@ hipError_t launch_route_group(hipStream_t s, const float* logits, int rows, int 
                               float* weights, int* ids, int* count, int* members, int maxm, int bm = 0,
                               int* plan_ucnt = nullptr, int* plan_items = nullptr, int* plan = nullptr,
                               const float* bias = nullptr, float scale = 1.f);
+// With plan (bm rows an item) the scatter launch also writes the prefill engine's item plan.
 hipError_t launch_group_large(hipStream_t s, const int* picks, int rows, int slots, int E, uint32_t* bits,
-                              int* prefix, int* counts, int* ids, int* count, int* members, int maxm);
+                              uint8_t* first, int* prefix, int* counts, int* ids, int* count, int* members, int maxm, int bm = 0,
+                              int* plan_ucnt = nullptr, int* plan_items = nullptr, int* plan = nullptr);
 
 // exl3_decode.hip
 hipError_t launch_decode_tiles(hipStream_t s, const uint32_t* T, int kin, int n, int bits, uint16_t* out);

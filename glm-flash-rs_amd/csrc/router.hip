@@ -20,34 +20,43 @@ __global__ void __launch_bounds__(64) route_kernel(const float* __restrict__ log
 // out[r][n] = sum over slots s (in order) of weights[r][s] * (y[r * slots + s][n] for the EXL3 slots s < exl3_slots,
 // shared[r * shared_stride + n] for the others when the caller gives the shared expert's output, else nothing) --
 // the reference's combine(y, shared, weights, out), moe.rs:171-181. Four columns a thread (16-byte loads and
-// stores), every slot's row in flight at once. D a multiple of 4.
+// stores); the slots in groups of 8, each group's rows in flight at once and added in slot order (a group's 8
+// registers, not one per possible slot, keep the kernel at a few dozen VGPRs and many resident waves). D a multiple
+// of 4.
 __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ y, const float* __restrict__ weights,
                                                       int slots, int exl3_slots, int D,
                                                       const float* __restrict__ shared, int shared_stride,
                                                       float* __restrict__ out) {
     typedef float f4v __attribute__((ext_vector_type(4)));
-    constexpr int MAXS = 32;
+    constexpr int G = 8;
     const int r = blockIdx.y, n = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (n >= D) return;
-    f4v v[MAXS];
-#pragma unroll
-    for (int s = 0; s < MAXS; ++s)
-        if (s < slots) {
-            if (s < exl3_slots)
-                v[s] = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(y + ((size_t)r * slots + s) * D + n));
-            else
-                v[s] = shared ? *reinterpret_cast<const f4v*>(shared + (size_t)r * shared_stride + n) : (f4v){0, 0, 0, 0};
-        }
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = 0; s0 < slots; s0 += G) {
+        f4v v[G];
 #pragma unroll
-    for (int s = 0; s < MAXS; ++s)
-        if (s < slots && (s < exl3_slots || shared)) {
-            const float w = weights[r * slots + s];
-            acc.x += w * v[s].x;
-            acc.y += w * v[s].y;
-            acc.z += w * v[s].z;
-            acc.w += w * v[s].w;
+        for (int j = 0; j < G; ++j) {
+            const int s = s0 + j;
+            if (s < slots) {
+                if (s < exl3_slots)
+                    v[j] = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(y + ((size_t)r * slots + s) * D + n));
+                else
+                    v[j] = shared ? *reinterpret_cast<const f4v*>(shared + (size_t)r * shared_stride + n)
+                                  : (f4v){0, 0, 0, 0};
+            }
         }
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const int s = s0 + j;
+            if (s < slots && (s < exl3_slots || shared)) {
+                const float w = weights[r * slots + s];
+                acc.x += w * v[j].x;
+                acc.y += w * v[j].y;
+                acc.z += w * v[j].z;
+                acc.w += w * v[j].w;
+            }
+        }
+    }
     *reinterpret_cast<float4*>(out + (size_t)r * D + n) = acc;
 }
 
