@@ -855,7 +855,8 @@ static hipError_t launch_gemm(int bits, dim3 grid, hipStream_t s, const PrefillA
 hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_experts* w, const uint16_t* input,
                        int input_stride, const int* picks, const int* ids, const int* count, const int* members,
                        int rows, int maxm, bool shared_x, const float* combine_weights, float* combine_out,
-                       bool* combined, bool planned, const float* combine_shared, int shared_stride) {
+                       bool* combined, bool planned, const float* combine_shared, int shared_stride,
+                       hipEvent_t shared_ready) {
     const PrefillDims& d = fx->d;
     if (combined) *combined = false;
     if (w->bits < 2 || w->bits > 5) return hipErrorInvalidValue;
@@ -917,6 +918,7 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
         if (combine_weights && combine_out && d.exl3_slots <= 16) {
             // the down epilogue and the layer's slot-ordered combine in one launch (the decode path's finish)
             if (combined) *combined = true;
+            if (shared_ready && (e = hipStreamWaitEvent(s, shared_ready, 0)) != hipSuccess) return e;
             return launch_down_finish(s, fx->zd, picks, w->svh_d, fx->out, rows, P, d.hidden, skd, d.slots,
                                       d.exl3_slots, combine_weights, combine_shared, shared_stride, combine_out);
         }

@@ -175,7 +175,7 @@ int experts_run(gfr_experts* ex, hipStream_t stream, const gfr_exl3_experts* w, 
                 int input_stride, const int32_t* picks, const int32_t* ids, const int32_t* count,
                 const int32_t* members, int rows, int maxm, const float* weights, float* out,
                 const gfr::RouteOne* route = nullptr, const float* shared = nullptr, int shared_stride = 0,
-                int launches = 0) {
+                int launches = 0, hipEvent_t shared_ready = nullptr) {
     const int P = rows * ex->slots, D = ex->hidden, N = ex->inter;
     const int maxu = P < w->experts ? P : w->experts;
     hipError_t e;
@@ -192,6 +192,9 @@ int experts_run(gfr_experts* ex, hipStream_t stream, const gfr_exl3_experts* w, 
                                      maxu)) != hipSuccess)
         return hip_fail(e, "down gemv");
     if (launches == 2) return 0;
+    // the shared branch joins here: only the finish (down epilogue + combine) reads its output
+    if (shared_ready && (e = hipStreamWaitEvent(stream, shared_ready, 0)) != hipSuccess)
+        return hip_fail(e, "wait for the shared expert");
     if ((e = gfr::launch_sum_finish(stream, ex->zd, ex->y, rows, P, D, gfr::gemv_down_splits(N), ex->slots,
                                     ex->exl3_slots, weights, shared, shared_stride, out)) != hipSuccess)
         return hip_fail(e, "down epilogue");
@@ -461,7 +464,7 @@ int gfr_moe_set_decode_rows(gfr_moe* m, int decode_rows) {
 
 namespace {
 int moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input, const float* logits,
-            const float* shared, int shared_stride, int rows) {
+            const float* shared, int shared_stride, int rows, hipEvent_t shared_ready = nullptr) {
     if (!m) return fail(GFR_EINVAL, "null moe");
     int rc = check_weights(w, m->hidden, m->inter);
     if (rc) return rc;
@@ -473,6 +476,7 @@ int moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uin
     if (shared && m->shared_exl3) return fail(GFR_EINVAL, "the layer's shared expert is EXL3: no shared output");
     if (shared && shared_stride < m->hidden) return fail(GFR_EINVAL, "shared stride %d < hidden %d", shared_stride,
                                                          m->hidden);
+    if (shared_ready && !shared) return fail(GFR_EINVAL, "a shared-ready event without a shared output");
     hipError_t e;
     if (rows <= m->decode_rows) {
         gfr_grouping* g = m->group_dec;
@@ -481,15 +485,16 @@ int moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uin
             const gfr::RouteOne r{logits, m->route_bias, m->route_scale, m->routed, m->picks, m->weights, g->ids,
                                   g->count, g->members};
             return experts_run(m->dec, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members, 1,
-                               g->max_rows, m->weights, m->out, &r, shared, shared_stride, m->launches);
+                               g->max_rows, m->weights, m->out, &r, shared, shared_stride, m->launches,
+                               shared_ready);
         }
         // four launches: route + group, gate/up (+ rotation), down (+ gate/up epilogue), down epilogue (+ combine)
         if ((e = gfr::launch_route_group(stream, logits, rows, m->routed, m->topk, m->picks, m->weights, g->ids,
-                                         g->count, g->members, g->max_rows, 0, nullptr, nullptr, nullptr,
+                                         g->count, g->members, g->max_rows, 0, nullptr, nullptr, nullptr, 0,
                                          m->route_bias, m->route_scale)) != hipSuccess)
             return hip_fail(e, "route + group");
         return experts_run(m->dec, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members, rows,
-                           g->max_rows, m->weights, m->out, nullptr, shared, shared_stride);
+                           g->max_rows, m->weights, m->out, nullptr, shared, shared_stride, 0, shared_ready);
     }
     gfr_grouping* g = m->group_pre;
     bool planned = false;
@@ -501,8 +506,8 @@ int moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uin
         gfr::prefill_plan_buffers(m->pre, &pu, &pi, &pp);
         if ((e = gfr::launch_route_group(stream, logits, rows, m->routed, m->topk, m->picks, m->weights, g->ids,
                                          g->count, g->members, g->max_rows,
-                                         gfr::prefill_item_rows(m->pre, rows, w->bits), pu, pi, pp, m->route_bias,
-                                         m->route_scale)) != hipSuccess)
+                                         gfr::prefill_item_rows(m->pre, rows, w->bits), pu, pi, pp, w->experts,
+                                         m->route_bias, m->route_scale)) != hipSuccess)
             return hip_fail(e, "route + group");
         planned = true;
     } else {
@@ -517,7 +522,8 @@ int moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uin
             gfr::prefill_plan_buffers(m->pre, &pu, &pi, &pp);
             if ((e = gfr::launch_group_large(stream, m->picks, rows, g->slots, g->experts, g->bits, g->first, g->prefix,
                                              g->counts, g->ids, g->count, g->members, g->max_rows,
-                                             gfr::prefill_item_rows(m->pre, rows, w->bits), pu, pi, pp)) !=
+                                             gfr::prefill_item_rows(m->pre, rows, w->bits), pu, pi, pp,
+                                             w->experts)) !=
                 hipSuccess)
                 return hip_fail(e, "grouping launch");
             planned = true;
@@ -526,9 +532,11 @@ int moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uin
     // windows on the split-K programs fold the combine into their down epilogue
     bool combined = false;
     if ((e = gfr::prefill_run(m->pre, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members, rows,
-                              g->max_rows, false, m->weights, m->out, &combined, planned, shared, shared_stride)) !=
-        hipSuccess)
+                              g->max_rows, false, m->weights, m->out, &combined, planned, shared, shared_stride,
+                              shared_ready)) != hipSuccess)
         return hip_fail(e, "prefill run");
+    if (!combined && shared_ready && (e = hipStreamWaitEvent(stream, shared_ready, 0)) != hipSuccess)
+        return hip_fail(e, "wait for the shared expert");
     if (!combined &&
         (e = gfr::launch_combine(stream, gfr::prefill_output(m->pre), m->weights, rows, m->slots,
                                  m->shared_exl3 ? m->slots : m->slots - 1, m->hidden, shared, shared_stride,
@@ -636,6 +644,13 @@ int gfr_moe_run_shared(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w
                        const float* logits, const float* shared, int shared_stride, int rows) {
     if (!shared) return fail(GFR_EINVAL, "null shared output");
     return moe_run(m, stream, w, input, logits, shared, shared_stride, rows);
+}
+
+int gfr_moe_run_shared_branch(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
+                              const float* logits, const float* shared, int shared_stride, int rows,
+                              hipEvent_t shared_ready) {
+    if (!shared || !shared_ready) return fail(GFR_EINVAL, "null shared output or event");
+    return moe_run(m, stream, w, input, logits, shared, shared_stride, rows, shared_ready);
 }
 
 int gfr_moe_run_router(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,

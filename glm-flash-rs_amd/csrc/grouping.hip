@@ -47,7 +47,8 @@ __device__ __forceinline__ void group_small_body(const int* picks, int rows, int
                                                  int* __restrict__ count, int* __restrict__ members, int maxm,
                                                  uint32_t* lds, int* scan_scratch, int bm = 0,
                                                  int* __restrict__ plan_ucnt = nullptr,
-                                                 int* __restrict__ plan_items = nullptr, int* __restrict__ plan = nullptr) {
+                                                 int* __restrict__ plan_items = nullptr, int* __restrict__ plan = nullptr,
+                                                 int plan_E = 0) {
     const int NWD = (rows + 31) >> 5;
     uint32_t* bits = lds;                                    // [E][NWD]
     int* ucnt = reinterpret_cast<int*>(lds + (size_t)E * NWD);  // [E]: count of the u-th used expert
@@ -60,13 +61,18 @@ __device__ __forceinline__ void group_small_body(const int* picks, int rows, int
     }
     __syncthreads();
     // experts in rounds of blockDim.x: count, then the ascending order of the used ones
-    int base = 0;
+    int base = 0, base_w = 0;
     for (int e0 = 0; e0 < E; e0 += blockDim.x) {
         const int e = e0 + threadIdx.x;
         int c = 0;
         if (e < E)
             for (int w = 0; w < NWD; ++w) c += __popc(bits[e * NWD + w]);
         int total;
+        if (plan) {                                          // used experts the weights hold (ids below plan_E)
+            int tw;
+            block_scan(c > 0 && e < plan_E, scan_scratch, &tw);
+            base_w += tw;
+        }
         const int incl = block_scan(c > 0, scan_scratch, &total);
         if (e < E) {
             place[e] = c > 0 ? base + incl - 1 : -1;
@@ -84,7 +90,9 @@ __device__ __forceinline__ void group_small_body(const int* picks, int rows, int
         int ibase = 0;
         for (int u0 = 0; u0 < used; u0 += blockDim.x) {
             const int u = u0 + threadIdx.x;
-            const int c = u < used ? ucnt[u] : 0, np = (c + bm - 1) / bm;
+            // ids ascend, so the experts the weights hold are the first base_w; the others (a shared expert that is
+            // not EXL3) get no items, as in prefill_plan_kernel
+            const int c = u < used ? ucnt[u] : 0, np = u < base_w ? (c + bm - 1) / bm : 0;
             int total;
             const int first = ibase + block_scan(np, scan_scratch, &total) - np;
             if (u < used) {
@@ -135,7 +143,7 @@ __global__ void __launch_bounds__(1024) route_group_kernel(const float* __restri
                                                            int* __restrict__ count, int* __restrict__ members,
                                                            int maxm, int bm, int* __restrict__ plan_ucnt,
                                                            int* __restrict__ plan_items, int* __restrict__ plan,
-                                                           RouteGate gate) {
+                                                           int plan_E, RouteGate gate) {
     extern __shared__ uint32_t lds[];
     __shared__ int scan_scratch[16];
     const int slots = topk + 1, E = routed + 1;
@@ -150,7 +158,7 @@ __global__ void __launch_bounds__(1024) route_group_kernel(const float* __restri
         weights[i] = wt[i];
     }
     group_small_body(pk, rows, slots, E, ids, count, members, maxm, rest, scan_scratch, bm, plan_ucnt, plan_items,
-                     plan);
+                     plan, plan_E);
 }
 
 // Large windows, launch 1: the 256 rows of this workgroup marked in an LDS bitmap [E][8], stored to
@@ -208,13 +216,14 @@ __global__ void __launch_bounds__(256) group_scatter_kernel(const int* __restric
                                                             const int* __restrict__ counts, int* __restrict__ ids,
                                                             int* __restrict__ count, int* __restrict__ members,
                                                             int maxm, int bm, int* __restrict__ plan_ucnt,
-                                                            int* __restrict__ plan_items, int* __restrict__ plan) {
+                                                            int* __restrict__ plan_items, int* __restrict__ plan,
+                                                            int plan_E) {
     __shared__ int scan_scratch[16];
     __shared__ int tot_sh[4];
     const int e = blockIdx.x, NWD = (rows + 31) >> 5;
     int below = 0, used = 0, ibelow = 0, itotal = 0;
     for (int q = threadIdx.x; q < E; q += blockDim.x) {
-        const int c = counts[q], np = plan ? (c + bm - 1) / bm : 0;
+        const int c = counts[q], np = plan && q < plan_E ? (c + bm - 1) / bm : 0;
         used += c > 0;
         below += (q < e) & (c > 0);
         itotal += np;
@@ -241,7 +250,8 @@ __global__ void __launch_bounds__(256) group_scatter_kernel(const int* __restric
         const int u = below;
         if (threadIdx.x == 0) ids[u] = e;
         if (plan) {
-            const int np = (ce + bm - 1) / bm, first = tot_sh[2];
+            // experts at or above plan_E (a shared expert that is not EXL3) get no items
+            const int np = e < plan_E ? (ce + bm - 1) / bm : 0, first = tot_sh[2];
             if (threadIdx.x == 0) plan_ucnt[u] = ce;
             for (int k = threadIdx.x; k < np; k += blockDim.x) plan_items[first + k] = (u << 16) | k;
         }
@@ -302,18 +312,18 @@ size_t route_group_lds(int rows, int slots, int E) {
 
 hipError_t launch_route_group(hipStream_t s, const float* logits, int rows, int routed, int topk, int* picks,
                               float* weights, int* ids, int* count, int* members, int maxm, int bm, int* plan_ucnt,
-                              int* plan_items, int* plan, const float* bias, float scale) {
+                              int* plan_items, int* plan, int plan_E, const float* bias, float scale) {
     const int E = routed + 1, slots = topk + 1;
     const size_t lds = route_group_lds(rows, slots, E);
     if (lds > GROUP_LDS_MAX) return hipErrorInvalidValue;
     route_group_kernel<<<1, 1024, lds, s>>>(logits, rows, routed, topk, picks, weights, ids, count, members, maxm,
-                                            bm, plan_ucnt, plan_items, plan, RouteGate{bias, scale});
+                                            bm, plan_ucnt, plan_items, plan, plan_E, RouteGate{bias, scale});
     return hipGetLastError();
 }
 
 hipError_t launch_group_large(hipStream_t s, const int* picks, int rows, int slots, int E, uint32_t* bits,
-                              uint8_t* first, int* prefix, int* counts, int* ids, int* count, int* members, int maxm, int bm,
-                              int* plan_ucnt, int* plan_items, int* plan) {
+                              uint8_t* first, int* prefix, int* counts, int* ids, int* count, int* members, int maxm,
+                              int bm, int* plan_ucnt, int* plan_items, int* plan, int plan_E) {
     if ((size_t)E * 8 * 4 > GROUP_LDS_MAX) return hipErrorInvalidValue;
     group_mark_kernel<<<(rows + 255) / 256, 256, (size_t)E * 8 * 4, s>>>(picks, rows, slots, E, bits, first);
     hipError_t err = hipGetLastError();
@@ -321,7 +331,7 @@ hipError_t launch_group_large(hipStream_t s, const int* picks, int rows, int slo
     group_prefix_kernel<<<E, 256, 0, s>>>(bits, rows, prefix, counts);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     group_scatter_kernel<<<E, 256, 0, s>>>(picks, rows, slots, E, bits, first, prefix, counts, ids, count, members, maxm,
-                                            bm, plan_ucnt, plan_items, plan);
+                                            bm, plan_ucnt, plan_items, plan, plan_E);
     return hipGetLastError();
 }
 

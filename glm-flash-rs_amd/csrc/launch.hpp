@@ -13,15 +13,18 @@ size_t route_group_lds(int rows, int slots, int E);   // LDS of launch_route_gro
 hipError_t launch_group_small(hipStream_t s, const int* picks, int rows, int slots, int E, int* ids, int* count,
                               int* members, int maxm);
 // route (route.hpp) + group_small in one launch; rows <= GROUP_SMALL_ROWS, routed + 1 <= 1024
-// with plan != nullptr it also writes the prefill engine's item plan for bm-row items (prefill_plan_buffers)
+// with plan != nullptr it also writes the prefill engine's item plan for bm-row items (prefill_plan_buffers) over
+// the experts below plan_E (those the weights hold)
 hipError_t launch_route_group(hipStream_t s, const float* logits, int rows, int routed, int topk, int* picks,
                               float* weights, int* ids, int* count, int* members, int maxm, int bm = 0,
                               int* plan_ucnt = nullptr, int* plan_items = nullptr, int* plan = nullptr,
-                              const float* bias = nullptr, float scale = 1.f);
-// With plan (bm rows an item) the scatter launch also writes the prefill engine's item plan.
+                              int plan_E = 0, const float* bias = nullptr, float scale = 1.f);
+// With plan (bm rows an item) the scatter launch also writes the prefill engine's item plan over the experts below
+// plan_E (those the weights hold).
 hipError_t launch_group_large(hipStream_t s, const int* picks, int rows, int slots, int E, uint32_t* bits,
-                              uint8_t* first, int* prefix, int* counts, int* ids, int* count, int* members, int maxm, int bm = 0,
-                              int* plan_ucnt = nullptr, int* plan_items = nullptr, int* plan = nullptr);
+                              uint8_t* first, int* prefix, int* counts, int* ids, int* count, int* members, int maxm,
+                              int bm = 0, int* plan_ucnt = nullptr, int* plan_items = nullptr, int* plan = nullptr,
+                              int plan_E = 0);
 
 // exl3_decode.hip
 hipError_t launch_decode_tiles(hipStream_t s, const uint32_t* T, int kin, int n, int bits, uint16_t* out);

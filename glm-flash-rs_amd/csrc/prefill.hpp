@@ -18,7 +18,8 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
                        int input_stride, const int* picks, const int* ids, const int* count, const int* members,
                        int rows, int maxm, bool shared_x, const float* combine_weights = nullptr,
                        float* combine_out = nullptr, bool* combined = nullptr, bool planned = false,
-                       const float* combine_shared = nullptr, int shared_stride = 0);
+                       const float* combine_shared = nullptr, int shared_stride = 0,
+                       hipEvent_t shared_ready = nullptr);   // the stream waits on it before the combine
 // The item plan of a window of `rows` at `bits`: member rows an item, and the buffers prefill_run's GEMMs read
 // (ucnt, items, plan). A caller that fills them itself (the fused route + group launch) passes planned = true.
 int prefill_item_rows(const gfr_fast_experts* fx, int rows, int bits);

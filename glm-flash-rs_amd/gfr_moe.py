@@ -60,6 +60,7 @@ def _load() -> ctypes.CDLL:
         "gfr_moe_set_decode_rows": ([VP, I], I),
         "gfr_moe_create_shared": ([ctypes.POINTER(VP), I, I, I, I, I, I], I),
         "gfr_moe_run_shared": ([VP, P, P, P, P, P, I, I], I),
+        "gfr_moe_run_shared_branch": ([VP, P, P, P, P, P, I, I, P], I),
         "gfr_moe_run_router": ([VP, P, P, P, P, P, I, I], I),
         "gfr_router_logits": ([P, P, I, P, I, I, I, P], I),
         "gfr_moe_set_launches": ([VP, I], I),
@@ -312,10 +313,18 @@ class Moe(_Engine):
         _check(lib().gfr_moe_set_router(self._h, _ptr(bias), float(scale) if bias is not None else 1.0))
 
     def run(self, w: Exl3Experts, input: torch.Tensor, logits: torch.Tensor, rows: int, stream=None,
-            shared: torch.Tensor = None):
-        """shared: the non-EXL3 shared expert's output [rows, >= hidden] fp32 (a layer made with shared_exl3=False)."""
+            shared: torch.Tensor = None, shared_ready: "torch.cuda.Event" = None):
+        """shared: the non-EXL3 shared expert's output [rows, >= hidden] fp32 (a layer made with shared_exl3=False).
+        shared_ready: an event recorded (on another stream) once `shared` is written; only the combine waits for it
+        (gfr_moe_run_shared_branch; SharedBranch drives the fork and the join)."""
         ws = w.struct()
-        if shared is None:
+        if shared_ready is not None:
+            if shared is None:
+                raise ValueError("shared_ready without a shared output")
+            _check(lib().gfr_moe_run_shared_branch(self._h, _stream(stream), ctypes.byref(ws), _ptr(input),
+                                                   _ptr(logits), _ptr(shared), shared.stride(0), rows,
+                                                   ctypes.c_void_p(shared_ready.cuda_event)))
+        elif shared is None:
             _check(lib().gfr_moe_run(self._h, _stream(stream), ctypes.byref(ws), _ptr(input), _ptr(logits), rows))
         else:
             _check(lib().gfr_moe_run_shared(self._h, _stream(stream), ctypes.byref(ws), _ptr(input), _ptr(logits),
@@ -327,6 +336,32 @@ class Moe(_Engine):
         ws = w.struct()
         _check(lib().gfr_moe_run_router(self._h, _stream(stream), ctypes.byref(ws), _ptr(input), _ptr(router_weight),
                                         _ptr(shared), shared.stride(0) if shared is not None else 0, rows))
+
+
+class SharedBranch:
+    """The shared / routed expert fork of the reference's shared_expert.rs Branch (:18-78): the shared expert's
+    kernels run on this branch's own stream (default priority), the routed experts on the caller's, and the two join
+    before the combine. run(main, shared_fn, routed_fn): shared_fn(stream) launches the shared expert on the branch
+    stream; routed_fn(ready) launches the routed layer on `main` with ready as its shared-ready event (Moe.run(...,
+    shared=..., shared_ready=ready)). The main stream is joined to the branch even when routed_fn raises, so the
+    caller's buffers are safe to reuse after main's later work. Works under stream capture (a fork and a join of
+    events)."""
+
+    def __init__(self, device="cuda"):
+        self.stream = torch.cuda.Stream(device)
+        self.fork = torch.cuda.Event()
+        self.joined = torch.cuda.Event()
+
+    def run(self, main, shared_fn, routed_fn):
+        self.fork.record(main)
+        self.stream.wait_event(self.fork)
+        with torch.cuda.stream(self.stream):
+            shared_fn(self.stream)
+        self.joined.record(self.stream)
+        try:
+            routed_fn(self.joined)
+        finally:
+            main.wait_event(self.joined)
 
 
 class Linear(_Engine):

@@ -121,6 +121,12 @@ int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const
 /* shared [rows][shared_stride] fp32: the shared expert's output (a layer made with shared_exl3 = 0 only) */
 int gfr_moe_run_shared(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
                        const float* logits, const float* shared, int shared_stride, int rows);
+/* The routed branch of shared_expert.rs Branch::run (:60-78): the caller forks its own shared expert onto another
+ * stream and records shared_ready there once `shared` is written; the routed experts run on `stream` and only the
+ * combine (the last launch) waits for the event, so the two branches overlap. Same result as gfr_moe_run_shared. */
+int gfr_moe_run_shared_branch(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
+                              const float* logits, const float* shared, int shared_stride, int rows,
+                              hipEvent_t shared_ready);
 /* The whole layer from the hidden rows: router logits (gfr_router_logits, the reference's router_part + router_sum,
  * moe.rs:77-87) into the layer's own buffer, then gfr_moe_run_shared (shared may be NULL: no shared term, or an
  * EXL3 shared expert). router_weight [routed][hidden] bf16. */

@@ -132,3 +132,60 @@ def test_moe_reference_layout_shared_output(gfr, oracle, weights, rows):
         if choice[topk - 1] - choice[topk] > 1e-5:      # no near-tie at the k-th place: the picks are the oracle's
             assert list(gp[r]) == list(p[r]), r
             np.testing.assert_allclose(gw[r], wt[r], rtol=2e-6)
+
+
+@pytest.mark.parametrize("rows", [1, 3, 40, 300])
+def test_shared_branch_overlap(gfr, weights, rows):
+    """shared_expert.rs Branch::run (:60-78) through SharedBranch and gfr_moe_run_shared_branch: the shared expert's
+    output is produced on the branch stream behind a long matmul (the buffer holds NaN until then), the routed layer
+    runs on the main stream and only its combine waits for the branch. The output is byte-equal to the serial
+    gfr_moe_run_shared, eagerly and in every replay of a captured graph (fork and join inside the capture)."""
+    topk = 8
+    g = torch.Generator(device="cuda").manual_seed(7 + rows)
+    x = torch.randn((rows, D), generator=g, device="cuda").to(torch.bfloat16)
+    logits = torch.randn((rows, E), generator=g, device="cuda")
+    src = torch.randn((rows, D), generator=g, device="cuda")
+    a = torch.randn((2048, 2048), generator=g, device="cuda")
+    shared = torch.empty((rows, D), device="cuda")
+    m = gfr.Moe(D, N, E, topk, max(rows, 4), shared_exl3=False)
+    m.run(weights, x, logits, rows, shared=src)
+    torch.cuda.synchronize()
+    want = m.output[:rows].clone()
+    branch = gfr.SharedBranch()
+    main = torch.cuda.Stream()
+
+    def layer():
+        shared.fill_(float("nan"))
+
+        def shared_fn(side):
+            t = a
+            for _ in range(4):
+                t = t @ a * (1.0 / 64.0)
+            shared.copy_(src + 0.0 * t[0, 0])
+
+        branch.run(main, shared_fn, lambda ready: m.run(weights, x, logits, rows, stream=main, shared=shared,
+                                                         shared_ready=ready))
+
+    with torch.cuda.stream(main):
+        m.output.zero_()
+        layer()
+    torch.cuda.synchronize()
+    assert torch.equal(m.output[:rows], want)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(main):
+        with torch.cuda.graph(graph, stream=main):
+            layer()
+    for _ in range(3):
+        m.output.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(main):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(m.output[:rows], want)
+
+
+def test_shared_branch_rejects_event_without_output(gfr, weights):
+    m = gfr.Moe(D, N, E, 8, 4, shared_exl3=False)
+    with pytest.raises(ValueError):
+        m.run(weights, torch.zeros((1, D), dtype=torch.bfloat16, device="cuda"), torch.zeros((1, E), device="cuda"),
+              1, shared_ready=torch.cuda.Event())
