@@ -567,7 +567,9 @@ __device__ __forceinline__ void combine_shared(const float* __restrict__ w, int 
 
 // Finish of the decode path: y[p] = the k-block parts of the down epilogue (Zd, already transformed and scaled) added
 // in order; with weights, out[row] = the token's slots in order, weighted. Program (token row, 128-column block), one
-// wave a slot (up to 16 at a time).
+// wave a slot (up to 16 at a time). Each wave loads its slot's weight (and wave 0 the first shared slot's weight and
+// output) together with the parts, so the combine adds no dependent round trip; each wave forms its weighted term
+// and wave 0 adds the terms in slot order.
 __global__ void __launch_bounds__(1024) sum_finish_kernel(const float* __restrict__ Z, float* __restrict__ y, int P,
                                                            int D, int SK, int slots, int exl3_slots,
                                                            const float* __restrict__ weights,
@@ -579,11 +581,20 @@ __global__ void __launch_bounds__(1024) sum_finish_kernel(const float* __restric
     const int n = blk * 128 + 2 * lane;
     const size_t tslot = ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 16 + wave;
     GEMV_MARK(2, tslot, 0);
+    // the first shared slot's weight and output, loaded up front (wave 0 adds them last)
+    const bool sh = weights && shared && exl3_slots < slots && wave == 0;
+    float sw = 0.f;
+    float2 sv = make_float2(0.f, 0.f);
+    if (sh) {
+        sw = weights[row * slots + exl3_slots];
+        sv = *reinterpret_cast<const float2*>(shared + (size_t)row * shared_stride + n);
+    }
     float o0 = 0.f, o1 = 0.f;
     for (int s0 = 0; s0 < exl3_slots; s0 += nwv) {
         const int s = s0 + wave;
         if (s < exl3_slots) {
             const int p = row * slots + s;
+            const float w = weights ? weights[p] : 0.f;
             float2 zs[16];
             float v0 = 0.f, v1 = 0.f;
             for (int k0 = 0; k0 < SK; k0 += 16) {           // parts in k order, sixteen in flight
@@ -597,23 +608,26 @@ __global__ void __launch_bounds__(1024) sum_finish_kernel(const float* __restric
                         v1 += zs[k].y;
                     }
             }
-            const float2 yv = make_float2(v0, v1);
-            *reinterpret_cast<float2*>(y + (size_t)p * D + n) = yv;
-            ys[wave][lane] = yv;
+            *reinterpret_cast<float2*>(y + (size_t)p * D + n) = make_float2(v0, v1);
+            ys[wave][lane] = make_float2(w * v0, w * v1);
         }
         if (weights) {
             __syncthreads();
             if (wave == 0)
                 for (int q = 0; q < nwv && s0 + q < exl3_slots; ++q) {
-                    const float w = weights[row * slots + s0 + q];
-                    o0 += w * ys[q][lane].x;
-                    o1 += w * ys[q][lane].y;
+                    o0 += ys[q][lane].x;
+                    o1 += ys[q][lane].y;
                 }
             __syncthreads();
         }
     }
     if (weights && wave == 0) {
-        combine_shared(weights + (size_t)row * slots, slots, exl3_slots, shared, shared_stride, row, n, o0, o1);
+        if (sh) {
+            o0 += sw * sv.x;
+            o1 += sw * sv.y;
+            combine_shared(weights + (size_t)row * slots, slots, exl3_slots + 1, shared, shared_stride, row, n, o0,
+                           o1);
+        }
         *reinterpret_cast<float2*>(out + (size_t)row * D + n) = make_float2(o0, o1);
     }
     GEMV_MARK(2, tslot, 5);
@@ -634,18 +648,36 @@ __global__ void __launch_bounds__(1024) down_finish_kernel(const float* __restri
     const size_t tslot = ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 16 + wave;
     GEMV_MARK(2, tslot, 0);
     const int n = blk * 128 + 2 * lane;
+    // the first shared slot's weight and output, loaded up front (wave 0 adds them last)
+    const bool sh = weights && shared && exl3_slots < slots && wave == 0;
+    float sw = 0.f;
+    float2 shv = make_float2(0.f, 0.f);
+    if (sh) {
+        sw = weights[row * slots + exl3_slots];
+        shv = *reinterpret_cast<const float2*>(shared + (size_t)row * shared_stride + n);
+    }
     float o0 = 0.f, o1 = 0.f;
     for (int s0 = 0; s0 < exl3_slots; s0 += nwv) {
         const int s = s0 + wave;
         if (s < exl3_slots) {
             const int p = row * slots + s;
             const int e = pick[p];
+            const float w = weights ? weights[p] : 0.f;
+            // the first partials and the expert's scales in flight together (the scale load waits only for e; the
+            // loads are unconditional, a split past SK re-reads the last one, so that the wait counts stay exact)
             float2 zs[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                zs[k] = *reinterpret_cast<const float2*>(Z + ((size_t)(k < SK ? k : SK - 1) * P + p) * D + n);
+            const uint32_t sv = *reinterpret_cast<const uint32_t*>(svh_d + (size_t)e * D + n);
             float v[2] = {0.f, 0.f};
             for (int k0 = 0; k0 < SK; k0 += 8) {            // partials in split order, eight in flight
+                if (k0 > 0) {
 #pragma unroll
-                for (int k = 0; k < 8; ++k)
-                    if (k0 + k < SK) zs[k] = *reinterpret_cast<const float2*>(Z + ((size_t)(k0 + k) * P + p) * D + n);
+                    for (int k = 0; k < 8; ++k)
+                        if (k0 + k < SK)
+                            zs[k] = *reinterpret_cast<const float2*>(Z + ((size_t)(k0 + k) * P + p) * D + n);
+                }
 #pragma unroll
                 for (int k = 0; k < 8; ++k)
                     if (k0 + k < SK) {
@@ -653,27 +685,30 @@ __global__ void __launch_bounds__(1024) down_finish_kernel(const float* __restri
                         v[1] += zs[k].y;
                     }
             }
-            const uint32_t sv = *reinterpret_cast<const uint32_t*>(svh_d + (size_t)e * D + n);
             fwht128_w64(v, lane);
             float2 yv;
             yv.x = v[0] * HAD_SCALE * f16_to_f32((uint16_t)sv);
             yv.y = v[1] * HAD_SCALE * f16_to_f32((uint16_t)(sv >> 16));
             *reinterpret_cast<float2*>(y + (size_t)p * D + n) = yv;
-            ys[wave][lane] = yv;
+            ys[wave][lane] = make_float2(w * yv.x, w * yv.y);
         }
         if (weights) {
             __syncthreads();
             if (wave == 0)
                 for (int q = 0; q < nwv && s0 + q < exl3_slots; ++q) {
-                    const float w = weights[row * slots + s0 + q];
-                    o0 += w * ys[q][lane].x;
-                    o1 += w * ys[q][lane].y;
+                    o0 += ys[q][lane].x;
+                    o1 += ys[q][lane].y;
                 }
             __syncthreads();
         }
     }
     if (weights && wave == 0) {
-        combine_shared(weights + (size_t)row * slots, slots, exl3_slots, shared, shared_stride, row, n, o0, o1);
+        if (sh) {
+            o0 += sw * shv.x;
+            o1 += sw * shv.y;
+            combine_shared(weights + (size_t)row * slots, slots, exl3_slots + 1, shared, shared_stride, row, n, o0,
+                           o1);
+        }
         *reinterpret_cast<float2*>(out + (size_t)row * D + n) = make_float2(o0, o1);
     }
     GEMV_MARK(2, tslot, 5);
