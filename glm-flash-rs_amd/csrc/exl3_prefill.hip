@@ -251,6 +251,67 @@ __global__ void __launch_bounds__(256) prefill_rot_kernel(const uint16_t* __rest
     }
 }
 
+// The same rotation with two 128-blocks of a token a wave and no idle rows: lanes of rows 0, 1 (lane bits 2 and 5,
+// see l8_row) take block 2 b and rows 2, 3 block 2 b + 1, and a lane keeps its matrix (MATS = 2: row & 1) in every
+// round, so the (slot, matrix) rows of a block fill the rounds exactly: round r is slot r (MATS = 2) or slots 2 r and
+// 2 r + 1 (MATS = 1). x * suh is exact in fp32 (bf16 times fp16), so it is one v_fma_mix_f32 from the fp16 scale;
+// the rest is rot_in's arithmetic as above, bit for bit. K / 128 even.
+template <int MATS>
+__global__ void __launch_bounds__(256) prefill_rot2_kernel(const uint16_t* __restrict__ x, int x_stride,
+                                                           const int* __restrict__ pick,
+                                                           const uint16_t* __restrict__ suh0,
+                                                           const uint16_t* __restrict__ suh1,
+                                                           uint16_t* __restrict__ out0, uint16_t* __restrict__ out1,
+                                                           int K, int rows, int slots, int exl3_slots) {
+    const int lane = threadIdx.x & 63;
+    const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int KP = K / 256, row = task / KP, bp = task % KP;
+    if (row >= rows) return;
+    const int j8 = l8_j(lane), r4 = l8_row(lane);
+    const int blk = 2 * bp + (r4 >> 1), k = blk * 128 + 8 * j8;
+    const int m = MATS == 2 ? (r4 & 1) : 0;
+    const uint16_t* suh = m ? suh1 : suh0;
+    uint16_t* outm = (m ? out1 : out0) + (size_t)blk * 128;
+    const uint4 xv = *reinterpret_cast<const uint4*>(x + (size_t)row * x_stride + k);
+    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+    float xf[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        xf[2 * i] = bf16_to_f32((uint16_t)xw[i]);
+        xf[2 * i + 1] = bf16_to_f32((uint16_t)(xw[i] >> 16));
+    }
+    const int nrd = MATS == 2 ? exl3_slots : (exl3_slots + 1) / 2;
+    const int pk = lane < exl3_slots ? pick[row * slots + lane] : 0;
+    const float st = lane_sign(lane) * HAD_SCALE;
+    constexpr int RC = 8;                                   // rounds a chunk: their scales in flight together
+    for (int r0 = 0; r0 < nrd; r0 += RC) {
+        uint4 sv[RC];
+#pragma unroll
+        for (int q = 0; q < RC; ++q) {
+            const int rd = min(r0 + q, nrd - 1);
+            const int sl = MATS == 2 ? rd : min(2 * rd + (r4 & 1), exl3_slots - 1);
+            const int e = __shfl(pk, sl, 64);
+            sv[q] = *reinterpret_cast<const uint4*>(suh + (size_t)e * K + k);
+        }
+#pragma unroll
+        for (int q = 0; q < RC; ++q) {
+            const int rd = r0 + q;
+            if (rd >= nrd) break;
+            const int sl = MATS == 2 ? rd : 2 * rd + (r4 & 1);
+            const uint32_t sw[4] = {sv[q].x, sv[q].y, sv[q].z, sv[q].w};
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                __asm__("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "=v"(v[2 * i]) : "v"(xf[2 * i]), "v"(sw[i]));
+                __asm__("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+                        : "=v"(v[2 * i + 1]) : "v"(xf[2 * i + 1]), "v"(sw[i]));
+            }
+            fwht128_l8(v, lane);
+            if (MATS == 2 || sl < exl3_slots) store_pairs_l8(outm + (size_t)(row * slots + sl) * K, v, lane, st);
+        }
+    }
+}
+
 // ---- GEMM --------------------------------------------------------------------------------------------------------
 struct PrefillArgs {
     const uint16_t* x0;      // rows [P][Kin] fp16 in pair order, matrix 0 (gate, or the down input xd)
@@ -870,7 +931,16 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
         return hipErrorInvalidValue;
     hipError_t e;
     // rotated rows of every EXL3 pair (one copy when the two input rotations are the same)
-    {
+    if ((d.hidden / 128) % 2 == 0) {
+        const int tasks = rows * (d.hidden / 256), grid = (tasks + 3) / 4;
+        if (!shared_x)
+            prefill_rot2_kernel<2><<<grid, 256, 0, s>>>(input, input_stride, picks, w->suh_g, w->suh_u, fx->xg, fx->xu,
+                                                        d.hidden, rows, d.slots, d.exl3_slots);
+        else
+            prefill_rot2_kernel<1><<<grid, 256, 0, s>>>(input, input_stride, picks, w->suh_g, w->suh_u, fx->xg, fx->xu,
+                                                        d.hidden, rows, d.slots, d.exl3_slots);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    } else {
         const int tasks = rows * (d.hidden / 128);
         const int mats = shared_x ? 1 : 2;
         if (d.exl3_slots * mats <= 16)   // fewer scale registers: more resident waves
