@@ -41,6 +41,16 @@ constexpr int PF_BM = PF_BM_ROWS;   // member rows an item (256: one workgroup a
 #endif
 constexpr int PF_BM4 = PF_BM4_ROWS;  // member rows an item for K = 4 (fits two workgroups a CU in LDS)
 static_assert(PF_BM4 >= PF_BM, "allocation bound");
+#ifndef PF_BM3_ROWS
+#define PF_BM3_ROWS 160
+#endif
+#ifndef PF_BM5_ROWS
+#define PF_BM5_ROWS 144
+#endif
+constexpr int PF_BM3 = PF_BM3_ROWS;  // K = 3: the direct fragment decode, 160 rows (252 VGPRs, no spills)
+constexpr int PF_BM5 = PF_BM5_ROWS;  // K = 5: 144 rows (256 VGPRs, no spills)
+// member rows a full-K item at each width (K = 2 keeps the fragment exchange through LDS and 128 rows)
+constexpr int pf_bm_for(int bits) { return bits == 4 ? PF_BM4 : bits == 3 ? PF_BM3 : bits == 5 ? PF_BM5 : PF_BM; }
 constexpr int PF_MAXU = 1024;       // distinct experts a window (grid / plan bound)
 
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
@@ -377,6 +387,65 @@ __device__ __forceinline__ h8_t a_fragment4(const uint32_t* tw, int lane) {
     return f;
 }
 
+// The same fragment for K = 3 and 5, whose pairs follow the same order (pair_row, K != 2). The lane's two value
+// groups (l = 2g and 2g + 1) are each 4 consecutive values 8 l + 4 half .. + 3 of format lane i; their windows end
+// at bits (v + 1) K of the lane's stream and span 3 K + 16 <= 31 bits, so one funnel shift of two adjacent words
+// (alignbit by a per-lane amount, the same for every tile) holds all four: value v0 + d at bits (3 - d) K.
+// fragk_words: the 2 x 2 words of the lane's groups (the word before the group's last bit wraps within the k tile,
+// as lane 0's previous word is lane 7's last); fragk_shifts: the two funnel shifts.
+template <int K>
+__device__ __forceinline__ void fragk_groups(int lane, int t, int& lo, int& sh) {
+    const int c = lane & 15, half = c >> 3, g = (lane >> 4) & 1, i = c & 7;
+    const int v0 = 8 * (2 * g + t) + 4 * half, e = (v0 + 4) * K, hiw = (e - 1) >> 5;
+    lo = K * i + hiw;                                   // the word holding the group's last bit
+    sh = 32 * (hiw + 1) - e;
+}
+template <int K>
+__device__ __forceinline__ void fragk_shifts(int lane, uint32_t (&sh)[2]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        int lo, s;
+        fragk_groups<K>(lane, t, lo, s);
+        sh[t] = (uint32_t)s;
+    }
+}
+template <int K>
+__device__ __forceinline__ void fragk_words(const uint32_t* tw, int lane, uint32_t (&wd)[4]) {
+    const uint32_t* w = tw + (lane >> 5) * (8 * K);     // k tile q / 2
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        int lo, s;
+        fragk_groups<K>(lane, t, lo, s);
+        wd[2 * t] = w[(lo + 8 * K - 1) % (8 * K)];
+        wd[2 * t + 1] = w[lo];
+    }
+}
+// Its four packed state pairs, st[2 t + h] = (window of v0 + h + 2 low, window of v0 + h high).
+template <int K>
+__device__ __forceinline__ void fragk_states(const uint32_t (&wd)[4], const uint32_t (&sh)[2], uint32_t (&st)[4]) {
+    static_assert(3 * K + 16 <= 32, "four windows in one funnel word");
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const uint32_t W = __builtin_amdgcn_alignbit(wd[2 * t], wd[2 * t + 1], sh[t]);
+        st[2 * t] = ((W << (16 - 3 * K)) & 0xFFFF0000u) | ((W >> K) & 0xFFFFu);
+        st[2 * t + 1] = ((W << (16 - 2 * K)) & 0xFFFF0000u) | (W & 0xFFFFu);
+    }
+}
+template <int K>
+__device__ __forceinline__ h8_t a_fragmentk(const uint32_t* tw, int lane, const uint32_t (&sh)[2]) {
+    uint32_t wd[4], s[4];
+    fragk_words<K>(tw, lane, wd);
+    fragk_states<K>(wd, sh, s);
+    h8_t f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const h2_t v = decode_pair(s[j]);
+        f[2 * j] = v[0];
+        f[2 * j + 1] = v[1];
+    }
+    return f;
+}
+
 // 16-byte direct-to-LDS load: lane i's 16 bytes land at lds_base + 16 i (lds_base uniform). Written as inline asm:
 // the compiler treats its builtin as an LDS store of unknown address and puts s_waitcnt vmcnt(0) before every later
 // LDS read, which drains the whole load pipeline each step; here the kernels wait for their stages themselves
@@ -435,11 +504,11 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
     constexpr int XLOADS = (MATS * RB + 3) / 4;          // direct loads of rows a wave a step (the last repeated)
     constexpr int TL = (K + 3) / 4;                      // direct loads of trellis words a wave a step
     constexpr int LOADS = XLOADS + TL;
-    static_assert((BM == 256 || BM == 176 || BM == 160 || BM == 128 || BM == 32) && NS <= 8, "tile shape");
+    static_assert((BM == 256 || BM == 176 || BM == 160 || BM == 144 || BM == 128 || BM == 32) && NS <= 8, "tile shape");
     __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
     __shared__ int rows_sh[BM];
     // K != 4: each lane decodes one trellis lane's 32 values of one tile and the fragments are exchanged here
-    __shared__ __attribute__((aligned(16))) uint4 afrag[(K == 4 || BM == 256) ? 1 : 4][4][64];
+    __shared__ __attribute__((aligned(16))) uint4 afrag[(K != 2 || BM == 256) ? 1 : 4][4][64];
 
     const int ncg = a.N / NCOLS;
     // XCD-aware order: the hardware deals consecutive workgroups to the 8 XCDs in turn; renumber so that each XCD gets
@@ -548,11 +617,17 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
         const int row = 16 * b + (lane & 15);
         return *reinterpret_cast<const h8_t*>(xb + row * 64 + ((q ^ ((row >> 1) & 3)) << 4));
     };
+    // K = 3, 5: the direct fragment decode's two per-lane funnel shifts (the same for every tile and step)
+    uint32_t ksh[2] = {0u, 0u};
+    if constexpr (K == 3 || K == 5) fragk_shifts<K>(lane, ksh);
     auto decode_a = [&](int slot, h8_t (&af)[4]) {
         const uint32_t* tw = reinterpret_cast<const uint32_t*>(lds + slot * STAGE + MATS * XBUF);
         if constexpr (K == 4) {
 #pragma unroll
             for (int t4 = 0; t4 < 4; ++t4) af[t4] = a_fragment4(tw + (stile0 + t4) * 64, lane);
+        } else if constexpr (K == 3 || K == 5) {
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4) af[t4] = a_fragmentk<K>(tw + (stile0 + t4) * (16 * K), lane, ksh);
         } else {
             // lane (t4, kt, i) decodes trellis lane i of k tile kt of tile t4 (32 values: columns i and i + 8 of
             // 16 rows), then hands each of its four 8-value pieces (column half, word pair g) to the MFMA lane
@@ -619,13 +694,18 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
         if (s + NS - 1 < S) issue(s + NS - 1);           // into stage s - 1's buffer, now free
         const int sn = (slot + 1) % NS;                   // the next step's slot (the last step reads a stale one,
                                                           // unused)
-        if constexpr (K == 4) {
+        if constexpr (K != 2) {
             // the next step's decode spread over this step's MFMA groups (sched_barrier keeps each group together,
             // so the VALU of the decode issues while the matrix core works)
             const uint32_t* twn = reinterpret_cast<const uint32_t*>(lds + sn * STAGE + MATS * XBUF);
             uint32_t wp[4], w0[4], w1[4], st[4];
+            uint32_t wk[2][K == 4 ? 1 : 4];                // K = 3, 5: words of two tiles, one read ahead
+            if constexpr (K == 4) {
 #pragma unroll
-            for (int t4 = 0; t4 < 4; ++t4) frag4_words(twn + (stile0 + t4) * 64, lane, wp[t4], w0[t4], w1[t4]);
+                for (int t4 = 0; t4 < 4; ++t4) frag4_words(twn + (stile0 + t4) * 64, lane, wp[t4], w0[t4], w1[t4]);
+            } else {
+                fragk_words<K>(twn + stile0 * (16 * K), lane, wk[0]);
+            }
 #pragma unroll
             for (int b = 0; b < RB; ++b) {
                 const h8_t bc = ring[b % D];
@@ -638,7 +718,14 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
 #pragma unroll
                 for (int pr = b * 16 / RB; pr < (b + 1) * 16 / RB; ++pr) {   // the 16 decoded pairs spread evenly
                     const int t = pr >> 2, j = pr & 3;
-                    if (j == 0) frag4_states(wp[t], w0[t], w1[t], lane, st);
+                    if (j == 0) {
+                        if constexpr (K == 4) {
+                            frag4_states(wp[t], w0[t], w1[t], lane, st);
+                        } else {
+                            fragk_states<K>(wk[t & 1], ksh, st);
+                            if (t < 3) fragk_words<K>(twn + (stile0 + t + 1) * (16 * K), lane, wk[(t + 1) & 1]);
+                        }
+                    }
                     const h2_t v = decode_pair(st[j]);
                     an[t][2 * j] = v[0];
                     an[t][2 * j + 1] = v[1];
@@ -847,7 +934,8 @@ constexpr int PF_SPLIT_PAIRS = PF_SPLIT_PAIRS_MAX;
 constexpr int PF_SPLIT_K = 512;
 constexpr int PF_SPLIT_BM = 32;
 static bool split_ok(int hidden, int inter) { return hidden % PF_SPLIT_K == 0 && inter % PF_SPLIT_K == 0; }
-static_assert(PF_SPLIT_BM <= PF_BM && PF_SPLIT_BM <= PF_BM4, "items are bounded at the smallest item size");
+static_assert(PF_SPLIT_BM <= PF_BM && PF_SPLIT_BM <= PF_BM4 && PF_SPLIT_BM <= PF_BM3 && PF_SPLIT_BM <= PF_BM5,
+              "items are bounded at the smallest item size");
 // The most items a window of P pairs over at most maxu distinct experts can plan, at any item size the engine uses.
 static size_t item_bound(size_t P, size_t maxu) {
     const size_t b = P / PF_SPLIT_BM + maxu;
@@ -905,9 +993,9 @@ template <int MATS>
 static hipError_t launch_gemm(int bits, dim3 grid, hipStream_t s, const PrefillArgs& a) {
     switch (bits) {
         case 2: prefill_gemm_kernel<MATS, 2, PF_BM><<<grid, 256, 0, s>>>(a); break;
-        case 3: prefill_gemm_kernel<MATS, 3, PF_BM><<<grid, 256, 0, s>>>(a); break;
+        case 3: prefill_gemm_kernel<MATS, 3, PF_BM3><<<grid, 256, 0, s>>>(a); break;
         case 4: prefill_gemm_kernel<MATS, 4, PF_BM4><<<grid, 256, 0, s>>>(a); break;
-        case 5: prefill_gemm_kernel<MATS, 5, PF_BM><<<grid, 256, 0, s>>>(a); break;
+        case 5: prefill_gemm_kernel<MATS, 5, PF_BM5><<<grid, 256, 0, s>>>(a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -958,7 +1046,7 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     const bool split = fx->zgu && P <= PF_SPLIT_PAIRS;
-    const int bm = split ? PF_SPLIT_BM : w->bits == 4 ? PF_BM4 : PF_BM;
+    const int bm = split ? PF_SPLIT_BM : pf_bm_for(w->bits);
     if (!planned) {
         prefill_plan_kernel<<<1, 1024, 0, s>>>(ids, count, members, maxm, w->experts, maxu, bm, fx->ucnt, fx->items,
                                                fx->plan);
@@ -1007,7 +1095,7 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
 float* prefill_output(const gfr_fast_experts* fx) { return fx->out; }
 int prefill_item_rows(const gfr_fast_experts* fx, int rows, int bits) {
     const bool split = fx->zgu && rows * fx->d.slots <= PF_SPLIT_PAIRS;
-    return split ? PF_SPLIT_BM : bits == 4 ? PF_BM4 : PF_BM;
+    return split ? PF_SPLIT_BM : pf_bm_for(bits);
 }
 void prefill_plan_buffers(gfr_fast_experts* fx, int** ucnt, int** items, int** plan) {
     *ucnt = fx->ucnt;
