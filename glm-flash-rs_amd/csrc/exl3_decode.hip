@@ -200,7 +200,10 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
             xearly = *reinterpret_cast<const uint32_t*>(a.x0 + (kt0 & ~7) * 16 + 2 * lane);
         int pick;
         float weight;
-        route_token_regs(a.logits, a.routed, a.slots - 1, a.routed, pick, weight, RouteGate{a.route_bias, a.route_scale});
+        // only the wave that publishes the routing needs the weights (the others use the picks)
+        const bool writer = u == 0 && cb == 0 && blockIdx.z == 0 && wave == 0;
+        route_token_regs(a.logits, a.routed, a.slots - 1, a.routed, pick, weight, RouteGate{a.route_bias, a.route_scale},
+                         writer);
         int rank = 0;                                    // ascending order of the token's slots' experts
         for (int j = 0; j < a.slots; ++j) rank += __builtin_amdgcn_readlane(pick, j) < pick;
         const uint64_t mine = __ballot(lane < a.slots && rank == u);
@@ -208,7 +211,7 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
         const int slot = __builtin_ctzll(mine);
         e = __builtin_amdgcn_readlane(pick, slot);
         code = lane == 0 ? slot : -1;                    // row 0, this slot
-        if (u == 0 && cb == 0 && blockIdx.z == 0 && wave == 0 && lane < a.slots) {
+        if (writer && lane < a.slots) {
             a.pick_out[lane] = pick;
             a.weight_out[lane] = weight;
             a.ids_out[rank] = pick;

@@ -44,9 +44,11 @@ __device__ __forceinline__ void route_load(const float* __restrict__ l, int E, R
 // One wave (64 lanes) routes one token into registers: lane s < topk holds the s-th pick and its weight, lane topk
 // the shared expert (weight 1). k rounds of a wave-wide max (DPP / permlane, no LDS) whose winner is the lowest id
 // holding it (a ballot per register, lowest set lane).
+// need_weight == false (uniform over the wave): the picks only, weight left 0 (callers that only need the experts).
 template <int PER>
 __device__ __forceinline__ void route_pick(const RouteIn<PER>& in, const float* __restrict__ l, int E, int topk,
-                                           int shared_id, int& pick, float& weight, RouteGate g) {
+                                           int shared_id, int& pick, float& weight, RouteGate g,
+                                           bool need_weight = true) {
     const int lane = threadIdx.x & 63;
     float v[PER];
 #pragma unroll
@@ -78,6 +80,8 @@ __device__ __forceinline__ void route_pick(const RouteIn<PER>& in, const float* 
         }
     }
     pick = lane < topk ? my_e : shared_id;
+    weight = 0.f;
+    if (!need_weight) return;
     if (g.bias) {
         // the picked experts' unbiased scores, normalised over the picks in slot order, times the scale
         const float sc = lane < topk ? sigmoidf_(l[my_e]) : 0.f;
@@ -95,18 +99,19 @@ __device__ __forceinline__ void route_pick(const RouteIn<PER>& in, const float* 
 
 template <int PER>
 __device__ __forceinline__ void route_token_per(const float* __restrict__ l, int E, int topk, int shared_id,
-                                                int& pick, float& weight, RouteGate g) {
+                                                int& pick, float& weight, RouteGate g, bool need_weight) {
     RouteIn<PER> in;
     route_load<PER>(l, E, g, in);
-    route_pick<PER>(in, l, E, topk, shared_id, pick, weight, g);
+    route_pick<PER>(in, l, E, topk, shared_id, pick, weight, g, need_weight);
 }
 
 __device__ __forceinline__ void route_token_regs(const float* __restrict__ l, int E, int topk, int shared_id,
-                                                 int& pick, float& weight, RouteGate g = {nullptr, 1.f}) {
-    if (E <= 64) route_token_per<1>(l, E, topk, shared_id, pick, weight, g);
-    else if (E <= 128) route_token_per<2>(l, E, topk, shared_id, pick, weight, g);
-    else if (E <= 256) route_token_per<4>(l, E, topk, shared_id, pick, weight, g);
-    else route_token_per<ROUTE_MAX_E / 64>(l, E, topk, shared_id, pick, weight, g);
+                                                 int& pick, float& weight, RouteGate g = {nullptr, 1.f},
+                                                 bool need_weight = true) {
+    if (E <= 64) route_token_per<1>(l, E, topk, shared_id, pick, weight, g, need_weight);
+    else if (E <= 128) route_token_per<2>(l, E, topk, shared_id, pick, weight, g, need_weight);
+    else if (E <= 256) route_token_per<4>(l, E, topk, shared_id, pick, weight, g, need_weight);
+    else route_token_per<ROUTE_MAX_E / 64>(l, E, topk, shared_id, pick, weight, g, need_weight);
 }
 
 // One wave routes one token; pk / wt (LDS or global) receive topk + 1 entries.
