@@ -17,7 +17,8 @@
 //     K in steps of 32, multi-stage direct-to-LDS staging and a register pipeline (next step's decode during this
 //     step's MFMAs). BM = 176 for K = 4: the trellis decode (VALU) is amortised over more rows, an expert of 512
 //     members takes 3 passes instead of 4, and 244 VGPRs and two workgroups' stages (2 x 80.6 KB) still fit.
-//     BM = 128 for the other widths (their fragment exchange needs more LDS).
+//     K = 3 and 5 decode their fragments directly as well (160 and 144 rows, the most without spills); K = 2
+//     hands decoded pieces to their MFMA lanes through LDS (128 rows).
 //   * the 128 columns of a gate/up item, and each 128 of a down item, are one Hadamard block, so the epilogue
 //     (transforms, scales, SwiGLU) runs in the workgroup: accumulators -> LDS (32 rows at a time) -> registers with
 //     8 consecutive values a lane and four rows a wave, so that three of the seven butterfly stages stay in registers.
