@@ -137,6 +137,30 @@ __global__ void __launch_bounds__(1024) group_small_kernel(const int* __restrict
 
 // Decode windows in one launch: wave w routes tokens w, w + 16, ... (route.hpp) into LDS and global picks /
 // weights, then the workgroup groups them (group_small_body). rows <= GROUP_SMALL_ROWS.
+// The workgroup's waves route rows r = wave, wave + waves, ... into pk / wt (topk + 1 entries a row); a wave's next
+// row's logits are loaded before it routes the current one, so the loads of consecutive rows overlap.
+template <int PER>
+__device__ __forceinline__ void route_rows(const float* __restrict__ logits, int rows, int routed, int topk, int* pk,
+                                           float* wt, RouteGate gate) {
+    const int lane = threadIdx.x & 63, nw = blockDim.x >> 6, slots = topk + 1;
+    int r = threadIdx.x >> 6;
+    if (r >= rows) return;
+    RouteIn<PER> cur, nxt;
+    route_load<PER>(logits + (size_t)r * routed, routed, gate, cur);
+    for (; r < rows; r += nw) {
+        const int rn = r + nw < rows ? r + nw : r;
+        route_load<PER>(logits + (size_t)rn * routed, routed, gate, nxt);
+        int pick;
+        float weight;
+        route_pick<PER>(cur, logits + (size_t)r * routed, routed, topk, routed, pick, weight, gate);
+        if (lane <= topk) {
+            pk[r * slots + lane] = pick;
+            wt[r * slots + lane] = weight;
+        }
+        cur = nxt;
+    }
+}
+
 __global__ void __launch_bounds__(1024) route_group_kernel(const float* __restrict__ logits, int rows, int routed,
                                                            int topk, int* __restrict__ picks,
                                                            float* __restrict__ weights, int* __restrict__ ids,
@@ -150,8 +174,10 @@ __global__ void __launch_bounds__(1024) route_group_kernel(const float* __restri
     int* pk = reinterpret_cast<int*>(lds);                     // [rows][slots]
     float* wt = reinterpret_cast<float*>(pk + rows * slots);   // [rows][slots]
     uint32_t* rest = reinterpret_cast<uint32_t*>(wt + rows * slots);
-    for (int r = threadIdx.x >> 6; r < rows; r += blockDim.x >> 6)
-        route_token(logits + (size_t)r * routed, routed, topk, routed, pk + r * slots, wt + r * slots, gate);
+    if (routed <= 64) route_rows<1>(logits, rows, routed, topk, pk, wt, gate);
+    else if (routed <= 128) route_rows<2>(logits, rows, routed, topk, pk, wt, gate);
+    else if (routed <= 256) route_rows<4>(logits, rows, routed, topk, pk, wt, gate);
+    else route_rows<ROUTE_MAX_E / 64>(logits, rows, routed, topk, pk, wt, gate);
     __syncthreads();
     for (int i = threadIdx.x; i < rows * slots; i += blockDim.x) {
         picks[i] = pk[i];
