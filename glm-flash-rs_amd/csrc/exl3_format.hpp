@@ -110,12 +110,6 @@ __device__ __forceinline__ void decode_lane(const uint32_t (&w)[K], uint32_t pre
     }
 }
 
-// decode_lane with the K != 2 pairing for every K (pairs (8l + j + 2, 8l + j)): the prefill path's k order.
-template <int K>
-__device__ __forceinline__ void decode_lane_std(const uint32_t (&w)[K], uint32_t prev, h2_t (&d)[2][8]) {
-    if constexpr (K == 2) decode_lane_windows<K>(w, prev, d);
-    else decode_lane<K>(w, prev, d);
-}
 
 // ---- the decode GEMV's dot: codebook words against activations, without the fp16 weight in between -------------
 // For one state s (16 bits, in half SEL of r), the masked codebook word m = (s * 0xCBAC1FED mod 2^32 & 0x8FFF8FFF) ^

@@ -17,8 +17,7 @@
 //     K in steps of 32, multi-stage direct-to-LDS staging and a register pipeline (next step's decode during this
 //     step's MFMAs). BM = 176 for K = 4: the trellis decode (VALU) is amortised over more rows, an expert of 512
 //     members takes 3 passes instead of 4, and 244 VGPRs and two workgroups' stages (2 x 80.6 KB) still fit.
-//     K = 3 and 5 decode their fragments directly as well (160 and 144 rows, the most without spills); K = 2
-//     hands decoded pieces to their MFMA lanes through LDS (128 rows).
+//     K = 2, 3 and 5 decode their fragments directly as well (176, 160 and 144 rows, the most without spills).
 //   * the 128 columns of a gate/up item, and each 128 of a down item, are one Hadamard block, so the epilogue
 //     (transforms, scales, SwiGLU) runs in the workgroup: accumulators -> LDS (32 rows at a time) -> registers with
 //     8 consecutive values a lane and four rows a wave, so that three of the seven butterfly stages stay in registers.
@@ -33,25 +32,23 @@
 
 namespace gfr {
 
-#ifndef PF_BM_ROWS
-#define PF_BM_ROWS 128
+// Member rows a full-K item at each width: the most that keep two workgroups' stages in LDS and the kernel within
+// 256 VGPRs without spills (K = 4: 244 VGPRs at 176 rows, 2 x 80.6 KB of LDS; K = 3 at 160 rows: 252; K = 5 at
+// 144: 256; K = 2 at 176: 239). Larger items decode each weight tile for more rows.
+#ifndef PF_BM2_ROWS
+#define PF_BM2_ROWS 176
 #endif
-constexpr int PF_BM = PF_BM_ROWS;   // member rows an item (256: one workgroup a CU; 128: two)
-#ifndef PF_BM4_ROWS
-#define PF_BM4_ROWS 176
-#endif
-constexpr int PF_BM4 = PF_BM4_ROWS;  // member rows an item for K = 4 (fits two workgroups a CU in LDS)
-static_assert(PF_BM4 >= PF_BM, "allocation bound");
 #ifndef PF_BM3_ROWS
 #define PF_BM3_ROWS 160
+#endif
+#ifndef PF_BM4_ROWS
+#define PF_BM4_ROWS 176
 #endif
 #ifndef PF_BM5_ROWS
 #define PF_BM5_ROWS 144
 #endif
-constexpr int PF_BM3 = PF_BM3_ROWS;  // K = 3: the direct fragment decode, 160 rows (252 VGPRs, no spills)
-constexpr int PF_BM5 = PF_BM5_ROWS;  // K = 5: 144 rows (256 VGPRs, no spills)
-// member rows a full-K item at each width (K = 2 keeps the fragment exchange through LDS and 128 rows)
-constexpr int pf_bm_for(int bits) { return bits == 4 ? PF_BM4 : bits == 3 ? PF_BM3 : bits == 5 ? PF_BM5 : PF_BM; }
+constexpr int PF_BM2 = PF_BM2_ROWS, PF_BM3 = PF_BM3_ROWS, PF_BM4 = PF_BM4_ROWS, PF_BM5 = PF_BM5_ROWS;
+constexpr int pf_bm_for(int bits) { return bits == 2 ? PF_BM2 : bits == 3 ? PF_BM3 : bits == 4 ? PF_BM4 : PF_BM5; }
 constexpr int PF_MAXU = 1024;       // distinct experts a window (grid / plan bound)
 
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
@@ -388,7 +385,8 @@ __device__ __forceinline__ h8_t a_fragment4(const uint32_t* tw, int lane) {
     return f;
 }
 
-// The same fragment for K = 3 and 5, whose pairs follow the same order (pair_row, K != 2). The lane's two value
+// The same fragment for K = 2, 3 and 5 (the prefill path stages its rows in the K != 2 pair order of pair_row at
+// every width). The lane's two value
 // groups (l = 2g and 2g + 1) are each 4 consecutive values 8 l + 4 half .. + 3 of format lane i; their windows end
 // at bits (v + 1) K of the lane's stream and span 3 K + 16 <= 31 bits, so one funnel shift of two adjacent words
 // (alignbit by a per-lane amount, the same for every tile) holds all four: value v0 + d at bits (3 - d) K.
@@ -397,7 +395,8 @@ __device__ __forceinline__ h8_t a_fragment4(const uint32_t* tw, int lane) {
 template <int K>
 __device__ __forceinline__ void fragk_groups(int lane, int t, int& lo, int& sh) {
     const int c = lane & 15, half = c >> 3, g = (lane >> 4) & 1, i = c & 7;
-    const int v0 = 8 * (2 * g + t) + 4 * half, e = (v0 + 4) * K, hiw = (e - 1) >> 5;
+    const int v0 = 8 * (2 * g + t) + 4 * half;
+    const int e = (v0 + 4) * K, hiw = (e - 1) >> 5;
     lo = K * i + hiw;                                   // the word holding the group's last bit
     sh = 32 * (hiw + 1) - e;
 }
@@ -509,7 +508,6 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
     __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
     __shared__ int rows_sh[BM];
     // K != 4: each lane decodes one trellis lane's 32 values of one tile and the fragments are exchanged here
-    __shared__ __attribute__((aligned(16))) uint4 afrag[(K != 2 || BM == 256) ? 1 : 4][4][64];
 
     const int ncg = a.N / NCOLS;
     // XCD-aware order: the hardware deals consecutive workgroups to the 8 XCDs in turn; renumber so that each XCD gets
@@ -620,42 +618,15 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
     };
     // K = 3, 5: the direct fragment decode's two per-lane funnel shifts (the same for every tile and step)
     uint32_t ksh[2] = {0u, 0u};
-    if constexpr (K == 3 || K == 5) fragk_shifts<K>(lane, ksh);
+    if constexpr (K != 4) fragk_shifts<K>(lane, ksh);
     auto decode_a = [&](int slot, h8_t (&af)[4]) {
         const uint32_t* tw = reinterpret_cast<const uint32_t*>(lds + slot * STAGE + MATS * XBUF);
         if constexpr (K == 4) {
 #pragma unroll
             for (int t4 = 0; t4 < 4; ++t4) af[t4] = a_fragment4(tw + (stile0 + t4) * 64, lane);
-        } else if constexpr (K == 3 || K == 5) {
+        } else {
 #pragma unroll
             for (int t4 = 0; t4 < 4; ++t4) af[t4] = a_fragmentk<K>(tw + (stile0 + t4) * (16 * K), lane, ksh);
-        } else {
-            // lane (t4, kt, i) decodes trellis lane i of k tile kt of tile t4 (32 values: columns i and i + 8 of
-            // 16 rows), then hands each of its four 8-value pieces (column half, word pair g) to the MFMA lane
-            // that owns it: column i + 8 half, k chunk 2 kt + g
-            const int t4 = lane >> 4, kt = (lane >> 3) & 1, i = lane & 7;
-            const uint32_t* tl = tw + (stile0 + t4) * (16 * K) + kt * (8 * K);
-            uint32_t w[K];
-#pragma unroll
-            for (int k = 0; k < K; ++k) w[k] = tl[i * K + k];
-            const uint32_t prev = tl[(i * K + 8 * K - 1) % (8 * K)];
-            h2_t d[2][8];
-            decode_lane_std<K>(w, prev, d);
-#pragma unroll
-            for (int half = 0; half < 2; ++half)
-#pragma unroll
-                for (int g = 0; g < 2; ++g)
-                    afrag[wave][t4][i + 8 * half + 16 * (2 * kt + g)] =
-                        make_uint4(h2_bits(d[half][4 * g]), h2_bits(d[half][4 * g + 1]), h2_bits(d[half][4 * g + 2]),
-                                   h2_bits(d[half][4 * g + 3]));
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-            for (int t = 0; t < 4; ++t) af[t] = __builtin_bit_cast(h8_t, afrag[wave][t][lane]);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");   // the reads complete before the next writes
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
     };
 
@@ -695,7 +666,7 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
         if (s + NS - 1 < S) issue(s + NS - 1);           // into stage s - 1's buffer, now free
         const int sn = (slot + 1) % NS;                   // the next step's slot (the last step reads a stale one,
                                                           // unused)
-        if constexpr (K != 2) {
+        {
             // the next step's decode spread over this step's MFMA groups (sched_barrier keeps each group together,
             // so the VALU of the decode issues while the matrix core works)
             const uint32_t* twn = reinterpret_cast<const uint32_t*>(lds + sn * STAGE + MATS * XBUF);
@@ -732,18 +703,6 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
                     an[t][2 * j + 1] = v[1];
                 }
                 __builtin_amdgcn_sched_barrier(0);
-            }
-        } else {
-            decode_a(sn, an);
-#pragma unroll
-            for (int b = 0; b < RB; ++b) {
-                const h8_t bc = ring[b % D];
-                ring[b % D] = b + D < RB ? read_b(slot, b + D) : read_b(sn, b + D - RB);
-                if (b < nblk) {
-#pragma unroll
-                    for (int t4 = 0; t4 < 4; ++t4)
-                        acc[t4][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac[t4], bc, acc[t4][b], 0, 0, 0);
-                }
             }
         }
         // keep the decode inside this step (the compiler would otherwise sink it next to its use)
@@ -935,7 +894,7 @@ constexpr int PF_SPLIT_PAIRS = PF_SPLIT_PAIRS_MAX;
 constexpr int PF_SPLIT_K = 512;
 constexpr int PF_SPLIT_BM = 32;
 static bool split_ok(int hidden, int inter) { return hidden % PF_SPLIT_K == 0 && inter % PF_SPLIT_K == 0; }
-static_assert(PF_SPLIT_BM <= PF_BM && PF_SPLIT_BM <= PF_BM4 && PF_SPLIT_BM <= PF_BM3 && PF_SPLIT_BM <= PF_BM5,
+static_assert(PF_SPLIT_BM <= PF_BM2 && PF_SPLIT_BM <= PF_BM3 && PF_SPLIT_BM <= PF_BM4 && PF_SPLIT_BM <= PF_BM5,
               "items are bounded at the smallest item size");
 // The most items a window of P pairs over at most maxu distinct experts can plan, at any item size the engine uses.
 static size_t item_bound(size_t P, size_t maxu) {
@@ -993,7 +952,7 @@ static hipError_t launch_gemm_split(int bits, dim3 grid, hipStream_t s, const Pr
 template <int MATS>
 static hipError_t launch_gemm(int bits, dim3 grid, hipStream_t s, const PrefillArgs& a) {
     switch (bits) {
-        case 2: prefill_gemm_kernel<MATS, 2, PF_BM><<<grid, 256, 0, s>>>(a); break;
+        case 2: prefill_gemm_kernel<MATS, 2, PF_BM2><<<grid, 256, 0, s>>>(a); break;
         case 3: prefill_gemm_kernel<MATS, 3, PF_BM3><<<grid, 256, 0, s>>>(a); break;
         case 4: prefill_gemm_kernel<MATS, 4, PF_BM4><<<grid, 256, 0, s>>>(a); break;
         case 5: prefill_gemm_kernel<MATS, 5, PF_BM5><<<grid, 256, 0, s>>>(a); break;
