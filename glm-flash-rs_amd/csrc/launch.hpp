@@ -41,7 +41,6 @@ int gemv_down_splits(int N);    // k-block parts of the decode down GEMV (one a 
 // Decode path: gate/up GEMV with rot_in fused (-> gate/up split partials Zgu [2][SK][P][N]); down GEMV with the
 // gate/up epilogue fused as its activation source and the down epilogue's transform applied to each k-block part
 // (-> Zd [N / 128][P][D], xd [P][N]); the parts' sum + combine.
-// The gate/up GEMV needs gemv_gateup_splits(D) <= 4.
 // One-token windows can route inside the gate/up launch: the token's logits, and where to store its picks /
 // weights and the window's grouping (ids, count, members with stride maxm) for the later launches.
 struct RouteOne {
