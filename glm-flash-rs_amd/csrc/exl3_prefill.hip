@@ -507,7 +507,6 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
     static_assert((BM == 256 || BM == 176 || BM == 160 || BM == 144 || BM == 128 || BM == 32) && NS <= 8, "tile shape");
     __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
     __shared__ int rows_sh[BM];
-    // K != 4: each lane decodes one trellis lane's 32 values of one tile and the fragments are exchanged here
 
     const int ncg = a.N / NCOLS;
     // XCD-aware order: the hardware deals consecutive workgroups to the 8 XCDs in turn; renumber so that each XCD gets
