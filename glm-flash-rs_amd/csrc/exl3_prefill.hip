@@ -134,23 +134,35 @@ __device__ __forceinline__ int l8_row(int lane) { return ((lane >> 2) & 1) | ((l
 // lane holds sigma * H(x) with sigma = (-1)^popcount(lane & 0b11011) (lane_sign). Negation is exact, so every value is
 // bit for bit +- the reference's butterfly result. Stages xor 1, 2, 8 are one v_fmac_f32_dpp a value (the DPP read of
 // a VGPR written by the VALU just before needs two wait states: the s_nop); xor 16 goes through ds_swizzle.
+#define GFR_DPP8(CTRL)                                                                                          \
+    __asm__ volatile("s_nop 1\n\t"                                                                            \
+                     "v_fmac_f32_dpp %0, %0, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                        \
+                     "v_fmac_f32_dpp %1, %1, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                        \
+                     "v_fmac_f32_dpp %2, %2, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                        \
+                     "v_fmac_f32_dpp %3, %3, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                        \
+                     "v_fmac_f32_dpp %4, %4, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                        \
+                     "v_fmac_f32_dpp %5, %5, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                        \
+                     "v_fmac_f32_dpp %6, %6, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                        \
+                     "v_fmac_f32_dpp %7, %7, %8 " CTRL " row_mask:0xf bank_mask:0xf"                              \
+                     : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]),        \
+                       "+v"(v[7])                                                                                \
+                     : "v"(m))
+// The 8 values of a stage in one block: a DPP read of a VGPR written by the VALU just before needs two wait states
+// (the s_nop); inside the block each value was last written 8 instructions earlier.
 template <int M>
 __device__ __forceinline__ void fwht_l8_cross(float (&v)[8], float m) {
+    if constexpr (M == 1) {
+        GFR_DPP8("quad_perm:[1,0,3,2]");
+    } else if constexpr (M == 2) {
+        GFR_DPP8("quad_perm:[2,3,0,1]");
+    } else if constexpr (M == 8) {
+        GFR_DPP8("row_ror:8");
+    } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        if constexpr (M == 1)
-            __asm__ volatile("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf"
-                             : "+v"(v[i]) : "v"(m));
-        else if constexpr (M == 2)
-            __asm__ volatile("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf"
-                             : "+v"(v[i]) : "v"(m));
-        else if constexpr (M == 8)
-            __asm__ volatile("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 row_ror:8 row_mask:0xf bank_mask:0xf"
-                             : "+v"(v[i]) : "v"(m));
-        else
-            v[i] = __builtin_fmaf(lane_xor_f<M>(v[i]), m, v[i]);
+        for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(lane_xor_f<M>(v[i]), m, v[i]);
     }
 }
+#undef GFR_DPP8
 // sigma of the lane (see fwht_l8_cross): the sign a transformed value carries
 __device__ __forceinline__ float lane_sign(int lane) { return (__popc(lane & 0x1b) & 1) ? -1.f : 1.f; }
 
