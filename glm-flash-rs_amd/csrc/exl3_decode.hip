@@ -498,7 +498,7 @@ __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const float gg = fminf(bf16r(gv[j] * HAD_SCALE * svg[j]), a.limit);
-                    const float uu = fminf(fmaxf(bf16r(uv[j] * HAD_SCALE * svu[j]), -a.limit), a.limit);
+                    const float uu = __builtin_amdgcn_fmed3f(bf16r(uv[j] * HAD_SCALE * svu[j]), -a.limit, a.limit);
                     const float act = bf16r(bf16r(gg / (1.f + expf(-gg))) * uu);
                     v[j] = act * sdd[j];
                 }
@@ -749,7 +749,7 @@ __global__ void __launch_bounds__(64) gateup_epilogue_kernel(const float* __rest
     for (int j = 0; j < 2; ++j) {
         const float gg = fminf(bf16r(gv[j] * HAD_SCALE * f16_to_f32(svh_g[(size_t)e * N + n + j])), limit);
         const float uu =
-            fminf(fmaxf(bf16r(uv[j] * HAD_SCALE * f16_to_f32(svh_u[(size_t)e * N + n + j])), -limit), limit);
+            __builtin_amdgcn_fmed3f(bf16r(uv[j] * HAD_SCALE * f16_to_f32(svh_u[(size_t)e * N + n + j])), -limit, limit);
         const float act = bf16r(bf16r(gg / (1.f + expf(-gg))) * uu);
         v[j] = act * f16_to_f32(suh_d[(size_t)e * N + n + j]);
     }

@@ -829,8 +829,8 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
                     float g1 = gv[i + 1] * HAD_SCALE * sc[0][i + 1], u1 = uv[i + 1] * HAD_SCALE * sc[1][i + 1];
                     bf16r2(g0, u0);
                     bf16r2(g1, u1);
-                    const float gg0 = fminf(g0, a.limit), uu0 = fminf(fmaxf(u0, -a.limit), a.limit);
-                    const float gg1 = fminf(g1, a.limit), uu1 = fminf(fmaxf(u1, -a.limit), a.limit);
+                    const float gg0 = fminf(g0, a.limit), uu0 = __builtin_amdgcn_fmed3f(u0, -a.limit, a.limit);
+                    const float gg1 = fminf(g1, a.limit), uu1 = __builtin_amdgcn_fmed3f(u1, -a.limit, a.limit);
                     // silu through the hardware exp2 / reciprocal (within an ulp or two of expf and the IEEE divide;
                     // the bf16 rounding that follows absorbs the difference)
                     const float ex0 = __builtin_amdgcn_exp2f(gg0 * -1.4426950408889634f);
