@@ -95,7 +95,7 @@ __global__ void __launch_bounds__(64) rot_in_kernel(const uint16_t* __restrict__
     for (int j = 0; j < 2; ++j) v[j] = (F16IN ? f16_to_f32(xr[j]) : bf16_to_f32(xr[j])) * f16_to_f32(suh[j]);
     fwht128_w64(v, lane);
     uint16_t* o = (mat ? out1 : out0) + (size_t)p * K + k;
-    const uint32_t packed = (uint32_t)f16_of_product(v[0], HAD_SCALE) | ((uint32_t)f16_of_product(v[1], HAD_SCALE) << 16);
+    const uint32_t packed = f16x2_of_products(v[0], v[1], HAD_SCALE);
     *reinterpret_cast<uint32_t*>(o) = packed;
 }
 
@@ -507,7 +507,7 @@ __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
                 if (hb == 0 && a.xd) {
                     const int p = __builtin_amdgcn_readlane(pair_l, (c0 + m) & 63);
                     *reinterpret_cast<uint32_t*>(a.xd + (size_t)p * a.Kin + n) =
-                        (uint32_t)f16_of_product(v[0], HAD_SCALE) | ((uint32_t)f16_of_product(v[1], HAD_SCALE) << 16);
+                        f16x2_of_products(v[0], v[1], HAD_SCALE);
                 }
             }
         }

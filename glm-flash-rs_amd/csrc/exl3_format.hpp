@@ -210,6 +210,15 @@ __device__ __forceinline__ uint16_t f16_of_product(float a, float b) {
     __asm__ volatile("" : "+v"(p));
     return f32_to_f16(p);
 }
+// (fp16(a0 * b) low, fp16(a1 * b) high): the same roundings as f16_of_product, both conversions in one
+// v_cvt_pk_f16_f32 (round to nearest even).
+__device__ __forceinline__ uint32_t f16x2_of_products(float a0, float a1, float b) {
+    typedef float f2_t __attribute__((ext_vector_type(2)));
+    typedef _Float16 hh2_t __attribute__((ext_vector_type(2)));
+    float p0 = a0 * b, p1 = a1 * b;
+    __asm__ volatile("" : "+v"(p0), "+v"(p1));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2_t){p0, p1}, hh2_t));
+}
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
 
 // The value of lane (lane ^ M) for M in {1, 2, 4, 8, 16, 32}, without LDS memory: DPP quad permutes, row shifts and

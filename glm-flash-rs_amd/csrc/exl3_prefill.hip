@@ -200,7 +200,7 @@ __device__ __forceinline__ void store_pairs_l8(uint16_t* block, const float (&v)
     uint32_t w[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        w[i] = (uint32_t)f16_of_product(v[2 * i], scale) | ((uint32_t)f16_of_product(v[2 * i + 1], scale) << 16);
+        w[i] = f16x2_of_products(v[2 * i], v[2 * i + 1], scale);
     const int j = l8_j(lane);
     const bool odd = j & 1;
     const uint32_t r0 = lane_xor<1>(odd ? w[0] : w[2]), r1 = lane_xor<1>(odd ? w[1] : w[3]);
