@@ -250,12 +250,31 @@ __device__ __forceinline__ float lane_xor_f(float v) {
     return __builtin_bit_cast(float, lane_xor<M>(__builtin_bit_cast(uint32_t, v)));
 }
 
+// One butterfly stage between lanes l and l ^ M, as one fma a value: v' = v * m + partner with m = +1 in the lower
+// lane (lower + upper) and -1 in the upper lane (lower - upper); fma by +-1 rounds exactly as the add or subtract.
+// Partners: DPP inside a 16-lane row (xor 4 as two bank-masked row shifts into one register), the gfx950 permlane16 /
+// permlane32 swaps across rows (no LDS round trip, which sits on the decode launches' latency chain). A swap of
+// (x, x) leaves the lower lane's own value in r[0] and the partner in r[1], the upper lane's the other way round, so
+// r[0] + m r[1] is (lower + upper) in the lower lane and (lower - upper) in the upper one.
 template <int M>
 __device__ __forceinline__ void fwht_stage(float (&v)[2], int lane) {
+    const float m = (lane & M) ? -1.f : 1.f;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const float o = lane_xor_f<M>(v[j]);
-        v[j] = (lane & M) ? o - v[j] : v[j] + o;
+        if constexpr (M == 16 || M == 32) {
+            const uint32_t b = __builtin_bit_cast(uint32_t, v[j]);
+            const auto r = M == 16 ? __builtin_amdgcn_permlane16_swap(b, b, false, false)
+                                   : __builtin_amdgcn_permlane32_swap(b, b, false, false);
+            v[j] = __builtin_fmaf(__builtin_bit_cast(float, (uint32_t)r[1]), m,
+                                  __builtin_bit_cast(float, (uint32_t)r[0]));
+        } else if constexpr (M == 4) {
+            const int x = __builtin_bit_cast(int, v[j]);
+            int p = __builtin_amdgcn_update_dpp(x, x, 0x104, 0xf, 0x5, false);   // lanes 0-3, 8-11: row_shl 4
+            p = __builtin_amdgcn_update_dpp(p, x, 0x114, 0xf, 0xA, false);       // lanes 4-7, 12-15: row_shr 4
+            v[j] = __builtin_fmaf(v[j], m, __builtin_bit_cast(float, p));
+        } else {
+            v[j] = __builtin_fmaf(v[j], m, lane_xor_f<M>(v[j]));
+        }
     }
 }
 
@@ -276,22 +295,31 @@ __device__ __forceinline__ void fwht128_w64(float (&v)[2], int lane) {
     fwht_stage<32>(v, lane);
 }
 
-// Wave-wide reductions through lane_xor (every lane gets the result).
-__device__ __forceinline__ float wave_max(float v) {
-    v = fmaxf(v, lane_xor_f<1>(v));
-    v = fmaxf(v, lane_xor_f<2>(v));
-    v = fmaxf(v, lane_xor_f<4>(v));
-    v = fmaxf(v, lane_xor_f<8>(v));
-    v = fmaxf(v, lane_xor_f<16>(v));
-    return fmaxf(v, lane_xor_f<32>(v));
+__device__ __forceinline__ float max_nn(float a, float b) {
+    float r;
+    __asm__("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
 }
-__device__ __forceinline__ int wave_min(int v) {
-    v = min(v, (int)lane_xor<1>((uint32_t)v));
-    v = min(v, (int)lane_xor<2>((uint32_t)v));
-    v = min(v, (int)lane_xor<4>((uint32_t)v));
-    v = min(v, (int)lane_xor<8>((uint32_t)v));
-    v = min(v, (int)lane_xor<16>((uint32_t)v));
-    return min(v, (int)lane_xor<32>((uint32_t)v));
+// The wave-wide maximum (every lane gets it) of inputs that are never NaN, in 8 VALU operations on the shortest
+// chain: v_max_f32 with the DPP operand (quad swaps, then the half-row and row mirrors: any pairing that joins the
+// two halves gives every lane the maximum), then the permlane16 and permlane32 swaps. (fmaxf's NaN quieting would add
+// a canonicalising max per operand.)
+__device__ __forceinline__ float wave_max_nn(float v) {
+    __asm__("s_nop 1\n\t"
+            "v_max_f32_dpp %0, %0, %0 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+            "s_nop 1\n\t"
+            "v_max_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+            "s_nop 1\n\t"
+            "v_max_f32_dpp %0, %0, %0 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+            "s_nop 1\n\t"
+            "v_max_f32_dpp %0, %0, %0 row_mirror row_mask:0xf bank_mask:0xf"
+            : "+v"(v));
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    v = max_nn(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+    const uint32_t c = __builtin_bit_cast(uint32_t, v);
+    const auto q = __builtin_amdgcn_permlane32_swap(c, c, false, false);
+    return max_nn(__builtin_bit_cast(float, (uint32_t)q[0]), __builtin_bit_cast(float, (uint32_t)q[1]));
 }
 
 }  // namespace gfr

@@ -51,18 +51,22 @@ __device__ __forceinline__ void route_pick(const RouteIn<PER>& in, const float* 
                                            bool need_weight = true) {
     const int lane = threadIdx.x & 63;
     float v[PER];
+    // a uniform branch: the softmax gate skips the sigmoids (selected after the fact, they were computed anyway)
+    if (g.bias) {
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-        const int e = j * 64 + lane;
-        v[j] = e < E ? (g.bias ? sigmoidf_(in.l[j]) + in.b[j] : in.l[j]) : -__builtin_inff();
+        for (int j = 0; j < PER; ++j)
+            v[j] = j * 64 + lane < E ? sigmoidf_(in.l[j]) + in.b[j] : -__builtin_inff();
+    } else {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) v[j] = j * 64 + lane < E ? in.l[j] : -__builtin_inff();
     }
     float my_v = 0.f;                                  // lane s < topk: the s-th pick's logit and id
     int my_e = 0;
     for (int s = 0; s < topk; ++s) {
         float lm = v[0];
 #pragma unroll
-        for (int j = 1; j < PER; ++j) lm = fmaxf(lm, v[j]);
-        const float best = wave_max(lm);
+        for (int j = 1; j < PER; ++j) lm = max_nn(lm, v[j]);
+        const float best = wave_max_nn(lm);           // scores are finite or -inf
         int be = 0;
 #pragma unroll
         for (int j = PER - 1; j >= 0; --j) {           // the lowest register (id block) holding it wins
