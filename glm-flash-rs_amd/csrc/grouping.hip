@@ -16,22 +16,37 @@
 
 namespace gfr {
 
-// Inclusive scan of x over the workgroup (blockDim.x a multiple of 64, at most 1024). `scratch` holds 16 ints.
-// Returns the inclusive prefix; *total receives the sum.
+// Inclusive scan of x over the wave: DPP row shifts by 1, 2, 4, 8 inside each 16-lane row (lanes past the row's
+// start read 0), then the gfx9 row broadcasts (lane 15 of rows 0 and 2 into rows 1 and 3, lane 31 into rows 2 and 3).
+__device__ __forceinline__ int wave_scan(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);   // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);   // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true);   // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true);   // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return x;
+}
+
+// Inclusive scan of x over the workgroup (blockDim.x a multiple of 64, at most 1024). `scratch` holds 16 ints,
+// 16-byte aligned. Returns the inclusive prefix; *total receives the sum. The wave totals are read back as four
+// 16-byte LDS loads issued together.
 __device__ __forceinline__ int block_scan(int x, int* scratch, int* total) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int v = __shfl_up(x, d, 64);
-        if (lane >= d) x += v;
-    }
+    x = wave_scan(x);
     if (lane == 63) scratch[wave] = x;
     __syncthreads();
+    int4 q[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) q[j] = reinterpret_cast<const int4*>(scratch)[j];
+    const int t[16] = {q[0].x, q[0].y, q[0].z, q[0].w, q[1].x, q[1].y, q[1].z, q[1].w,
+                       q[2].x, q[2].y, q[2].z, q[2].w, q[3].x, q[3].y, q[3].z, q[3].w};
     int off = 0, all = 0;
-    for (int w = 0; w < nw; ++w) {
-        const int s = scratch[w];
-        if (w < wave) off += s;
-        all += s;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+        const int v = w < nw ? t[w] : 0;
+        off += w < wave ? v : 0;
+        all += v;
     }
     __syncthreads();
     *total = all;
@@ -67,13 +82,13 @@ __device__ __forceinline__ void group_small_body(const int* picks, int rows, int
         int c = 0;
         if (e < E)
             for (int w = 0; w < NWD; ++w) c += __popc(bits[e * NWD + w]);
-        int total;
-        if (plan) {                                          // used experts the weights hold (ids below plan_E)
-            int tw;
-            block_scan(c > 0 && e < plan_E, scan_scratch, &tw);
-            base_w += tw;
-        }
-        const int incl = block_scan(c > 0, scan_scratch, &total);
+        // one scan of both counts: used experts (low 16 bits) and, for the plan, the used experts the weights hold
+        // (ids below plan_E, high 16 bits); a round has at most 1024 experts, so neither field carries over
+        int packed_total;
+        const int packed = block_scan((c > 0 ? 1 : 0) | (plan && c > 0 && e < plan_E ? 1 << 16 : 0), scan_scratch,
+                                      &packed_total);
+        const int incl = packed & 0xffff, total = packed_total & 0xffff;
+        base_w += packed_total >> 16;
         if (e < E) {
             place[e] = c > 0 ? base + incl - 1 : -1;
             if (c > 0) {
@@ -128,7 +143,7 @@ __global__ void __launch_bounds__(1024) group_small_kernel(const int* __restrict
                                                            int E, int* __restrict__ ids, int* __restrict__ count,
                                                            int* __restrict__ members, int maxm) {
     extern __shared__ uint32_t lds[];
-    __shared__ int scan_scratch[16];
+    __shared__ __attribute__((aligned(16))) int scan_scratch[16];
     int* pk = reinterpret_cast<int*>(lds);                     // [rows][slots], read many times below
     for (int i = threadIdx.x; i < rows * slots; i += blockDim.x) pk[i] = picks[i];
     __syncthreads();
@@ -169,7 +184,7 @@ __global__ void __launch_bounds__(1024) route_group_kernel(const float* __restri
                                                            int* __restrict__ plan_items, int* __restrict__ plan,
                                                            int plan_E, RouteGate gate) {
     extern __shared__ uint32_t lds[];
-    __shared__ int scan_scratch[16];
+    __shared__ __attribute__((aligned(16))) int scan_scratch[16];
     const int slots = topk + 1, E = routed + 1;
     int* pk = reinterpret_cast<int*>(lds);                     // [rows][slots]
     float* wt = reinterpret_cast<float*>(pk + rows * slots);   // [rows][slots]
@@ -215,7 +230,7 @@ __global__ void __launch_bounds__(256) group_mark_kernel(const int* __restrict__
 // Launch 2, workgroup per expert: exclusive popcount prefix of its bitmap words, and its row count.
 __global__ void __launch_bounds__(256) group_prefix_kernel(const uint32_t* __restrict__ bits, int rows,
                                                            int* __restrict__ prefix, int* __restrict__ counts) {
-    __shared__ int scan_scratch[16];
+    __shared__ __attribute__((aligned(16))) int scan_scratch[16];
     const int e = blockIdx.x, NWD = (rows + 31) >> 5;
     const int per = (NWD + blockDim.x - 1) / blockDim.x, w0 = threadIdx.x * per;
     const uint32_t* b = bits + (size_t)e * NWD;
@@ -244,7 +259,7 @@ __global__ void __launch_bounds__(256) group_scatter_kernel(const int* __restric
                                                             int maxm, int bm, int* __restrict__ plan_ucnt,
                                                             int* __restrict__ plan_items, int* __restrict__ plan,
                                                             int plan_E) {
-    __shared__ int scan_scratch[16];
+    __shared__ __attribute__((aligned(16))) int scan_scratch[16];
     __shared__ int tot_sh[4];
     const int e = blockIdx.x, NWD = (rows + 31) >> 5;
     int below = 0, used = 0, ibelow = 0, itotal = 0;
@@ -323,7 +338,6 @@ namespace gfr {
 size_t group_small_lds(int rows, int slots, int E) {
     return ((size_t)rows * slots + (size_t)E * ((rows + 31) / 32) + 2 * (size_t)E) * 4;
 }
-
 hipError_t launch_group_small(hipStream_t s, const int* picks, int rows, int slots, int E, int* ids, int* count,
                               int* members, int maxm) {
     const size_t lds = group_small_lds(rows, slots, E);
