@@ -21,6 +21,9 @@
 
 namespace gfr {
 
+#ifndef GFR_GATEUP_PREFETCH
+#define GFR_GATEUP_PREFETCH 1
+#endif
 #ifdef GFR_GEMV_TRACE
 // timing builds only: per-wave timestamps of the decode launches (gate/up, down, finish)
 __device__ uint64_t* g_gemv_trace[3];
@@ -138,6 +141,8 @@ struct GemvArgs {
     int* members_out;
     int x_f16;               // XSRC 1: the input rows are fp16 (the single linear) instead of bf16
     int ucap;                // programs x = chunk * ucap + u: distinct-expert slots of the grid (RB members a chunk)
+    const uint32_t* tnext;   // gate/up GEMV: the down trellis [E][...] read ahead by the gate waves, or nullptr
+    size_t next_words;       // its words an expert
 };
 
 
@@ -381,6 +386,23 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
         }
     };
     chunk(c0, nr0);
+#if GFR_GATEUP_PREFETCH
+    // Read-ahead of this expert's down matrix for the next launch. The gate waves (mat 0, first chunk) end about 2 us
+    // before the up waves that share their CUs, with the HBM idle: each loads one dword of every 128-byte line of its
+    // share (gridDim.y * SK * NW gate waves an expert), so the down launch's trellis loads hit the memory-side cache
+    // instead of HBM. The wave waits for them before it ends (the loaded registers are never read).
+    if (MATS == 2 && a.tnext && mat == 0 && c0 == 0) {
+        const int nwv = (int)gridDim.y * a.SK * NW, widx = ((int)blockIdx.y * a.SK + split) * NW + wave;
+        const size_t lines = a.next_words / 32, per = (lines + nwv - 1) / nwv;
+        const size_t l0 = (size_t)widx * per, l1 = l0 + per < lines ? l0 + per : lines;
+        const uint32_t* base = a.tnext + (size_t)e * a.next_words;
+        for (size_t l = l0 + lane; l < l1; l += 64) {
+            uint32_t d;
+            __asm__ volatile("global_load_dword %0, %1, off" : "=v"(d) : "v"(base + l * 32) : "memory");
+        }
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+#endif
     GEMV_MARK(TW, tslot, 5);
 }
 
@@ -886,8 +908,11 @@ hipError_t launch_gemv(hipStream_t s, const uint16_t* X0, const uint16_t* X1, co
 hipError_t launch_expert_gateup(hipStream_t s, const uint16_t* x, int x_stride, const uint16_t* suh_g,
                                 const uint16_t* suh_u, const uint32_t* gt, const uint32_t* ut, const int* uids,
                                 const int* ucount, const int* members, float* Zgu, int D, int N, int P, int rows,
-                                int maxm, int slots, int E, int bits, int maxu, const RouteOne* route) {
+                                int maxm, int slots, int E, int bits, int maxu, const RouteOne* route,
+                                const uint32_t* dt_next) {
     GemvArgs a{};
+    a.tnext = dt_next;
+    a.next_words = (size_t)(N / 16) * (D / 16) * 8 * bits;
     a.x0 = x; a.x_stride = x_stride; a.suh0 = suh_g; a.suh1 = suh_u; a.t0 = gt; a.t1 = ut;
     a.uids = uids; a.ucount = ucount; a.members = members; a.z = Zgu; a.Kin = D; a.N = N; a.P = P;
     a.SK = gemv_gateup_splits(D); a.maxm = maxm; a.slots = slots; a.E = E;

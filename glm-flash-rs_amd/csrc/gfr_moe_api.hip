@@ -181,7 +181,7 @@ int experts_run(gfr_experts* ex, hipStream_t stream, const gfr_exl3_experts* w, 
     hipError_t e;
     if ((e = gfr::launch_expert_gateup(stream, input, input_stride, w->suh_g, w->suh_u, w->gt, w->ut, ids, count,
                                        members, ex->zgu, D, N, P, rows, maxm, ex->slots, w->experts, w->bits, maxu,
-                                       route)) !=
+                                       route, w->dt)) !=
         hipSuccess)
         return hip_fail(e, "gate/up gemv");
     if (launches == 1) return 0;

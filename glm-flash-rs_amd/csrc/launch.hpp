@@ -57,7 +57,10 @@ struct RouteOne {
 hipError_t launch_expert_gateup(hipStream_t s, const uint16_t* x, int x_stride, const uint16_t* suh_g,
                                 const uint16_t* suh_u, const uint32_t* gt, const uint32_t* ut, const int* uids,
                                 const int* ucount, const int* members, float* Zgu, int D, int N, int P, int rows,
-                                int maxm, int slots, int E, int bits, int maxu, const RouteOne* route);
+                                int maxm, int slots, int E, int bits, int maxu, const RouteOne* route,
+                                const uint32_t* dt_next = nullptr);
+// dt_next: the layer's down trellis; the gate waves read each window expert's down matrix once into the caches
+// after their own work (expert_gemv_kernel), so the down launch's first loads hit the memory-side cache
 // SKgu: the gate/up partials' K splits (gemv_gateup_splits)
 hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, int SKgu, const uint16_t* svh_g,
                               const uint16_t* svh_u, const uint16_t* suh_d, float limit, uint16_t* xd,
