@@ -413,6 +413,7 @@ def main():
     layer_total = sum(nbytes.values())
     us_step = secs * 1e6 / args.steps
     gu_gbs = nbytes["gate_up"] / launches_us["gate_up"] / 1e3
+    read_ahead = SLOTS * D * N * BITS // 8
     roof = {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
             "kernel": "expert_gemv_kernel<4,8,4,2,1,1,true> (the layer's gate/up launch: router, input rotation, "
@@ -420,6 +421,11 @@ def main():
             "bytes_per_launch": nbytes["gate_up"], "us_per_launch": round(launches_us["gate_up"], 3),
             "timing": "HIP events on the layer's stream around graph replays of the layer cut after its first launch "
                       "(gfr_moe_set_launches(1)); includes the launch's share of the inter-kernel gaps",
+            "read_ahead": {"bytes": read_ahead,
+                           "what": "the gate waves also read each window expert's down trellis once into the "
+                                   "memory-side cache for the down launch: in this launch's time and traffic, not in "
+                                   "bytes_per_launch (they are the down launch's operand bytes)",
+                           "gbs_incl": round((nbytes["gate_up"] + read_ahead) / launches_us["gate_up"] / 1e3, 1)},
             "down": {"kernel": "down_gemv_kernel<4,1>", "bytes_per_launch": nbytes["down"],
                      "us_per_launch": round(launches_us["down"], 3),
                      "gbs": round(nbytes["down"] / launches_us["down"] / 1e3, 1),
