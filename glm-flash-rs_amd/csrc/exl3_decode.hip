@@ -753,27 +753,37 @@ __global__ void __launch_bounds__(64) gateup_epilogue_kernel(const float* __rest
     const int lane = threadIdx.x;
     const int e = pick[row * slots + slot];
     const int n = blk * 128 + 2 * lane;
-    float gv[2], uv[2];
+    // the gate and up splits' partials eight each at a time in flight (a pair of columns one 8-byte load), added in
+    // split order; the expert's scales are loaded once its id has landed
+    float gv[2] = {0.f, 0.f}, uv[2] = {0.f, 0.f};
+    for (int s0 = 0; s0 < SK; s0 += 8) {
+        float2 zg[8], zu[8];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        float sg = 0.f, su = 0.f;
-        for (int s = 0; s < SK; ++s) {
-            sg += Z[((size_t)(0 * SK + s) * P + p) * N + n + j];
-            su += Z[((size_t)(1 * SK + s) * P + p) * N + n + j];
-        }
-        gv[j] = sg;
-        uv[j] = su;
+        for (int k = 0; k < 8; ++k)
+            if (s0 + k < SK) {
+                zg[k] = *reinterpret_cast<const float2*>(Z + ((size_t)(s0 + k) * P + p) * N + n);
+                zu[k] = *reinterpret_cast<const float2*>(Z + ((size_t)(SK + s0 + k) * P + p) * N + n);
+            }
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (s0 + k < SK) {
+                gv[0] += zg[k].x; gv[1] += zg[k].y;
+                uv[0] += zu[k].x; uv[1] += zu[k].y;
+            }
     }
+    const size_t so = (size_t)e * N + n;
+    const uint32_t sg = *reinterpret_cast<const uint32_t*>(svh_g + so), su = *reinterpret_cast<const uint32_t*>(svh_u + so),
+                   sd = *reinterpret_cast<const uint32_t*>(suh_d + so);
     fwht128_w64(gv, lane);
     fwht128_w64(uv, lane);
     float v[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const float gg = fminf(bf16r(gv[j] * HAD_SCALE * f16_to_f32(svh_g[(size_t)e * N + n + j])), limit);
-        const float uu =
-            __builtin_amdgcn_fmed3f(bf16r(uv[j] * HAD_SCALE * f16_to_f32(svh_u[(size_t)e * N + n + j])), -limit, limit);
+        const float gg = fminf(bf16r(gv[j] * HAD_SCALE * f16_to_f32((uint16_t)(sg >> (16 * j)))), limit);
+        const float uu = __builtin_amdgcn_fmed3f(bf16r(uv[j] * HAD_SCALE * f16_to_f32((uint16_t)(su >> (16 * j)))),
+                                                 -limit, limit);
         const float act = bf16r(bf16r(gg / (1.f + expf(-gg))) * uu);
-        v[j] = act * f16_to_f32(suh_d[(size_t)e * N + n + j]);
+        v[j] = act * f16_to_f32((uint16_t)(sd >> (16 * j)));
     }
     fwht128_w64(v, lane);
     const uint16_t h0 = f16_of_product(v[0], HAD_SCALE), h1 = f16_of_product(v[1], HAD_SCALE);
@@ -799,17 +809,25 @@ __global__ void __launch_bounds__(64) down_epilogue_kernel(const float* __restri
     const int lane = threadIdx.x;
     const int e = pick[row * slots + slot];
     const int n = blk * 128 + 2 * lane;
-    float v[2];
+    // the splits' partials sixteen at a time in flight (each pair of columns one 8-byte load), added in split order
+    float v[2] = {0.f, 0.f};
+    for (int k0 = 0; k0 < SK; k0 += 16) {
+        float2 zs[16];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        float s = 0.f;
-        for (int k = 0; k < SK; ++k) s += Z[((size_t)k * P + p) * D + n + j];
-        v[j] = s;
+        for (int k = 0; k < 16; ++k)
+            if (k0 + k < SK) zs[k] = *reinterpret_cast<const float2*>(Z + ((size_t)(k0 + k) * P + p) * D + n);
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            if (k0 + k < SK) {
+                v[0] += zs[k].x;
+                v[1] += zs[k].y;
+            }
     }
+    const uint32_t sv = *reinterpret_cast<const uint32_t*>(svh_d + (size_t)e * D + n);
     fwht128_w64(v, lane);
     float2 o;
-    o.x = v[0] * HAD_SCALE * f16_to_f32(svh_d[(size_t)e * D + n]);
-    o.y = v[1] * HAD_SCALE * f16_to_f32(svh_d[(size_t)e * D + n + 1]);
+    o.x = v[0] * HAD_SCALE * f16_to_f32((uint16_t)sv);
+    o.y = v[1] * HAD_SCALE * f16_to_f32((uint16_t)(sv >> 16));
     *reinterpret_cast<float2*>(y + (size_t)p * D + n) = o;
 }
 
