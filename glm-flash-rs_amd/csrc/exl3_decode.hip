@@ -983,11 +983,12 @@ hipError_t launch_sum_finish(hipStream_t s, const float* Zd, float* y, int rows,
 }
 
 // One linear with its input rotation fused (XSRC 1, fp16 input): Z[split][n] partials of
-// W_q[0] over one row, one split a 256-k pair of blocks (gemv_linear_splits), added in order by the epilogue launch.
-// Four waves a split, four k tiles each: (kin / 256) x (n / 128) workgroups, 384 waves at config 1 (measured
-// against 192, 768 and other shapes on MI355X: 6.8 against 7.1-8.7 us).
+// W_q[0] over one row, one split a 128-k block (gemv_linear_splits), added in order by the epilogue launch. Four
+// waves a split, two k tiles each: (kin / 128) x (n / 128) workgroups, 768 waves at config 1. Measured on MI355X
+// with the epilogue loading all splits at once: 5.57 us against 5.90 (384 waves, four tiles), 6.10 (two-wave
+// workgroups, four tiles) and 6.85 (two-wave, two tiles).
 #ifndef GFR_LIN_KTW
-#define GFR_LIN_KTW 4
+#define GFR_LIN_KTW 2
 #endif
 #ifndef GFR_LIN_NW
 #define GFR_LIN_NW 4
