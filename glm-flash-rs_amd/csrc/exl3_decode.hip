@@ -876,7 +876,12 @@ static int ktw_for(int Kin) {
 int gemv_splits(int Kin) { return Kin / 16 / (4 * ktw_for(Kin)); }
 // waves a workgroup of the block-building GEMVs: one 128-block each, as many as divide the blocks
 static int nw_gateup(int D) { return (D / 128) % 4 == 0 ? 4 : 2; }   // hidden: a multiple of 256
-int gemv_gateup_splits(int D) { return D / 128 / nw_gateup(D); }
+// k tiles a wave of the gate/up GEMV: 8, one 128-point block (the bs = 1 layer measured 18.94 us against 19.13 with
+// 4, twice the waves, each block's rotation built by two of them)
+#ifndef GFR_GU_KTW
+#define GFR_GU_KTW 8
+#endif
+int gemv_gateup_splits(int D) { return D / 16 / GFR_GU_KTW / nw_gateup(D); }
 int gemv_down_splits(int N) { return N / 128; }   // one part a 128-k block (down_gemv_kernel)
 
 template <int K, int KTW, int NW, int MATS, int XSRC, bool ROUTE1>
@@ -941,9 +946,11 @@ hipError_t launch_expert_gateup(hipStream_t s, const uint16_t* x, int x_stride, 
         a.logits = route->logits; a.routed = route->routed; a.pick_out = route->picks; a.weight_out = route->weights;
         a.route_bias = route->bias; a.route_scale = route->scale;
         a.ids_out = route->ids; a.count_out = route->count; a.members_out = route->members;
-        return nw == 4 ? gemv_bits<8, 4, 2, 1, true>(bits, 1, grid, s, a) : gemv_bits<8, 2, 2, 1, true>(bits, 1, grid, s, a);
+        return nw == 4 ? gemv_bits<GFR_GU_KTW, 4, 2, 1, true>(bits, 1, grid, s, a)
+                       : gemv_bits<GFR_GU_KTW, 2, 2, 1, true>(bits, 1, grid, s, a);
     }
-    return nw == 4 ? gemv_bits<8, 4, 2, 1>(bits, rb, grid, s, a) : gemv_bits<8, 2, 2, 1>(bits, rb, grid, s, a);
+    return nw == 4 ? gemv_bits<GFR_GU_KTW, 4, 2, 1>(bits, rb, grid, s, a)
+                   : gemv_bits<GFR_GU_KTW, 2, 2, 1>(bits, rb, grid, s, a);
 }
 
 hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, int SKgu, const uint16_t* svh_g,
