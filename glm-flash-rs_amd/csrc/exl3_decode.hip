@@ -389,18 +389,37 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
 #if GFR_GATEUP_PREFETCH
     // Read-ahead of this expert's down matrix for the next launch. The gate waves (mat 0, first chunk) end about 2 us
     // before the up waves that share their CUs, with the HBM idle: each loads one dword of every 128-byte line of its
-    // share (gridDim.y * SK * NW gate waves an expert), so the down launch's trellis loads hit the memory-side cache
-    // instead of HBM. The wave waits for them before it ends (the loaded registers are never read).
+    // share (gridDim.y * SK * NW gate waves an expert, at most 4 lines a lane), so the down launch's trellis loads hit
+    // the memory-side cache instead of HBM. A lane's loads and the wait for them are one asm statement with
+    // early-clobber outputs: the loaded registers are never read, and no register the compiler allocates can be
+    // written by a load still in flight (a late return into a reused address register sends the next load astray).
     if (MATS == 2 && a.tnext && mat == 0 && c0 == 0) {
         const int nwv = (int)gridDim.y * a.SK * NW, widx = ((int)blockIdx.y * a.SK + split) * NW + wave;
         const size_t lines = a.next_words / 32, per = (lines + nwv - 1) / nwv;
         const size_t l0 = (size_t)widx * per, l1 = l0 + per < lines ? l0 + per : lines;
-        const uint32_t* base = a.tnext + (size_t)e * a.next_words;
-        for (size_t l = l0 + lane; l < l1; l += 64) {
-            uint32_t d;
-            __asm__ volatile("global_load_dword %0, %1, off" : "=v"(d) : "v"(base + l * 32) : "memory");
+        if (l0 < l1 && per <= 256) {
+            const uint32_t* base = a.tnext + (size_t)e * a.next_words;
+            // lines past the share re-read its last line (the count is the wave's, the same on every lane)
+            auto at = [&](int j) {
+                const size_t l = l0 + lane + 64 * j;
+                return base + (l < l1 ? l : l1 - 1) * 32;
+            };
+            uint32_t d0, d1, d2, d3;
+            const int nl = (int)((per + 63) / 64);
+            if (nl == 1)
+                __asm__ volatile("global_load_dword %0, %1, off\n\ts_waitcnt vmcnt(0)"
+                                 : "=&v"(d0) : "v"(at(0)) : "memory");
+            else if (nl == 2)
+                __asm__ volatile("global_load_dword %0, %2, off\n\tglobal_load_dword %1, %3, off\n\t"
+                                 "s_waitcnt vmcnt(0)"
+                                 : "=&v"(d0), "=&v"(d1) : "v"(at(0)), "v"(at(1)) : "memory");
+            else
+                __asm__ volatile("global_load_dword %0, %4, off\n\tglobal_load_dword %1, %5, off\n\t"
+                                 "global_load_dword %2, %6, off\n\tglobal_load_dword %3, %7, off\n\t"
+                                 "s_waitcnt vmcnt(0)"
+                                 : "=&v"(d0), "=&v"(d1), "=&v"(d2), "=&v"(d3)
+                                 : "v"(at(0)), "v"(at(1)), "v"(at(2)), "v"(at(3)) : "memory");
         }
-        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
 #endif
     GEMV_MARK(TW, tslot, 5);
