@@ -43,7 +43,7 @@ __device__ __forceinline__ void route_load(const float* __restrict__ l, int E, R
 
 // One wave (64 lanes) routes one token into registers: lane s < topk holds the s-th pick and its weight, lane topk
 // the shared expert (weight 1). k rounds of a wave-wide max (DPP / permlane, no LDS) whose winner is the lowest id
-// holding it (a ballot per register, lowest set lane).
+// holding it: up to 256 experts over each lane's sorted scores, above that a ballot per register.
 // need_weight == false (uniform over the wave): the picks only, weight left 0 (callers that only need the experts).
 template <int PER>
 __device__ __forceinline__ void route_pick(const RouteIn<PER>& in, const float* __restrict__ l, int E, int topk,
@@ -62,25 +62,75 @@ __device__ __forceinline__ void route_pick(const RouteIn<PER>& in, const float* 
     }
     float my_v = 0.f;                                  // lane s < topk: the s-th pick's logit and id
     int my_e = 0;
-    for (int s = 0; s < topk; ++s) {
-        float lm = v[0];
+    if constexpr (PER <= 4) {
+        // Each lane's PER scores sorted once, highest first (equal scores: lower id first). A round then takes the
+        // wave-wide maximum of the lanes' heads; its lane pops its head. Equal maxima on several lanes (rare) go to
+        // the lowest id among them. The same picks as the scan below, in fewer operations a round.
+        int id[PER];
 #pragma unroll
-        for (int j = 1; j < PER; ++j) lm = max_nn(lm, v[j]);
-        const float best = wave_max_nn(lm);           // scores are finite or -inf
-        int be = 0;
-#pragma unroll
-        for (int j = PER - 1; j >= 0; --j) {           // the lowest register (id block) holding it wins
-            const uint64_t b = __ballot(v[j] == best && j * 64 + lane < E);
-            if (b) be = j * 64 + __builtin_ctzll(b);
+        for (int j = 0; j < PER; ++j) id[j] = j * 64 + lane;
+        auto cx = [&](int a_, int b_) {
+            const bool sw = v[b_] > v[a_] || (v[b_] == v[a_] && id[b_] < id[a_]);
+            const float tv = v[a_];
+            const int ti = id[a_];
+            v[a_] = sw ? v[b_] : v[a_];
+            id[a_] = sw ? id[b_] : id[a_];
+            v[b_] = sw ? tv : v[b_];
+            id[b_] = sw ? ti : id[b_];
+        };
+        if constexpr (PER == 2) cx(0, 1);
+        if constexpr (PER == 4) {
+            cx(0, 1); cx(2, 3); cx(0, 2); cx(1, 3); cx(1, 2);
         }
-        if ((be & 63) == lane) {
+        for (int s = 0; s < topk; ++s) {
+            const float best = wave_max_nn(v[0]);     // scores are finite or -inf
+            const uint64_t c = __ballot(v[0] == best);
+            int w = __builtin_ctzll(c);
+            if (__popcll(c) > 1) {
+                int m = v[0] == best ? id[0] : 0x7fffffff;
+                m = min(m, (int)lane_xor<1>((uint32_t)m));
+                m = min(m, (int)lane_xor<2>((uint32_t)m));
+                m = min(m, (int)lane_xor<4>((uint32_t)m));
+                m = min(m, (int)lane_xor<8>((uint32_t)m));
+                m = min(m, (int)lane_xor<16>((uint32_t)m));
+                m = min(m, (int)lane_xor<32>((uint32_t)m));
+                w = __builtin_ctzll(__ballot(v[0] == best && id[0] == m));
+            }
+            const int be = __builtin_amdgcn_readlane(id[0], w);
+            if (lane == w) {
 #pragma unroll
-            for (int j = 0; j < PER; ++j)
-                if (j == (be >> 6)) v[j] = -__builtin_inff();
+                for (int j = 0; j + 1 < PER; ++j) {
+                    v[j] = v[j + 1];
+                    id[j] = id[j + 1];
+                }
+                v[PER - 1] = -__builtin_inff();
+            }
+            if (lane == s) {
+                my_v = best;
+                my_e = be;
+            }
         }
-        if (lane == s) {
-            my_v = best;
-            my_e = be;
+    } else {
+        for (int s = 0; s < topk; ++s) {
+            float lm = v[0];
+#pragma unroll
+            for (int j = 1; j < PER; ++j) lm = max_nn(lm, v[j]);
+            const float best = wave_max_nn(lm);       // scores are finite or -inf
+            int be = 0;
+#pragma unroll
+            for (int j = PER - 1; j >= 0; --j) {       // the lowest register (id block) holding it wins
+                const uint64_t b = __ballot(v[j] == best && j * 64 + lane < E);
+                if (b) be = j * 64 + __builtin_ctzll(b);
+            }
+            if ((be & 63) == lane) {
+#pragma unroll
+                for (int j = 0; j < PER; ++j)
+                    if (j == (be >> 6)) v[j] = -__builtin_inff();
+            }
+            if (lane == s) {
+                my_v = best;
+                my_e = be;
+            }
         }
     }
     pick = lane < topk ? my_e : shared_id;

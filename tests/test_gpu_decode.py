@@ -315,6 +315,7 @@ def test_route_vs_oracle(gfr, oracle, rows, E, topk):
     lg = torch.randn((rows, E), generator=g)
     lg[0, :] = 0.5                          # all tied: picks 0..k-1
     lg[1, 10:20] = 3.0                      # a tied block on top
+    lg[2, [c for c in (70, 5, 130, 66, 69) if c < E]] = 4.0   # ties across 64-id blocks and lanes
     lg = lg.cuda()
     picks, w = gfr.route(lg, topk)
     torch.cuda.synchronize()
