@@ -310,9 +310,13 @@ __global__ void __launch_bounds__(256) prefill_rot2_kernel(const uint16_t* __res
         for (int q = 0; q < RC; ++q) {
             const int rd = min(r0 + q, nrd - 1);
             const int sl = MATS == 2 ? rd : min(2 * rd + (r4 & 1), exl3_slots - 1);
-            const int e = __shfl(pk, sl, 64);
+            const int e = MATS == 2 ? __builtin_amdgcn_readlane(pk, sl) : __shfl(pk, sl, 64);
             sv[q] = *reinterpret_cast<const uint4*>(suh + (size_t)e * K + k);
         }
+        // keep the chunk's scale loads together: left alone, the compiler sinks each into its round, one memory
+        // round trip a round
+#pragma unroll
+        for (int q = 0; q < RC; ++q) __asm__ volatile("" : "+v"(sv[q].x), "+v"(sv[q].y), "+v"(sv[q].z), "+v"(sv[q].w));
 #pragma unroll
         for (int q = 0; q < RC; ++q) {
             const int rd = r0 + q;
