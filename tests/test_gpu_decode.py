@@ -342,6 +342,44 @@ def test_moe_layer_config5_decode_vs_oracle(gfr, oracle, bits):
     _check_tokens(oracle, w, x, p, wt, m.output[:1].cpu().numpy(), (0,), topk + 1, what=f"config 5 K={bits}")
 
 
+def test_config5_decode_graph_replays_match_eager(gfr):
+    """Config 5's K = 5 layer at bs = 1 (hidden 5120: the gate/up launch's read-ahead of the down matrices takes two
+    loads a lane there) over 4 tokens, captured in one graph and replayed 3 times with eager runs in between: every
+    replay's outputs equal the eager ones bit for bit."""
+    import synth
+    E, D, N, topk, bits, T = 160, 5120, 1536, 8, 5, 4
+    w = synth.experts(E + 1, D, N, bits, seed=70)
+    x = synth.activations(T, D, 71)
+    lg = synth.zipf_logits(T, E, topk, 1.1, 72)
+    m = gfr.Moe(D, N, E, topk, 1)
+    outs = torch.empty(T, D, device="cuda")
+    s = torch.cuda.Stream()
+
+    def run_all():
+        for t in range(T):
+            m.run(w, x[t:t + 1], lg[t:t + 1], 1, stream=s)
+            outs[t].copy_(m.output[0])     # a device copy on the same stream, captured with the layer
+
+    with torch.cuda.stream(s):
+        run_all()
+    s.synchronize()
+    eager = outs.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            run_all()
+    for _ in range(3):
+        with torch.cuda.stream(s):
+            outs.zero_()
+            g.replay()
+        s.synchronize()
+        assert torch.equal(outs, eager)
+        with torch.cuda.stream(s):
+            run_all()
+        s.synchronize()
+        assert torch.equal(outs, eager)
+
+
 def _biased_inputs(rows, E, seed):
     g = torch.Generator(device="cuda").manual_seed(seed)
     logits = torch.randn(rows, E, generator=g, device="cuda")
