@@ -437,6 +437,9 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
 // order. Every sum has a fixed order, and a row's result never depends on the other rows.
 //   a.Kin = intermediate size (the down input), a.N = hidden size; a.suh0 = suh_d, a.svh_g / svh_u the gate / up
 //   output scales, a.t0 the down trellis, a.zgu / SKgu the gate/up partials, a.z = Zd, a.x1 (reused) = svh_d.
+#ifndef GFR_DOWN_HB2_MIN
+#define GFR_DOWN_HB2_MIN 4096   // hidden sizes from which a down workgroup covers two 128-output blocks
+#endif
 #ifndef GFR_DOWN_XCD
 #define GFR_DOWN_XCD 1
 #endif
@@ -454,10 +457,10 @@ __device__ inline void xcd_grouped(int& bx, int& by, int& bz) {
     bz = g / (gy * gx);
 }
 
-template <int K, int RB>
+template <int K, int RB, int HB>
 __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t xs[RB][128];   // the k block's activations, each twice
-    __shared__ float red[4][RB][128];
+    __shared__ float red[4][RB][128 * HB];
     __shared__ float2 psum[4][RB][2][64];                            // each wave's quarter of the gate / up splits
     int bx, hb, kb;
     xcd_grouped(bx, hb, kb);
@@ -489,11 +492,16 @@ __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
         su = *reinterpret_cast<const uint32_t*>(a.svh_u + so);
         sd = *reinterpret_cast<const uint32_t*>(a.suh0 + so);
     }
-    uint32_t wr[2][K];
+    // HB output blocks of 128: the same two k tiles of each (column tiles (hb HB + h) 8 + t); the first block's
+    // words decoded before the barrier, the others' kept as words and decoded after the first block's dots
+    uint32_t wr[HB][2][K];
     {
-        const uint32_t* src = a.t0 + (((size_t)e * KT + kb * 8 + 2 * wave) * NT + hb * 8 + t) * (8 * K) + i * K;
-        load_words<K>(src, wr[0]);
-        load_words<K>(src + (size_t)NT * (8 * K), wr[1]);
+        const uint32_t* src = a.t0 + (((size_t)e * KT + kb * 8 + 2 * wave) * NT + hb * HB * 8 + t) * (8 * K) + i * K;
+#pragma unroll
+        for (int h = 0; h < HB; ++h) {
+            load_words<K>(src + h * 8 * (8 * K), wr[h][0]);
+            load_words<K>(src + (size_t)NT * (8 * K) + h * 8 * (8 * K), wr[h][1]);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     for (int m = 0; m < nr; ++m) {
@@ -554,43 +562,53 @@ __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
         }
     }
     GEMV_MARK(1, tslot, 2);
-    // ---- this wave's two tiles decoded (they wait for their own words only)
+    // ---- this wave's two tiles of the first block decoded (they wait for their own words only)
     uint32_t cw[2][32];
+    auto decode_block = [&](int h) {
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
+        for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
-        for (int j = 0; j < K; ++j) __asm__ volatile("" : "+v"(wr[kk][j]));
-        lane_words<K>(wr[kk], prev_word(wr[kk][K - 1], i), cw[kk]);
-    }
+            for (int j = 0; j < K; ++j) __asm__ volatile("" : "+v"(wr[h][kk][j]));
+            lane_words<K>(wr[h][kk], prev_word(wr[h][kk][K - 1], i), cw[kk]);
+        }
+    };
+    decode_block(0);
     GEMV_MARK(1, tslot, 3);
     __syncthreads();                                     // every member's activations are in LDS
-    float acc[RB][2];
 #pragma unroll
-    for (int m = 0; m < RB; ++m) {
-        acc[m][0] = acc[m][1] = 0.f;
-        if (m < nr) {
+    for (int h = 0; h < HB; ++h) {
+        if (h > 0) decode_block(h);
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                uint32_t xd[16];
-                load_tile_acts(&xs[m][(2 * wave + kk) * 16], xd);
-                tile_dot(cw[kk], xd, acc[m]);
+        for (int m = 0; m < RB; ++m) {
+            if (m < nr) {
+                float acc[2] = {0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    uint32_t xd[16];
+                    load_tile_acts(&xs[m][(2 * wave + kk) * 16], xd);
+                    tile_dot(cw[kk], xd, acc);
+                }
+                red[wave][m][128 * h + 16 * t + i] = acc[0];
+                red[wave][m][128 * h + 16 * t + i + 8] = acc[1];
             }
-            red[wave][m][16 * t + i] = acc[m][0];
-            red[wave][m][16 * t + i + 8] = acc[m][1];
         }
     }
     GEMV_MARK(1, tslot, 4);
     __syncthreads();
-    // ---- the four waves in order, then the down epilogue's transform and scale of this k block's part
-    const uint32_t sv = *reinterpret_cast<const uint32_t*>(a.x1 + (size_t)e * a.N + hb * 128 + 2 * lane);
-    for (int m = wave; m < nr; m += 4) {
+    // ---- the four waves in order, then the down epilogue's transform and scale of this k block's part, a (member,
+    // block) a wave
+    for (int q = wave; q < nr * HB; q += 4) {
+        const int m = q / HB, h = q - m * HB, ob = (hb * HB + h) * 128;
+        const uint32_t sv = *reinterpret_cast<const uint32_t*>(a.x1 + (size_t)e * a.N + ob + 2 * lane);
         float v[2];
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-            v[j] = red[0][m][2 * lane + j] + red[1][m][2 * lane + j] + red[2][m][2 * lane + j] + red[3][m][2 * lane + j];
+        for (int j = 0; j < 2; ++j) {
+            const int c = 128 * h + 2 * lane + j;
+            v[j] = red[0][m][c] + red[1][m][c] + red[2][m][c] + red[3][m][c];
+        }
         fwht128_w64(v, lane);
         const int p = __builtin_amdgcn_readlane(pair_l, (c0 + m) & 63);
-        *reinterpret_cast<float2*>(a.z + ((size_t)kb * a.P + p) * a.N + hb * 128 + 2 * lane) =
+        *reinterpret_cast<float2*>(a.z + ((size_t)kb * a.P + p) * a.N + ob + 2 * lane) =
             make_float2(v[0] * HAD_SCALE * f16_to_f32((uint16_t)sv), v[1] * HAD_SCALE * f16_to_f32((uint16_t)(sv >> 16)));
     }
     GEMV_MARK(1, tslot, 5);
@@ -983,18 +1001,24 @@ hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, int SKgu, 
     a.Kin = N; a.N = D; a.P = P; a.SK = gemv_down_splits(N); a.maxm = maxm; a.slots = slots; a.E = E;
     const int rb = rb_for(rows);
     a.ucap = maxu;
-    const dim3 grid(chunks_x(maxu, rows < maxm ? rows : maxm, rb), D / 128, N / 128);
+    // two 128-output blocks a workgroup at wide outputs (one gate/up epilogue build and one workgroup's setup for
+    // twice the trellis); the sums are the same either way
+    const int hbw = (D / 128) % 2 == 0 && D >= GFR_DOWN_HB2_MIN ? 2 : 1;
+    const dim3 grid(chunks_x(maxu, rows < maxm ? rows : maxm, rb), D / 128 / hbw, N / 128);
+#define GFR_DOWN_HB(KB, HB)                                                                                       \
+    if (rb == 1) down_gemv_kernel<KB, 1, HB><<<grid, 256, 0, s>>>(a);                                               \
+    else if (rb == 2) down_gemv_kernel<KB, 2, HB><<<grid, 256, 0, s>>>(a);                                          \
+    else if (rb == 4) down_gemv_kernel<KB, 4, HB><<<grid, 256, 0, s>>>(a);                                          \
+    else down_gemv_kernel<KB, 8, HB><<<grid, 256, 0, s>>>(a);
 #define GFR_DOWN(KB)                                                                                              \
     case KB:                                                                                                    \
-        if (rb == 1) down_gemv_kernel<KB, 1><<<grid, 256, 0, s>>>(a);                                           \
-        else if (rb == 2) down_gemv_kernel<KB, 2><<<grid, 256, 0, s>>>(a);                                      \
-        else if (rb == 4) down_gemv_kernel<KB, 4><<<grid, 256, 0, s>>>(a);                                      \
-        else down_gemv_kernel<KB, 8><<<grid, 256, 0, s>>>(a);                                                   \
+        if (hbw == 2) { GFR_DOWN_HB(KB, 2) } else { GFR_DOWN_HB(KB, 1) }                                          \
         break;
     switch (bits) {
         GFR_DOWN(2) GFR_DOWN(3) GFR_DOWN(4) GFR_DOWN(5)
         default: return hipErrorInvalidValue;
     }
+#undef GFR_DOWN_HB
 #undef GFR_DOWN
     return hipGetLastError();
 }
