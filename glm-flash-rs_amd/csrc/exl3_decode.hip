@@ -21,6 +21,9 @@
 
 namespace gfr {
 
+#ifndef GFR_SHARED_NOROUTE
+#define GFR_SHARED_NOROUTE 1
+#endif
 #ifndef GFR_GATEUP_PREFETCH
 #define GFR_GATEUP_PREFETCH 1
 #endif
@@ -203,26 +206,33 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
     if constexpr (ROUTE1) {
         if constexpr (XSRC == 1)
             xearly = *reinterpret_cast<const uint32_t*>(a.x0 + (kt0 & ~7) * 16 + 2 * lane);
-        int pick;
-        float weight;
-        // only the wave that publishes the routing needs the weights (the others use the picks)
-        const bool writer = u == 0 && cb == 0 && blockIdx.z == 0 && wave == 0;
-        route_token_regs(a.logits, a.routed, a.slots - 1, a.routed, pick, weight, RouteGate{a.route_bias, a.route_scale},
-                         writer);
-        int rank = 0;                                    // ascending order of the token's slots' experts
-        for (int j = 0; j < a.slots; ++j) rank += __builtin_amdgcn_readlane(pick, j) < pick;
-        const uint64_t mine = __ballot(lane < a.slots && rank == u);
-        if (mine == 0) return;                           // u >= slots: no such expert
-        const int slot = __builtin_ctzll(mine);
-        e = __builtin_amdgcn_readlane(pick, slot);
-        code = lane == 0 ? slot : -1;                    // row 0, this slot
-        if (writer && lane < a.slots) {
-            a.pick_out[lane] = pick;
-            a.weight_out[lane] = weight;
-            a.ids_out[rank] = pick;
-            a.members_out[(size_t)rank * a.maxm] = lane;
-            for (int j = 1; j < a.maxm; ++j) a.members_out[(size_t)rank * a.maxm + j] = -1;
-            if (lane == 0) a.count_out[0] = a.slots;
+        if (GFR_SHARED_NOROUTE && u == a.slots - 1) {
+            // the shared expert (id `routed`, above every routed id, in the last slot) is always the window's last
+            // unit: its waves need no routing and start their trellis stream at once
+            e = a.routed;
+            code = lane == 0 ? a.slots - 1 : -1;
+        } else {
+            int pick;
+            float weight;
+            // only the wave that publishes the routing needs the weights (the others use the picks)
+            const bool writer = u == 0 && cb == 0 && blockIdx.z == 0 && wave == 0;
+            route_token_regs(a.logits, a.routed, a.slots - 1, a.routed, pick, weight,
+                             RouteGate{a.route_bias, a.route_scale}, writer);
+            int rank = 0;                                // ascending order of the token's slots' experts
+            for (int j = 0; j < a.slots; ++j) rank += __builtin_amdgcn_readlane(pick, j) < pick;
+            const uint64_t mine = __ballot(lane < a.slots && rank == u);
+            if (mine == 0) return;                       // u >= slots: no such expert
+            const int slot = __builtin_ctzll(mine);
+            e = __builtin_amdgcn_readlane(pick, slot);
+            code = lane == 0 ? slot : -1;                // row 0, this slot
+            if (writer && lane < a.slots) {
+                a.pick_out[lane] = pick;
+                a.weight_out[lane] = weight;
+                a.ids_out[rank] = pick;
+                a.members_out[(size_t)rank * a.maxm] = lane;
+                for (int j = 1; j < a.maxm; ++j) a.members_out[(size_t)rank * a.maxm + j] = -1;
+                if (lane == 0) a.count_out[0] = a.slots;
+            }
         }
         if (e >= a.E) return;
     } else {
