@@ -6,7 +6,7 @@
  *   FastExperts         src/fast_experts.rs:27-208    -> gfr_fast_experts_*  (prefill chunks)
  *   Moe::run_prefetched src/moe.rs:66-182             -> gfr_moe_*           (router .. combine)
  * The reference binds its kernels through the CUDA driver (src/cuda.rs); a Rust caller binds these functions with
- * `extern "C"` declarations instead (INTEGRATION.md shows the stubs).
+ * `extern "C"` declarations of the prototypes below instead.
  *
  * Conventions (src/cuda.rs:102-123, experts.rs:461-464):
  *   - every function returns 0 on success, a negative GFR_E* code when a precondition fails, or a positive
