@@ -246,6 +246,10 @@ def other_configs(args, copies, stream):
     del graph, moe
     torch.cuda.empty_cache()
 
+    # ---- the shared-expert fork and the routed-expert read hints (shared_expert.rs, l2_prefetch.rs)
+    out["shared_branch_and_hints"] = prefetch_leg(copies, stream)
+    torch.cuda.empty_cache()
+
     # ---- c5: 4 layers, hidden 5120, 160 routed + 1 shared, top-8, K = 2, 3, 4, 5
     D5, N5, E5, K5 = 5120, 1536, 160, 8
     bits5 = (2, 3, 4, 5)
@@ -301,6 +305,79 @@ def other_configs(args, copies, stream):
                      "bytes": nbytes, "seconds": round(secs, 4), "gbs": round(nbytes / secs / 1e9, 3),
                      "hash_tasks_in_flight_max": min(2 * min(16, os.cpu_count() or 1), nchunks)}
     return out
+
+
+def prefetch_leg(copies, stream, reps=8):
+    """The shared-expert fork and the routed-expert read hints of the reference's decode round (shared_expert.rs
+    Branch::run, l2_prefetch.rs Owner::experts + l2pf.cu), at config 2's shape for one token: group the routed token,
+    then the shared expert's work (a bf16 stand-in of its gate/up and down products, 6.3 MB each, in place of the
+    reference's FP8 branch) and the routed experts (ExpertGpu, 4 EXL3 slots). Three forms, each a graph of 64 steps
+    over the 16 cold weight copies, timed alternately:
+      serial   shared work, then the routed experts, on one stream;
+      branch   the shared work on a forked stream (gfr_moe.SharedBranch), joined after the routed experts;
+      hinted   serial, plus the hint of the routed experts' gate/up heads forked onto a side stream right after the
+               grouping (gfr_moe.Prefetch) and joined at the end."""
+    import torch
+    import gfr_moe
+    import synth
+    rows, R = 1, 16
+    g = gfr_moe.Grouping(E + 1, SLOTS, rows)
+    ex = gfr_moe.ExpertGpu(D, N, SLOTS, TOPK, rows)
+    pf = gfr_moe.Prefetch()
+    br = gfr_moe.SharedBranch()
+    stride = copies[0].gt[0].numel() * 4
+    T = gfr_moe.PfTensor
+    for k, w in enumerate(copies):
+        pf.add_experts(k, gfr_moe.pf_experts(T(w.gt.data_ptr(), E * stride), T(w.ut.data_ptr(), E * stride), E))
+    plan = pf.expert_plans[0][1]
+    xs = synth.activations(R, D, 951)
+    picks, _ = gfr_moe.route(synth.logits(R, E, 952), TOPK)
+    wgu = (torch.randn(D, 2 * N, device="cuda") * 0.02).to(torch.bfloat16)
+    wd = (torch.randn(N, D, device="cuda") * 0.02).to(torch.bfloat16)
+    shared = torch.empty(rows, D, device="cuda", dtype=torch.bfloat16)
+
+    def step(j, form):
+        def f():
+            c, r = j % len(copies), j % R
+            p = picks[r:r + 1]
+
+            def shared_fn(st=None):
+                h = torch.matmul(xs[r:r + 1], wgu)
+                torch.matmul(h[:, :N], wd, out=shared)
+
+            def routed(ready=None):
+                ex.run_rows(copies[c], xs[r:r + 1], p, g.ids, g.count, g.members, rows, rows, stream=stream)
+
+            g.run(p, rows, stream=stream)
+            if form == "branch":
+                br.run(stream, shared_fn, routed)
+                return
+            if form == "hinted":
+                pf.experts(stream, c, rows, g.ids, g.count)
+            shared_fn()
+            routed()
+            if form == "hinted":
+                pf.join(stream)
+        return f
+
+    forms = ("serial", "branch", "hinted")
+    with torch.cuda.stream(stream):            # library handles (hipBLASLt) are created outside the capture
+        for form in forms:
+            step(0, form)()
+    stream.synchronize()
+    glen = 4 * len(copies)
+    graphs = {form: graph_of([step(j, form) for j in range(glen)], stream) for form in forms}
+    us = {form: [] for form in forms}
+    for form in forms:
+        time_graphs([graphs[form]] * 2, stream)
+    for _ in range(reps):
+        for form in forms:
+            us[form].append(time_graphs([graphs[form]] * 4, stream) / (4 * glen) * 1e6)
+    med = {k: round(sorted(v)[len(v) // 2], 3) for k, v in us.items()}
+    return {"config": "config 2 shape, one token: grouping, shared-expert stand-in (bf16 gate/up + down products, "
+                      "12.6 MB), routed experts (ExpertGpu, 4 EXL3 slots); 16 cold weight copies",
+            "us_per_step_serial": med["serial"], "us_per_step_shared_branch": med["branch"],
+            "us_per_step_hinted": med["hinted"], "hint_bytes_per_step": 2 * TOPK * plan.bytes}
 
 
 def _zipf_logits_gpu(rows, E, topk, s, seed):

@@ -88,6 +88,11 @@ def _load() -> ctypes.CDLL:
         "gfr_prepared_experts": ([VP, I, ctypes.POINTER(_Exl3Struct)], I),
         "gfr_prepared_destroy": ([VP], I),
         "gfr_sha256_hex": ([P, ctypes.c_uint64, ctypes.c_char_p], I),
+        "gfr_prefetch_abi": ([], ctypes.c_uint32),
+        "gfr_prefetch_properties": ([ctypes.POINTER(I), ctypes.POINTER(I)], I),
+        "gfr_prefetch_capturing": ([P, ctypes.POINTER(I)], I),
+        "gfr_prefetch_segments": ([P, I, I, P], I),
+        "gfr_prefetch_experts": ([P, P, I, P, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, I, P], I),
         "gfr_tensor_extent": ([ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64), I, I,
                                ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)], I),
     }
@@ -362,6 +367,203 @@ class SharedBranch:
             routed_fn(self.joined)
         finally:
             main.wait_event(self.joined)
+
+
+# ---- Cache-warming read hints (src/l2_prefetch_plan.rs, src/l2_prefetch.rs; kernels in csrc/prefetch.hip) -------
+# The plan functions restate the reference's host policy (same constants, bounds and rounding), so a caller that
+# plans with them gets the spans the reference would plan; a failed bound raises ValueError where the reference's
+# ensure! returns an error.
+PF_ALIGN = 16
+PF_BUDGET = 8 << 20
+PF_L2_FALLBACK = 24 << 20
+PF_EXPERT_BYTES = 64 << 10
+PF_MAX_ROWS = 64
+PF_CHUNK = 32 << 10         # the reference's bulk-prefetch piece: one instruction a 32 KiB chunk
+PF_THREADS = 128
+PF_LINE_CHUNK = 2 << 10     # a thread's share here: 16 lines of 128 bytes, one dword load a line
+
+
+@dataclass(frozen=True)
+class PfTensor:
+    """A weight tensor's device range (l2_prefetch_plan.rs Tensor)."""
+    address: int
+    bytes: int
+    contiguous: bool = True
+
+
+@dataclass(frozen=True)
+class PfSpan:
+    address: int
+    bytes: int
+
+
+@dataclass(frozen=True)
+class ExpertPlan:
+    bases: tuple
+    stride: int
+    bytes: int
+    experts: int
+
+
+def _pf_ensure(ok, msg):
+    if not ok:
+        raise ValueError(msg)
+
+
+def pf_budget(l2_bytes: int) -> int:
+    """Bytes a site may hint: half the L2, at most 8 MiB (l2_prefetch_plan.rs:80-82)."""
+    return min(PF_BUDGET, (PF_L2_FALLBACK if l2_bytes == 0 else l2_bytes) // 2)
+
+
+def pf_rows_enabled(rows: int) -> bool:
+    """Hints are for decode rounds only: 1..64 rows (l2_prefetch_plan.rs:83-85)."""
+    return 0 < rows <= PF_MAX_ROWS
+
+
+def pf_grid(nbytes: int, cus: int, chunk: int = PF_CHUNK) -> int:
+    """Workgroups of a segment launch: one thread a chunk, 128 threads a workgroup, 1..cus (l2_prefetch_plan.rs:86-92;
+    the default chunk is the reference's, Prefetch passes PF_LINE_CHUNK for this library's line reads)."""
+    _pf_ensure(0 < nbytes <= PF_BUDGET and cus > 0, "L2 segment grid bounds")
+    pieces = -(-nbytes // chunk)
+    return max(1, min(cus, -(-pieces // PF_THREADS)))
+
+
+def pf_expert_grid(rows: int, experts: int, capacity: int, cus: int):
+    """(maxu, grid) of an expert hint: the window's min(rows * 8, experts) routed experts plus the shared slot, one
+    workgroup an expert up to the CU count (l2_prefetch_plan.rs:93-111)."""
+    _pf_ensure(pf_rows_enabled(rows) and experts > 0 and cus > 0, "L2 expert grid policy")
+    maxu = min(rows * 8, experts) + 1
+    _pf_ensure(maxu <= capacity and maxu <= 2 ** 31 - 1, "L2 expert group capacity")
+    return maxu, min(cus, maxu)
+
+
+def pf_span(t: PfTensor, left: int):
+    """The 16-byte aligned part of a tensor that fits in `left` bytes, or None (l2_prefetch_plan.rs Tensor::span)."""
+    if not t.contiguous or t.bytes == 0 or left < PF_ALIGN:
+        return None
+    _pf_ensure(t.address != 0, "null L2 prefetch address")
+    end = t.address + t.bytes
+    _pf_ensure(end < 2 ** 64, "L2 tensor extent overflow")
+    _pf_ensure(t.address + PF_ALIGN - 1 < 2 ** 64, "L2 alignment overflow")
+    address = (t.address + PF_ALIGN - 1) // PF_ALIGN * PF_ALIGN
+    n = min(left, max(0, end - address)) // PF_ALIGN * PF_ALIGN
+    return PfSpan(address, n) if n > 0 else None
+
+
+def pf_take(items, budget: int):
+    """Spans of the items in order until the budget is spent (l2_prefetch_plan.rs take, without its test-only Q4
+    item). An item is a PfTensor, or a (scale, weight) pair of PfTensors: the scales first."""
+    _pf_ensure(0 < budget <= PF_BUDGET, "L2 site budget bound")
+    spans, left = [], budget
+    for it in items:
+        if left < PF_ALIGN:
+            break
+        for t in (it if isinstance(it, tuple) else (it,)):
+            sp = pf_span(t, left)
+            if sp is not None:
+                left -= sp.bytes
+                spans.append(sp)
+    return spans
+
+
+def pf_experts(gate: PfTensor, up: PfTensor, count: int):
+    """The routed-expert hint of one layer: the first min(64 KiB, stride) bytes of each expert in the gate and up
+    trellis tensors, or None when the layout does not allow it (l2_prefetch_plan.rs:183-219)."""
+    if count == 0 or gate.bytes != up.bytes or not gate.contiguous or not up.contiguous or gate.bytes % count:
+        return None
+    stride = gate.bytes // count
+    n = min(PF_EXPERT_BYTES, stride) // PF_ALIGN * PF_ALIGN
+    if n == 0 or stride % PF_ALIGN or gate.address % PF_ALIGN or up.address % PF_ALIGN:
+        return None
+    _pf_ensure(gate.address != 0 and up.address != 0, "null L2 expert address")
+    _pf_ensure(gate.address + gate.bytes < 2 ** 64 and up.address + up.bytes < 2 ** 64, "L2 expert extent overflow")
+    _pf_ensure(count < 2 ** 63 and stride < 2 ** 63, "L2 expert launch bounds")
+    return ExpertPlan((gate.address, up.address), stride, n, count)
+
+
+def prefetch_properties():
+    """(CU count, L2 bytes) of the current device (gfr_prefetch_properties)."""
+    cus, l2 = ctypes.c_int(), ctypes.c_int()
+    _check(lib().gfr_prefetch_properties(ctypes.byref(cus), ctypes.byref(l2)))
+    return cus.value, l2.value
+
+
+def prefetch_capturing(stream) -> bool:
+    active = ctypes.c_int()
+    _check(lib().gfr_prefetch_capturing(_stream(stream), ctypes.byref(active)))
+    return active.value == 1
+
+
+class Prefetch:
+    """Side-stream read hints (src/l2_prefetch.rs Owner:214-407, the per-layer tables without the model's attention
+    sites): segment tables and routed-expert plans registered once (device tables allocated here, at setup), then
+    mark / experts fork a side stream from `main` and launch the read kernels on it, and join(main) makes main wait
+    for them. The kernels write nothing, so a hint never changes a result. The weights, tables and ids must stay
+    alive until the join; under capture, a fork and a join must both fall in the same capture (as the reference's)."""
+
+    def __init__(self, device="cuda"):
+        self.device = torch.device(device)
+        self.cus, self.l2 = prefetch_properties()
+        _pf_ensure(lib().gfr_prefetch_abi() == 1, "prefetch ABI mismatch")
+        self.budget = pf_budget(self.l2)
+        self.side = torch.cuda.Stream(self.device)
+        self.fork_ev = torch.cuda.Event()
+        self.joined = torch.cuda.Event()
+        self.tables = {}
+        self.expert_plans = {}
+        self.pending = False
+        self.captured = False
+        self.stats = {"launches": 0, "expert_launches": 0, "skipped_rows": 0, "bytes_planned": 0}
+
+    def add_segments(self, key, spans):
+        _pf_ensure(0 < len(spans) < 2 ** 31, "L2 span table bounds")
+        total = sum(sp.bytes for sp in spans)
+        table = torch.tensor([[sp.address, sp.bytes] for sp in spans], dtype=torch.int64, device=self.device)
+        self.tables[key] = (table, len(spans), pf_grid(total, self.cus, PF_LINE_CHUNK))
+        self.stats["bytes_planned"] += total
+
+    def add_experts(self, layer, plan: ExpertPlan):
+        bases = torch.tensor(list(plan.bases), dtype=torch.int64, device=self.device)
+        self.expert_plans[layer] = (bases, plan)
+
+    def _fork(self, main):
+        capture = prefetch_capturing(main)
+        if self.pending and capture != self.captured:
+            self.pending = False
+        self.fork_ev.record(main)
+        self.side.wait_event(self.fork_ev)
+        self.captured = capture
+        self.pending = True
+
+    def mark(self, main, key, rows: int):
+        if not pf_rows_enabled(rows):
+            self.stats["skipped_rows"] += 1
+            return
+        if key not in self.tables:
+            return
+        table, n, grid = self.tables[key]
+        self._fork(main)
+        _check(lib().gfr_prefetch_segments(_ptr(table), n, grid, _stream(self.side)))
+        self.stats["launches"] += 1
+
+    def experts(self, main, layer, rows: int, ids: torch.Tensor, count: torch.Tensor):
+        """Call right after grouped routing (ids / count: the grouping's device output), before the shared expert."""
+        if not pf_rows_enabled(rows) or layer not in self.expert_plans:
+            return
+        _pf_ensure(ids.dtype == torch.int32 and ids.numel() > 0 and count.numel() >= 1, "L2 routing buffer bounds")
+        bases, plan = self.expert_plans[layer]
+        maxu, grid = pf_expert_grid(rows, plan.experts, ids.numel(), self.cus)
+        self._fork(main)
+        _check(lib().gfr_prefetch_experts(_ptr(ids), _ptr(count), maxu, _ptr(bases), plan.stride, plan.bytes,
+                                          plan.experts, grid, _stream(self.side)))
+        self.stats["expert_launches"] += 1
+
+    def join(self, main):
+        if self.pending:
+            if prefetch_capturing(main) == self.captured:
+                self.joined.record(self.side)
+                main.wait_event(self.joined)
+            self.pending = False
 
 
 class Linear(_Engine):

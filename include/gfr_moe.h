@@ -203,6 +203,31 @@ int gfr_exl3_rotate(hipStream_t stream, const uint16_t* x, int x_stride, int x_f
 /* ---- Debug / parity: decoded fp16 weights of one matrix [kin][n] (row = k), bit-exact to experts.rs:47-74 ---- */
 int gfr_exl3_decode_tiles(hipStream_t stream, const uint32_t* trellis, int kin, int n, int bits, uint16_t* out);
 
+/* ---- Cache-warming reads of weight memory (native/l2-prefetch/bridge.cpp:11-45, l2pf.cu) ----------------------
+ * Read hints only: the kernels load one dword of every 128-byte line of the given ranges and write nothing, so no
+ * result can change. On MI355X a line read lands in the reading XCD's L2 and in the 256 MB memory-side cache, from
+ * which the expert launches on every XCD then read it. Meant for a side stream forked from the caller's main stream
+ * right after grouped routing (the reference's l2_prefetch.rs Owner::experts), joined before the routed experts'
+ * results are needed; nothing here synchronises or allocates, so the launches can be captured into a graph.
+ * Preconditions return GFR_EINVAL where the reference returns cudaErrorInvalidValue. */
+#define GFR_PREFETCH_EXPERT_BYTES_MAX 65536
+uint32_t gfr_prefetch_abi(void);                                     /* alaska_l2pf_abi, bridge.cpp:11: 1 */
+/* alaska_l2pf_properties, bridge.cpp:12-20: the current device's CU count and L2 size in bytes (one XCD's L2). */
+int gfr_prefetch_properties(int* cus, int* l2_bytes);
+/* alaska_l2pf_capturing, bridge.cpp:21-29: *active = 1 while the stream is being captured; an invalidated capture
+ * returns hipErrorStreamCaptureInvalidated. */
+int gfr_prefetch_capturing(hipStream_t stream, int* active);
+/* alaska_l2pf_segments, bridge.cpp:30-35: table = device array of count (address, bytes) int64 pairs, each
+ * 16-byte aligned with bytes a positive multiple of 16 (entries that are not are skipped); grid workgroups of 128
+ * threads, segment s starting at thread s of the grid. */
+int gfr_prefetch_segments(const int64_t* table, int count, int grid, hipStream_t stream);
+/* alaska_l2pf_experts, bridge.cpp:36-45: for u < min(*count, maxu) (device values), the first `bytes` of expert
+ * ids[u] in the gate and up trellis tensors bases[0] and bases[1] (device array of 2 addresses), at
+ * bases[m] + ids[u] * stride; ids outside [0, experts) are skipped. bytes in (0, min(stride,
+ * GFR_PREFETCH_EXPERT_BYTES_MAX)], bytes and stride multiples of 16, grid > 0. */
+int gfr_prefetch_experts(const int32_t* ids, const int32_t* count, int maxu, const int64_t* bases, int64_t stride,
+                         int64_t bytes, int64_t experts, int grid, hipStream_t stream);
+
 /* ---- Prepared weights (src/prepared.rs) ------------------------------------------------------------------------
  * The reference's prepared format: a JSON manifest {format: 1, file_size, chunk, chunk_sha256[], storages[], tree,
  * key} next to data.bin (prepared.rs:15-40). Tensor paths are the reference's ("weights.layers[3].moe.experts.gt").
