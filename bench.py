@@ -460,7 +460,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--copies", type=int, default=16)
     ap.add_argument("--routings", type=int, default=64)
-    ap.add_argument("--cpu-tokens", type=int, default=6)
+    ap.add_argument("--cpu-tokens", type=int, default=12)
     ap.add_argument("--cpu-threads", type=int, default=16, help="threads of the all-cores CPU baseline (capped "
                     "at the cores this process may use)")
     ap.add_argument("--no-cpu", action="store_true")
