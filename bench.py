@@ -472,6 +472,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary config 1 / 3 / 5 lines")
     ap.add_argument("--extra-launches", type=int, default=4096)
     ap.add_argument("--c5-prefill-rows", type=int, default=16384)
+    ap.add_argument("--hints-only", action="store_true", help="run only the shared-expert fork / read-hint leg "
+                    "and print its JSON (for a kernel trace of it)")
     ap.add_argument("--counter-summary", metavar="CSV", help="print per-kernel counter averages of a rocprofv3 "
                     "counter_collection.csv and exit (no GPU work)")
     args = ap.parse_args()
@@ -482,6 +484,12 @@ def main():
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.hints_only:
+        import torch
+        import synth
+        copies = [synth.experts(E + 1, D, N, BITS, seed=1000 + 17 * c) for c in range(args.copies)]
+        print(json.dumps(prefetch_leg(copies, torch.cuda.Stream())), flush=True)
+        return
     if args.calibrate_copy:
         calibrate_copy()
     secs, copies, xs, logits, stream, launches_us = decode_bench(args)

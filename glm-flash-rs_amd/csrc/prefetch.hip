@@ -23,46 +23,63 @@ int set_error(int code, const std::string& msg);   // gfr_moe_api.hip (the threa
 
 constexpr uint64_t PF_LINE = 128;
 
-// One dword of each 128-byte line of [p, p + bytes) for lines first, first + stride, ...; four lines a lane in flight
-// (the lines past the end of a group re-read the group's first line). p is 16-byte aligned and bytes a multiple of 16.
-__device__ __forceinline__ void touch_lines(const uint8_t* p, uint64_t bytes, uint64_t first, uint64_t stride) {
-    const uint64_t lines = (bytes + PF_LINE - 1) / PF_LINE;
-    for (uint64_t i = first; i < lines; i += 4 * stride) {
-        const uint8_t* a[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint64_t l = i + k * stride;
-            a[k] = p + (l < lines ? l : i) * PF_LINE;
-        }
-        uint32_t d0, d1, d2, d3;
-        __asm__ volatile("global_load_dword %0, %4, off\n\tglobal_load_dword %1, %5, off\n\t"
-                         "global_load_dword %2, %6, off\n\tglobal_load_dword %3, %7, off\n\t"
-                         "s_waitcnt vmcnt(0)"
-                         : "=&v"(d0), "=&v"(d1), "=&v"(d2), "=&v"(d3)
-                         : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3])
-                         : "memory");
-    }
+// Four line reads of one lane, issued together and waited for together (one memory round trip). The loaded registers
+// are never read; the outputs are early-clobber so that no register the compiler allocates (an address of the next
+// batch) can be written by a load still in flight.
+__device__ __forceinline__ void touch4(const uint8_t* a0, const uint8_t* a1, const uint8_t* a2, const uint8_t* a3) {
+    uint32_t d0, d1, d2, d3;
+    __asm__ volatile("global_load_dword %0, %4, off\n\tglobal_load_dword %1, %5, off\n\t"
+                     "global_load_dword %2, %6, off\n\tglobal_load_dword %3, %7, off\n\t"
+                     "s_waitcnt vmcnt(0)"
+                     : "=&v"(d0), "=&v"(d1), "=&v"(d2), "=&v"(d3)
+                     : "v"(a0), "v"(a1), "v"(a2), "v"(a3)
+                     : "memory");
 }
 
-// table: n pairs of int64 (device address, bytes). Segment s starts at thread s mod the grid, so a table of many
-// one-line segments spreads over the threads (l2pf.cu:58-70). Entries that are not 16-byte aligned, or empty, are
-// skipped (the reference's host plan never produces them).
+// A lane's line addresses, gathered over every range before any is read: four make one round trip, whichever
+// ranges they come from (a lane waits once per four lines, not once per range). A partial batch repeats its first
+// address.
+struct LineBatch {
+    const uint8_t* a[4];
+    int n = 0;
+    __device__ __forceinline__ void add(const uint8_t* p) {
+        a[n++] = p;
+        if (n == 4) {
+            touch4(a[0], a[1], a[2], a[3]);
+            n = 0;
+        }
+    }
+    __device__ __forceinline__ void flush() {
+        if (n == 0) return;
+        for (int k = n; k < 4; ++k) a[k] = a[0];
+        touch4(a[0], a[1], a[2], a[3]);
+        n = 0;
+    }
+};
+
+// table: n pairs of int64 (device address, bytes). The ranges' 128-byte lines are numbered in table order and
+// thread t of the grid reads lines t, t + threads, ... (one dword a line). Entries that are not 16-byte aligned, or
+// empty, are skipped (the reference's host plan never produces them). l2pf.cu:58-70 instead hands each segment to
+// every thread in turn, which here would cost one round trip a segment.
 __global__ void __launch_bounds__(256) prefetch_segments_kernel(const int64_t* __restrict__ table, int n) {
     const uint64_t index = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    LineBatch lb;
+    uint64_t pos = index, start = 0;                   // this thread's next line, the current range's first line
     for (int s = 0; s < n; ++s) {
         const uint64_t addr = (uint64_t)table[2 * s];
         const int64_t bytes = table[2 * s + 1];
         if (addr == 0 || (addr & 15) || bytes <= 0 || (bytes & 15)) continue;
-        const uint64_t first = (index + stride - (uint64_t)s % stride) % stride;
-        touch_lines(reinterpret_cast<const uint8_t*>(addr), (uint64_t)bytes, first, stride);
+        const uint64_t lines = ((uint64_t)bytes + PF_LINE - 1) / PF_LINE;
+        for (; pos < start + lines; pos += stride) lb.add(reinterpret_cast<const uint8_t*>(addr) + (pos - start) * PF_LINE);
+        start += lines;
     }
+    lb.flush();
 }
 
-// The first `bytes` of expert ids[u] in each of the two matrices, for u < min(count[0], maxu): the (u, matrix) ranges
-// are segments spread over the whole grid as in the segment kernel (range s starts at thread s), so a few experts
-// still use every workgroup; ids outside [0, experts) are skipped, so no read leaves the expert tensors
-// (l2pf.cu:72-88 gives each expert one block; the work is the same).
+// The first `bytes` of expert ids[u] in each of the two matrices, for u < min(count[0], maxu): the ranges
+// (u, matrix) are numbered u-major and their lines read as in the segment kernel; ids outside [0, experts) are
+// skipped, so no read leaves the expert tensors (l2pf.cu:72-88 gives each expert one block instead).
 __global__ void __launch_bounds__(256) prefetch_experts_kernel(const int32_t* __restrict__ ids,
                                                               const int32_t* __restrict__ count, int maxu,
                                                               const int64_t* __restrict__ bases, int64_t stride,
@@ -70,12 +87,15 @@ __global__ void __launch_bounds__(256) prefetch_experts_kernel(const int32_t* __
     const uint64_t index = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const uint64_t nthreads = (uint64_t)gridDim.x * blockDim.x;
     const int c = *count, n = c < maxu ? c : maxu;
-    for (int s = 0; s < 2 * n; ++s) {
+    const uint64_t lines = ((uint64_t)bytes + PF_LINE - 1) / PF_LINE;
+    LineBatch lb;
+    for (uint64_t pos = index; pos < 2 * (uint64_t)n * lines; pos += nthreads) {
+        const uint64_t s = pos / lines, l = pos - s * lines;
         const int64_t e = ids[s >> 1];
         if (e < 0 || e >= experts) continue;
-        const uint8_t* p = reinterpret_cast<const uint8_t*>((uint64_t)bases[s & 1]) + e * stride;
-        touch_lines(p, (uint64_t)bytes, (index + nthreads - (uint64_t)s % nthreads) % nthreads, nthreads);
+        lb.add(reinterpret_cast<const uint8_t*>((uint64_t)bases[s & 1]) + e * stride + l * PF_LINE);
     }
+    lb.flush();
 }
 
 }  // namespace gfr
