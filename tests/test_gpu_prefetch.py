@@ -138,3 +138,31 @@ def test_hints_in_a_captured_graph(gfr):
     cus, l2 = gfr.prefetch_properties()
     assert cus > 0 and l2 > 0
     assert not gfr.prefetch_capturing(s)
+
+
+def _bytesum(t):
+    return t.contiguous().view(torch.uint8).sum(dtype=torch.int64).item()
+
+
+def test_many_segments_write_nothing(gfr):
+    """A table of many short ranges (the reference plans up to 130 heads of 8,176 bytes for one matrix,
+    l2_prefetch_plan.rs tests) over the down trellis, then the scales with what is left of a 1 MiB budget: launches
+    at several grid sizes leave the weights unchanged."""
+    w, _, _ = _setup(gfr, 1, 431)
+    T = gfr.PfTensor
+    base = w.dt.data_ptr()
+    heads = [T(base + k * 65536, 8176) for k in range(128)]
+    spans = gfr.pf_take(heads + [(T(w.svh_d.data_ptr(), w.svh_d.numel() * 2), T(w.suh_d.data_ptr(), w.suh_d.numel() * 2))],
+                        1 << 20)
+    assert len(spans) == 129 and spans[-1] == gfr.PfSpan(w.svh_d.data_ptr(), (1 << 20) - 128 * 8176)
+    before = [_bytesum(t) for t in (w.dt, w.svh_d, w.suh_d)]
+    pf = gfr.Prefetch()
+    pf.add_segments("heads", spans)
+    s = torch.cuda.Stream()
+    table, n, _ = pf.tables["heads"]
+    for grid in (1, 7, 256):
+        gfr._check(gfr.lib().gfr_prefetch_segments(table.data_ptr(), n, grid, s.cuda_stream))
+    pf.mark(s, "heads", 1)
+    pf.join(s)
+    s.synchronize()
+    assert [_bytesum(t) for t in (w.dt, w.svh_d, w.suh_d)] == before
