@@ -11,7 +11,7 @@
 // Two device entry points, as the reference's:
 //   segments  a table of (address, bytes) pairs in device memory (a host-planned list of the next kernels' weights)
 //   experts   device-indexed: the first `bytes` of every routed expert of a grouping (ids[0 .. count)) in the gate and
-//             up trellis tensors (bases[0], bases[1] + id * stride), with no host round trip, so it can be captured
+//             up trellis tensors (at bases[m] + id * stride, m = 0, 1), with no host round trip, so it can be captured
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <string>
