@@ -49,18 +49,34 @@ def graph_of(fn_steps, stream):
     return g
 
 
-def time_graphs(plan, stream):
-    """plan: list of graphs replayed in order; returns seconds between HIP events recorded on `stream`."""
+def time_graphs(plan, stream, lead=()):
+    """plan: list of graphs replayed in order; returns seconds between HIP events recorded on `stream`. lead: graphs
+    replayed (untimed) right before the start event with no synchronisation in between, so that the GPU is still
+    busy while the host submits the timed replays (no host-launch gap at the start of a short timed region)."""
     import torch
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):          # a graph replays on the current stream: time on that stream
+        for g in lead:
+            g.replay()
         start.record(stream)
         for g in plan:
             g.replay()
         end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end) / 1e3
+
+
+def ramp(graph, stream, seconds):
+    """Untimed replays of `graph` for at least `seconds` of wall time: the GPU's clocks reach their steady state under
+    back-to-back work (the first tens of ms of a layer loop run measurably slower on MI355X)."""
+    import torch
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        while time.perf_counter() - t0 < seconds:
+            for _ in range(8):
+                graph.replay()
+            stream.synchronize()
 
 
 def replay_plan(steps, glen, full, rest):
@@ -72,9 +88,11 @@ def replay_plan(steps, glen, full, rest):
 
 def decode_bench(args):
     """Config 2: `args.steps` bs=1 layer steps as graph replays. Step j uses weight copy j % copies and routing
-    j % routings; the warm-up replays steps from the middle of the cycle, so the timed replay does not start on the
-    copies it just touched. Also times the layer's first launch alone and its first two launches (the same steps,
-    gfr_moe_set_launches), which gives each launch's share of a step inside the layer's own sequence."""
+    j % routings. Before each timed replay: `--warmup` steps plus a fixed-time clock ramp (`--ramp-ms` of replays,
+    whatever --warmup is), both on routings the timed steps do not use, so the timed replay does not start on weights
+    it just touched; the last warm replay is still running when the timed replay is submitted. Also times the
+    layer's first launch alone and its first two launches (the same steps, gfr_moe_set_launches), which gives each
+    launch's share of a step inside the layer's own sequence."""
     import torch
     import gfr_moe
     import synth
@@ -86,9 +104,9 @@ def decode_bench(args):
     moe = gfr_moe.Moe(D, N, E, TOPK, 1)
     glen = min(args.steps, 8 * args.copies)
 
-    def step(j):
-        return lambda: moe.run(copies[j % len(copies)], xs[j % R:j % R + 1], logits[j % R:j % R + 1], 1,
-                               stream=stream)
+    def step(j, r=None):
+        r = j % R if r is None else r % R
+        return lambda: moe.run(copies[j % len(copies)], xs[r:r + 1], logits[r:r + 1], 1, stream=stream)
 
     with torch.cuda.stream(stream):
         for j in range(len(copies)):
@@ -100,10 +118,12 @@ def decode_bench(args):
         moe.set_launches(launches)
         full = graph_of([step(j) for j in range(glen)], stream)
         rest = graph_of([step(j) for j in range(args.steps % glen)], stream) if args.steps % glen else None
+        # warm steps: copies from the middle of the cycle, routings past the ones the timed steps use
         nw = max(args.warmup, 1)
-        warm = graph_of([step(warm0 + j) for j in range(min(nw, glen))], stream)
-        time_graphs([warm] * max(nw // glen, 1), stream)
-        per_launch[launches] = time_graphs(replay_plan(args.steps, glen, full, rest), stream)
+        warm = graph_of([step(warm0 + j, glen + j) for j in range(min(nw, glen))], stream)
+        ramp(warm, stream, args.ramp_ms / 1e3)
+        per_launch[launches] = time_graphs(replay_plan(args.steps, glen, full, rest), stream,
+                                           lead=[warm] * max(nw // glen, 4))
         del full, rest, warm
     moe.set_launches(0)
     secs = per_launch[0]
@@ -421,6 +441,7 @@ def cpu_baseline(args, copies, xs, logits):
 
     total = sum(token(t) for t in range(args.cpu_tokens))
     one = {"value": round(args.cpu_tokens / total, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+           "cpu_model": cpu_model(),
            "sample": f"{args.cpu_tokens} tokens of config 2: per token the 5 experts' gate/up/down trellis decode "
                      f"+ fixed-order fp32 matvec + epilogues (oracle/gfr_oracle.c, scalar, 1 thread)",
            "seconds": round(total, 2)}
@@ -432,8 +453,72 @@ def cpu_baseline(args, copies, xs, logits):
         list(ex.map(token, range(threads)))
     wall = time.perf_counter() - t0
     many = {"value": round(threads / wall, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{threads} tokens of config 2 at once, one a thread, same scalar C path", "seconds": round(wall, 2)}
     return one, many
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline_c1(tokens=16):
+    """Config 1 on the host: per token the 2048 x 1536 K = 4 trellis decoded (gfro_unpack_f32) and the linear
+    (gfro_linear: input scales, transform, fixed-order fp32 matvec, output transform and scales), scalar C, 1 thread,
+    on seeded weights and fp16 tokens of the config's shape."""
+    import numpy as np
+    import oracle
+    kin, n = 2048, 1536
+    rng = np.random.default_rng(5)
+    words = rng.integers(0, 2 ** 32, (kin // 16, n // 16, 8 * BITS), dtype=np.uint64).astype(np.uint32)
+    sc = lambda k: ((rng.integers(0, 2, k) * 2 - 1) * (rng.random(k) + 0.5)).astype(np.float16).view(np.uint16)
+    suh, svh = sc(kin), sc(n)
+    xs = rng.standard_normal((tokens, kin)).astype(np.float16).view(np.uint16)
+    t0 = time.perf_counter()
+    for t in range(tokens):
+        oracle.linear(xs[t], oracle.unpack_f32(words, kin, n, BITS), suh, svh)
+    secs = time.perf_counter() - t0
+    return {"value": round(tokens / secs, 3), "unit": "tok/s", "cores": 1, "kind": "port", "cpu_model": cpu_model(),
+            "sample": f"{tokens} tokens of config 1: per token the trellis decode + linear (oracle/gfr_oracle.c, "
+                      "scalar, 1 thread)", "seconds": round(secs, 2)}
+
+
+def cpu_baseline_c3(copies, rows=32):
+    """Config 3 on the host, row-batched: one 32-token Zipf(1.1) window; each distinct expert's trellis decoded once
+    (gfro_unpack_f32), then every member row through it (gfro_expert_row: rotation, fixed-order fp32 matvecs,
+    epilogues), then the combine; scalar C, 1 thread."""
+    import numpy as np
+    import oracle
+    import synth
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from refs import np_u16, np_u32
+    w = copies[0]
+    x = np_u16(synth.activations(rows, D, 961))
+    picks, weights = oracle.route(synth.zipf_logits(rows, E, TOPK, 1.1, 962).cpu().numpy(), TOPK, E)
+    used = sorted(set(int(e) for e in picks.reshape(-1)))
+    words = {e: (np_u32(w.gt[e]), np_u32(w.ut[e]), np_u32(w.dt[e])) for e in used}
+    vec = {nm: np_u16(getattr(w, nm)) for nm in ("suh_g", "suh_u", "suh_d", "svh_g", "svh_u", "svh_d")}
+    y = np.empty((rows, SLOTS, D), np.float32)
+    t0 = time.perf_counter()
+    for e in used:
+        wg, wu, wd = (oracle.unpack_f32(words[e][0], D, N, BITS), oracle.unpack_f32(words[e][1], D, N, BITS),
+                      oracle.unpack_f32(words[e][2], N, D, BITS))
+        for r, s in zip(*np.nonzero(picks == e)):
+            y[r, s] = oracle.expert_row(x[r], wg, wu, wd, *(vec[nm][e] for nm in ("suh_g", "suh_u", "suh_d", "svh_g",
+                                                                                   "svh_u", "svh_d")),
+                                        sk_gu=1, sk_d=1, warps=1)[0]
+    oracle.combine(y, weights, rows, SLOTS)
+    secs = time.perf_counter() - t0
+    return {"value": round(rows / secs, 3), "unit": "tok/s", "cores": 1, "kind": "port", "cpu_model": cpu_model(),
+            "sample": f"one {rows}-token window of config 3 ({len(used)} distinct experts, each decoded once, then "
+                      "its member rows; oracle/gfr_oracle.c, scalar, 1 thread)", "seconds": round(secs, 2)}
 
 
 def counter_summary(path):
@@ -458,6 +543,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--ramp-ms", type=float, default=300.0, help="untimed decode replays (wall ms) before each "
+                    "timed decode replay, whatever --warmup is: the clock ramp")
     ap.add_argument("--copies", type=int, default=16)
     ap.add_argument("--routings", type=int, default=64)
     ap.add_argument("--cpu-tokens", type=int, default=12)
@@ -529,9 +616,11 @@ def main():
     if not args.no_extra:
         extra = other_configs(args, copies, stream)
         log("other configs: " + json.dumps(extra))
-    cpu = cpu_all = None
+    cpu = cpu_all = cpu_c1 = cpu_c3 = None
     if not args.no_cpu:
         cpu, cpu_all = cpu_baseline(args, copies, xs, logits)
+        cpu_c1, cpu_c3 = cpu_baseline_c1(), cpu_baseline_c3(copies)
+        log(f"cpu baseline c1: {cpu_c1['value']} tok/s; c3: {cpu_c3['value']} tok/s")
         log(f"cpu baseline: {cpu['value']} tok/s over {cpu['seconds']} s; {cpu_all['cores']} threads "
             f"{cpu_all['value']} tok/s")
     out = {
@@ -542,7 +631,8 @@ def main():
                                "experts, inter 1536, top-4, K=4", "global_batch": 1, "seq_len": 1,
                    "parallelism": "single-gpu", "weight_copies": args.copies, "routings": args.routings,
                    "weight_bytes_cycled": int(args.copies * (E + 1) * 3 * D * N * BITS // 8)},
-        "roofline": roof, "cpu_baseline": cpu, "cpu_baseline_all_cores": cpu_all, "prefill": prefill,
+        "roofline": roof, "cpu_baseline": cpu, "cpu_baseline_all_cores": cpu_all,
+        "cpu_baseline_other_configs": {"c1": cpu_c1, "c3": cpu_c3}, "prefill": prefill,
         "other_configs": extra,
     }
     print(json.dumps(out), flush=True)

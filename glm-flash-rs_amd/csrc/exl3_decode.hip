@@ -21,21 +21,6 @@
 
 namespace gfr {
 
-#ifndef GFR_SHARED_NOROUTE
-#define GFR_SHARED_NOROUTE 1
-#endif
-#ifndef GFR_GATEUP_PREFETCH
-#define GFR_GATEUP_PREFETCH 1
-#endif
-#ifdef GFR_GEMV_TRACE
-// timing builds only: per-wave timestamps of the decode launches (gate/up, down, finish)
-__device__ uint64_t* g_gemv_trace[3];
-#define GEMV_MARK(W, SLOT, k) do { uint64_t* tr_ = g_gemv_trace[W]; __builtin_amdgcn_sched_barrier(0); \
-    if (tr_ && (threadIdx.x & 63) == 0) tr_[(size_t)(SLOT) * 8 + (k)] = __builtin_amdgcn_s_memrealtime(); \
-    __builtin_amdgcn_sched_barrier(0); } while (0)
-#else
-#define GEMV_MARK(W, SLOT, k) do { } while (0)
-#endif
 
 template <int K>
 __device__ __forceinline__ void load_words(const uint32_t* __restrict__ p, uint32_t (&w)[K]) {
@@ -197,16 +182,13 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, t = lane >> 3, i = lane & 7;
     const int KT = a.Kin >> 4, NT = a.N >> 4;
     const int kt0 = split * KC + wave * KTW;
-    constexpr int TW = XSRC == 1 ? 0 : 2;
-    const size_t tslot = (((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * NW + wave;
-    GEMV_MARK(TW, tslot, 0);
 
     int e, code;
     uint32_t xearly = 0;   // ROUTE1 with the fused rotation: the token's input pair, loaded while it is routed
     if constexpr (ROUTE1) {
         if constexpr (XSRC == 1)
             xearly = *reinterpret_cast<const uint32_t*>(a.x0 + (kt0 & ~7) * 16 + 2 * lane);
-        if (GFR_SHARED_NOROUTE && u == a.slots - 1) {
+        if (u == a.slots - 1) {
             // the shared expert (id `routed`, above every routed id, in the last slot) is always the window's last
             // unit: its waves need no routing and start their trellis stream at once
             e = a.routed;
@@ -243,7 +225,6 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
         // check sits here: a later exit, after the ballot, cost the RB > 1 forms most of their registers)
         if (u >= cntu || e >= a.E || (c0 > 0 && __builtin_amdgcn_readlane(code, c0 & 63) < 0)) return;
     }
-    GEMV_MARK(TW, tslot, 1);
     const int cnt = __popcll(__ballot(code >= 0));        // members come first
     const int pair_l = code >= 0 ? (code >> 5) * a.slots + (code & 31) : 0;
 
@@ -341,7 +322,6 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
             for (int kk = PRE; kk < KTW; ++kk) load_words<K>(tsrc + (size_t)kk * NT * (8 * K), wr[kk]);
         });
         __builtin_amdgcn_sched_barrier(0);
-        GEMV_MARK(TW, tslot, 2);
         float acc[RB][2];
 #pragma unroll
         for (int m = 0; m < RB; ++m) acc[m][0] = acc[m][1] = 0.f;
@@ -363,11 +343,7 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
                     tile_dot(cw, xd, acc[m]);
                 }
             }
-#ifdef GFR_GEMV_TRACE
-            if (kk == 0) GEMV_MARK(TW, tslot, 3);
-#endif
         }
-        GEMV_MARK(TW, tslot, 4);
         if constexpr (NW == 1) {
 #pragma unroll
             for (int m = 0; m < RB; ++m)
@@ -396,7 +372,6 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
         }
     };
     chunk(c0, nr0);
-#if GFR_GATEUP_PREFETCH
     // Read-ahead of this expert's down matrix for the next launch. The gate waves (mat 0, first chunk) end about 2 us
     // before the up waves that share their CUs, with the HBM idle: each loads one dword of every 128-byte line of its
     // share (gridDim.y * SK * NW gate waves an expert, at most 4 lines a lane), so the down launch's trellis loads hit
@@ -431,8 +406,6 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
                                  : "v"(at(0)), "v"(at(1)), "v"(at(2)), "v"(at(3)) : "memory");
         }
     }
-#endif
-    GEMV_MARK(TW, tslot, 5);
 }
 
 // ---- down GEMV of the decode path ------------------------------------------------------------------------------
@@ -447,12 +420,8 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
 // order. Every sum has a fixed order, and a row's result never depends on the other rows.
 //   a.Kin = intermediate size (the down input), a.N = hidden size; a.suh0 = suh_d, a.svh_g / svh_u the gate / up
 //   output scales, a.t0 the down trellis, a.zgu / SKgu the gate/up partials, a.z = Zd, a.x1 (reused) = svh_d.
-#ifndef GFR_DOWN_HB2_MIN
-#define GFR_DOWN_HB2_MIN 4096   // hidden sizes from which a down workgroup covers two 128-output blocks
-#endif
-#ifndef GFR_DOWN_XCD
-#define GFR_DOWN_XCD 1
-#endif
+// hidden sizes from which a down workgroup covers two 128-output blocks
+constexpr int DOWN_HB2_MIN = 4096;
 // The dispatcher hands workgroup L (linear launch order) to XCD L % 8, and each XCD has its own L2. Renumber the grid
 // so that XCD x runs the logical range [x T/8, (x+1) T/8) with y (the output row block) fastest, then x, then z: the
 // row blocks of one (unit, k block) then share one L2 for the partials and scales they all read. Grids whose size
@@ -460,7 +429,7 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
 __device__ inline void xcd_grouped(int& bx, int& by, int& bz) {
     bx = blockIdx.x; by = blockIdx.y; bz = blockIdx.z;
     const int gx = gridDim.x, gy = gridDim.y, T = gx * gy * gridDim.z;
-    if (!GFR_DOWN_XCD || (T & 7)) return;
+    if (T & 7) return;
     const int L = bx + gx * (by + gy * bz), g = (L & 7) * (T >> 3) + (L >> 3);
     by = g % gy;
     bx = (g / gy) % gx;
@@ -477,13 +446,10 @@ __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
     const int u = bx % a.ucap, c0 = (bx / a.ucap) * RB;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, t = lane >> 3, i = lane & 7;
     const int KT = a.Kin >> 4, NT = a.N >> 4;
-    const size_t tslot = (((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * 4 + wave;
-    GEMV_MARK(1, tslot, 0);
     const int cntu = a.ucount[0];
     const int e = a.uids[u];
     const int code = lane < a.maxm ? a.members[(size_t)u * a.maxm + lane] : -1;
     if (u >= cntu || e >= a.E || (c0 > 0 && __builtin_amdgcn_readlane(code, c0 & 63) < 0)) return;
-    GEMV_MARK(1, tslot, 1);
     const int cnt = __popcll(__ballot(code >= 0));
     const int nr = cnt - c0 < RB ? cnt - c0 : RB;
     const int pair_l = code >= 0 ? (code >> 5) * a.slots + (code & 31) : 0;
@@ -571,7 +537,6 @@ __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
             }
         }
     }
-    GEMV_MARK(1, tslot, 2);
     // ---- this wave's two tiles of the first block decoded (they wait for their own words only)
     uint32_t cw[2][32];
     auto decode_block = [&](int h) {
@@ -583,7 +548,6 @@ __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
         }
     };
     decode_block(0);
-    GEMV_MARK(1, tslot, 3);
     __syncthreads();                                     // every member's activations are in LDS
 #pragma unroll
     for (int h = 0; h < HB; ++h) {
@@ -603,7 +567,6 @@ __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
             }
         }
     }
-    GEMV_MARK(1, tslot, 4);
     __syncthreads();
     // ---- the four waves in order, then the down epilogue's transform and scale of this k block's part, a (member,
     // block) a wave
@@ -621,7 +584,6 @@ __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
         *reinterpret_cast<float2*>(a.z + ((size_t)kb * a.P + p) * a.N + ob + 2 * lane) =
             make_float2(v[0] * HAD_SCALE * f16_to_f32((uint16_t)sv), v[1] * HAD_SCALE * f16_to_f32((uint16_t)(sv >> 16)));
     }
-    GEMV_MARK(1, tslot, 5);
 }
 
 // The combine's terms past the EXL3 slots (the reference's combine(y, shared, weights, out), moe.rs:171-181): the
@@ -651,8 +613,6 @@ __global__ void __launch_bounds__(1024) sum_finish_kernel(const float* __restric
     const int row = blockIdx.x, blk = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nwv = blockDim.x >> 6;
     const int n = blk * 128 + 2 * lane;
-    const size_t tslot = ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 16 + wave;
-    GEMV_MARK(2, tslot, 0);
     // the first shared slot's weight and output, loaded up front (wave 0 adds them last)
     const bool sh = weights && shared && exl3_slots < slots && wave == 0;
     float sw = 0.f;
@@ -702,7 +662,6 @@ __global__ void __launch_bounds__(1024) sum_finish_kernel(const float* __restric
         }
         *reinterpret_cast<float2*>(out + (size_t)row * D + n) = make_float2(o0, o1);
     }
-    GEMV_MARK(2, tslot, 5);
 }
 
 // Down epilogue (exl3.cu:300-321) and, with weights, the slot-ordered combine of a token. Program (token row,
@@ -717,8 +676,6 @@ __global__ void __launch_bounds__(1024) down_finish_kernel(const float* __restri
     __shared__ float2 ys[16][64];
     const int row = blockIdx.x, blk = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nwv = blockDim.x >> 6;
-    const size_t tslot = ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 16 + wave;
-    GEMV_MARK(2, tslot, 0);
     const int n = blk * 128 + 2 * lane;
     // the first shared slot's weight and output, loaded up front (wave 0 adds them last)
     const bool sh = weights && shared && exl3_slots < slots && wave == 0;
@@ -783,7 +740,6 @@ __global__ void __launch_bounds__(1024) down_finish_kernel(const float* __restri
         }
         *reinterpret_cast<float2*>(out + (size_t)row * D + n) = make_float2(o0, o1);
     }
-    GEMV_MARK(2, tslot, 5);
 }
 
 // gateup epilogue (exl3.cu:260-296): ordered split sums of gate and up, rotation, svh scales, GLM's limited SwiGLU
@@ -884,12 +840,6 @@ __global__ void __launch_bounds__(64) down_epilogue_kernel(const float* __restri
 #include "launch.hpp"
 
 namespace gfr {
-
-#ifdef GFR_GEMV_TRACE
-extern "C" int gfr_gemv_trace_set(int which, uint64_t* p) {
-    return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_gemv_trace), &p, sizeof p, which * sizeof p, hipMemcpyHostToDevice);
-}
-#endif
 
 hipError_t launch_decode_tiles(hipStream_t s, const uint32_t* T, int kin, int n, int bits, uint16_t* out) {
     const dim3 grid((n / 16 + 7) / 8, kin / 16);
@@ -1013,7 +963,7 @@ hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, int SKgu, 
     a.ucap = maxu;
     // two 128-output blocks a workgroup at wide outputs (one gate/up epilogue build and one workgroup's setup for
     // twice the trellis); the sums are the same either way
-    const int hbw = (D / 128) % 2 == 0 && D >= GFR_DOWN_HB2_MIN ? 2 : 1;
+    const int hbw = (D / 128) % 2 == 0 && D >= DOWN_HB2_MIN ? 2 : 1;
     const dim3 grid(chunks_x(maxu, rows < maxm ? rows : maxm, rb), D / 128 / hbw, N / 128);
 #define GFR_DOWN_HB(KB, HB)                                                                                       \
     if (rb == 1) down_gemv_kernel<KB, 1, HB><<<grid, 256, 0, s>>>(a);                                               \

@@ -356,7 +356,6 @@ struct PrefillArgs {
     float limit;
     int sk, P;               // split-K launches: K splits, pairs
     float* z;                // split-K output: partial sums [mats][sk][P][N] fp32 (no epilogue)
-    uint64_t* trace;         // GFR_PF_TRACE builds only: per-workgroup timestamps [grid][8]
 };
 
 // The A fragment of one 16-column trellis tile over two k tiles (K = 4): lane l owns column c = l % 16 of the tile
@@ -664,20 +663,10 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
     decode_a(0, a0);
     // one step: multiply (ac, B fragments of the ring) while an is decoded for step s + 1 and the ring is refilled
     // D fragments ahead (the last D of them from step s + 1's stage)
-#ifdef GFR_PF_TRACE
-    uint64_t tw = 0;
-    const uint64_t tl0 = __builtin_amdgcn_s_memtime();
-#endif
     auto step = [&](int s, int slot, const h8_t (&ac)[4], h8_t (&an)[4]) {
         // stage s + 1 landed (at most the stages after it in flight) and every wave is done with stage s - 1
-#ifdef GFR_PF_TRACE
-        const uint64_t w0 = __builtin_amdgcn_s_memtime();
-#endif
         wait_stages(min(S - 1, s + NS - 2) - (s + 1));
         lds_barrier();
-#ifdef GFR_PF_TRACE
-        tw += __builtin_amdgcn_s_memtime() - w0;
-#endif
         if (s + NS - 1 < S) issue(s + NS - 1);           // into stage s - 1's buffer, now free
         const int sn = (slot + 1) % NS;                   // the next step's slot (the last step reads a stale one,
                                                           // unused)
@@ -753,19 +742,9 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
                 for (int t4 = 0; t4 < 4; ++t4) *reinterpret_cast<f4_t*>(zr + t4 * 16) = acc[t4][b];
             }
         }
-#ifdef GFR_PF_TRACE
-        if (tid == 0) {
-            uint64_t* o = a.trace + (size_t)(MATS == 2 ? 0 : 16384) * 8 + (size_t)blockIdx.x * 8;
-            o[0] = tl0; o[1] = __builtin_amdgcn_s_memtime(); o[2] = o[1]; o[3] = tw;
-            o[4] = __builtin_amdgcn_s_memrealtime(); o[5] = MATS;
-        }
-#endif
         return;
     }
     __syncthreads();
-#ifdef GFR_PF_TRACE
-    const uint64_t tl1 = __builtin_amdgcn_s_memtime();
-#endif
 
     // ---- epilogue: ER rows at a time through LDS; each wave takes ER / 4 rows, four at a time (lane layout of
     // fwht128_l8). The column scales are the same for every row: loaded once.
@@ -875,13 +854,6 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
     chunk(std::integral_constant<int, 3>{});
     chunk(std::integral_constant<int, 4>{});
     chunk(std::integral_constant<int, 5>{});
-#ifdef GFR_PF_TRACE
-    if (tid == 0) {
-        uint64_t* o = a.trace + (size_t)(MATS == 2 ? 0 : 16384) * 8 + (size_t)blockIdx.x * 8;
-        o[0] = tl0; o[1] = tl1; o[2] = __builtin_amdgcn_s_memtime(); o[3] = tw; o[4] = __builtin_amdgcn_s_memrealtime();
-        o[5] = MATS;
-    }
-#endif
 }
 
 }  // namespace gfr
@@ -892,9 +864,6 @@ struct gfr_fast_experts {
     float* out;
     int *ucnt, *items, *plan;
     float *zgu, *zd;          // split-K partials of windows of at most PF_SPLIT_PAIRS pairs (else null)
-#ifdef GFR_PF_TRACE
-    uint64_t* trace;
-#endif
 };
 
 namespace gfr {
@@ -931,9 +900,6 @@ hipError_t prefill_create(gfr_fast_experts** out, int hidden, int inter, int slo
         (e = hipMalloc(&fx->xd, P * inter * 2)) != hipSuccess || (e = hipMalloc(&fx->out, P * hidden * 4)) != hipSuccess ||
         (e = hipMalloc(&fx->ucnt, PF_MAXU * 4)) != hipSuccess || (e = hipMalloc(&fx->items, max_items * 4)) != hipSuccess ||
         (e = hipMalloc(&fx->plan, 16)) != hipSuccess
-#ifdef GFR_PF_TRACE
-        || (e = hipMalloc(&fx->trace, 32768 * 8 * 8)) != hipSuccess
-#endif
     ) {
         prefill_destroy(fx);
         return e;
@@ -1031,9 +997,6 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
     // item_bound(max P, PF_MAXU), which is at least this
     const int max_items = P / bm + maxu < P ? P / bm + maxu : P;
     PrefillArgs a{};
-#ifdef GFR_PF_TRACE
-    a.trace = fx->trace;
-#endif
     a.uids = ids; a.members = members; a.ucnt = fx->ucnt; a.items = fx->items; a.plan = fx->plan;
     a.maxm = maxm; a.slots = d.slots; a.limit = 10.f;
     if (split) {
@@ -1077,9 +1040,6 @@ void prefill_plan_buffers(gfr_fast_experts* fx, int** ucnt, int** items, int** p
     *items = fx->items;
     *plan = fx->plan;
 }
-#ifdef GFR_PF_TRACE
-extern "C" uint64_t* gfr_fast_experts_trace(const gfr_fast_experts* fx) { return fx->trace; }
-#endif
 uint16_t* prefill_xd(const gfr_fast_experts* fx) { return fx->xd; }
 uint16_t* prefill_rotated(const gfr_fast_experts* fx, int mat) { return mat ? fx->xu : fx->xg; }
 

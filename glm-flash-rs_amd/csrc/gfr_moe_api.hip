@@ -476,6 +476,10 @@ int moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uin
     if (shared && m->shared_exl3) return fail(GFR_EINVAL, "the layer's shared expert is EXL3: no shared output");
     if (shared && shared_stride < m->hidden) return fail(GFR_EINVAL, "shared stride %d < hidden %d", shared_stride,
                                                          m->hidden);
+    // the combine reads the shared rows 16 bytes at a time
+    if (shared && (shared_stride % 4 || reinterpret_cast<uintptr_t>(shared) % 16))
+        return fail(GFR_EINVAL, "shared output: stride %d must be a multiple of 4 and the pointer 16-byte aligned",
+                    shared_stride);
     if (shared_ready && !shared) return fail(GFR_EINVAL, "a shared-ready event without a shared output");
     hipError_t e;
     if (rows <= m->decode_rows) {
@@ -671,6 +675,10 @@ int gfr_router_logits(hipStream_t stream, const uint16_t* input, int input_strid
                     gfr::router_logits_max_hidden());
     if (routed <= 0 || rows <= 0 || input_stride < hidden)
         return fail(GFR_EINVAL, "routed %d rows %d stride %d", routed, rows, input_stride);
+    // the logits kernel reads input and weight rows 16 bytes at a time
+    if (input_stride % 8 || reinterpret_cast<uintptr_t>(input) % 16 || reinterpret_cast<uintptr_t>(router_weight) % 16)
+        return fail(GFR_EINVAL, "router input stride %d must be a multiple of 8 and both pointers 16-byte aligned",
+                    input_stride);
     hipError_t e = gfr::launch_router_logits(stream, input, input_stride, router_weight, hidden, routed, rows, logits);
     if (e != hipSuccess) return hip_fail(e, "router logits");
     return 0;

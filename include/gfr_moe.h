@@ -118,7 +118,8 @@ int gfr_moe_create(gfr_moe** out, int hidden, int inter, int routed, int topk, i
 int gfr_moe_create_shared(gfr_moe** out, int hidden, int inter, int routed, int topk, int max_rows, int shared_exl3);
 int gfr_moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
                 const float* logits, int rows);                                 /* Moe::run_prefetched :66-182 */
-/* shared [rows][shared_stride] fp32: the shared expert's output (a layer made with shared_exl3 = 0 only) */
+/* shared [rows][shared_stride] fp32: the shared expert's output (a layer made with shared_exl3 = 0 only);
+ * shared_stride a multiple of 4 and shared 16-byte aligned (read 16 bytes at a time). */
 int gfr_moe_run_shared(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
                        const float* logits, const float* shared, int shared_stride, int rows);
 /* The routed branch of shared_expert.rs Branch::run (:60-78): the caller forks its own shared expert onto another
@@ -135,6 +136,9 @@ int gfr_moe_run_router(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w
 float* gfr_moe_output(const gfr_moe* m);
 int32_t* gfr_moe_picks(const gfr_moe* m);        /* [rows][topk + 1] */
 float* gfr_moe_weights(const gfr_moe* m);        /* [rows][topk + 1] */
+/* Windows of at most decode_rows rows run the decode engine (default 4, at most 64), larger ones the prefill engine.
+ * rows == 1 runs three launches: gate/up GEMV (router and input rotation fused), down GEMV (gate/up epilogue fused),
+ * sum of the down parts + combine. */
 int gfr_moe_set_decode_rows(gfr_moe* m, int decode_rows);
 /* No counterpart in the reference: for callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). One token through the bs = 1 layer of gfr_moe_run (the
@@ -144,9 +148,7 @@ int gfr_moe_set_decode_rows(gfr_moe* m, int decode_rows);
  * 50 slots x hidden bytes) returns GFR_EINVAL. Allocates nothing. The array keeps the last call's contents; calls that
  * overlap on one GPU race on it. out [hidden] fp32; picks / weights [topk + 1] copies of the routing (may be NULL). */
 int gfr_moe_token_static(hipStream_t stream, const gfr_exl3_experts* w, int routed, int topk, const uint16_t* input,
-                         const float* logits, float* out, int32_t* picks, float* weights);  /* rows at or below run the decode path (default 4, max 64) */
-/* rows == 1 runs three launches: gate/up GEMV (router and input rotation fused), down GEMV (gate/up epilogue fused),
- * sum of the down parts + combine. */
+                         const float* logits, float* out, int32_t* picks, float* weights);
 /* The layer's router gate: bias == NULL (default) the softmax gate of gfr_route_topk; else GLM's gate of
  * gfr_route_topk_biased with this bias [routed] (device, fp32; must outlive the runs) and scale (2.5 for GLM). */
 int gfr_moe_set_router(gfr_moe* m, const float* bias, float scale);
@@ -170,7 +172,8 @@ int gfr_route_topk(hipStream_t stream, const float* logits, int rows, int routed
 /* Router logits (moe.rs:77-87, router_part [1,9,8] + router_sum; Triton, source absent): logits[r][e] =
  * sum over k of input[r][k] * router_weight[e][k], bf16 inputs, fp32 products and sums in a fixed order.
  * input [rows][input_stride] bf16, router_weight [routed][hidden] bf16, logits [rows][routed] fp32; hidden a
- * multiple of 8, at most 65536. */
+ * multiple of 8, at most 65536; input_stride a multiple of 8, input and router_weight 16-byte aligned (rows are read
+ * 16 bytes at a time). */
 int gfr_router_logits(hipStream_t stream, const uint16_t* input, int input_stride, const uint16_t* router_weight,
                       int hidden, int routed, int rows, float* logits);
 
@@ -219,7 +222,8 @@ int gfr_prefetch_properties(int* cus, int* l2_bytes);
 int gfr_prefetch_capturing(hipStream_t stream, int* active);
 /* alaska_l2pf_segments, bridge.cpp:30-35: table = device array of count (address, bytes) int64 pairs, each
  * 16-byte aligned with bytes a positive multiple of 16 (entries that are not are skipped); grid workgroups of 128
- * threads, segment s starting at thread s of the grid. */
+ * threads. The 128-byte lines of all segments are numbered in table order and dealt to the grid's threads: thread t
+ * reads lines t, t + threads, t + 2 threads, ... */
 int gfr_prefetch_segments(const int64_t* table, int count, int grid, hipStream_t stream);
 /* alaska_l2pf_experts, bridge.cpp:36-45: for u < min(*count, maxu) (device values), the first `bytes` of expert
  * ids[u] in the gate and up trellis tensors bases[0] and bases[1] (device array of 2 addresses), at

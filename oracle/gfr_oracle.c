@@ -198,6 +198,25 @@ void gfro_down_epilogue(float* z, const uint16_t* svh_d, int d, float* y) {
     for (int i = 0; i < d; ++i) y[i] = z[i] * HAD * gfro_f16_to_f32(svh_d[i]);
 }
 
+/* Row batches of the three per-row steps above, for checking whole windows: each is exactly a loop of the single-row
+ * function over the rows (tests/test_oracle.py checks that), nothing else. rot: row r of out = gfro_rot of input row
+ * rows[r] of x [*][x_stride] with scale vector suh. The epilogues: row r of g / u / z in place, as gfro_gateup_epilogue
+ * / gfro_down_epilogue. */
+void gfro_rot_rows(const uint16_t* x_bf16, long x_stride, const int32_t* rows, int nrows, const uint16_t* suh, int k,
+                   uint16_t* out) {
+    for (int r = 0; r < nrows; ++r) gfro_rot(x_bf16 + (size_t)rows[r] * x_stride, suh, k, out + (size_t)r * k);
+}
+
+void gfro_gateup_epilogue_rows(float* g, float* u, const uint16_t* svh_g, const uint16_t* svh_u,
+                               const uint16_t* suh_d, int nrows, int n, float limit, uint16_t* xd) {
+    for (int r = 0; r < nrows; ++r)
+        gfro_gateup_epilogue(g + (size_t)r * n, u + (size_t)r * n, svh_g, svh_u, suh_d, n, limit, xd + (size_t)r * n);
+}
+
+void gfro_down_epilogue_rows(float* z, const uint16_t* svh_d, int nrows, int d, float* y) {
+    for (int r = 0; r < nrows; ++r) gfro_down_epilogue(z + (size_t)r * d, svh_d, d, y + (size_t)r * d);
+}
+
 /* experts.rs:113-146 reference_first, at any shape and split order */
 void gfro_expert_row(const uint16_t* x_bf16, int D, int N, const float* wg, const float* wu, const float* wd,
                      const uint16_t* suh_g, const uint16_t* suh_u, const uint16_t* suh_d,

@@ -43,6 +43,11 @@ void gfro_gateup_epilogue(float* g, float* u, const uint16_t* svh_g, const uint1
                           const uint16_t* suh_d, int n, float limit, uint16_t* xd);
 /* exl3.cu:300-321 down epilogue on summed partials z [d] (in place) -> y fp32 [d] */
 void gfro_down_epilogue(float* z, const uint16_t* svh_d, int d, float* y);
+void gfro_rot_rows(const uint16_t* x_bf16, long x_stride, const int32_t* rows, int nrows, const uint16_t* suh, int k,
+                   uint16_t* out);
+void gfro_gateup_epilogue_rows(float* g, float* u, const uint16_t* svh_g, const uint16_t* svh_u,
+                               const uint16_t* suh_d, int nrows, int n, float limit, uint16_t* xd);
+void gfro_down_epilogue_rows(float* z, const uint16_t* svh_d, int nrows, int d, float* y);
 
 /* One expert on one row (experts.rs:113-135, reference_first, generalised to the shape): decoded weights
  * wg, wu [D][N], wd [N][D] as fp32 (gfro_unpack_f32), per-expert scale vectors. sk_gu / sk_d / warps give the

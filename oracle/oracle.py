@@ -34,6 +34,8 @@ def _load():
         "gfro_had": ([P, ctypes.c_long], None), "gfro_matmul": ([P, P, I, I, I, I, P], None),
         "gfro_rot": ([P, P, I, P], None),
         "gfro_gateup_epilogue": ([P, P, P, P, P, I, F, P], None), "gfro_down_epilogue": ([P, P, I, P], None),
+        "gfro_rot_rows": ([P, ctypes.c_long, P, I, P, I, P], None),
+        "gfro_gateup_epilogue_rows": ([P, P, P, P, P, I, I, F, P], None), "gfro_down_epilogue_rows": ([P, P, I, I, P], None),
         "gfro_expert_row": ([P, I, I, P, P, P, P, P, P, P, P, P, I, I, I, F, P, P], None),
         "gfro_linear": ([P, I, I, P, P, P, P], None),
         "gfro_group": ([P, I, I, I, I, P, P, P], I), "gfro_route": ([P, I, I, I, I, P, P], None),
@@ -111,6 +113,37 @@ def rot(x_bf16, suh):
     out = np.empty(x.shape[-1], np.uint16)
     lib().gfro_rot(_p(x), _p(s), x.shape[-1], _p(out))
     return out
+
+
+def rot_rows(x_bf16, rows, suh):
+    """gfro_rot of the listed rows of x [*][k] bf16 bits with one scale vector -> fp16 bits [len(rows)][k]."""
+    x = np.ascontiguousarray(x_bf16, np.uint16)
+    r = np.ascontiguousarray(rows, np.int32)
+    s = np.ascontiguousarray(suh, np.uint16)
+    k = x.shape[-1]
+    out = np.empty((len(r), k), np.uint16)
+    lib().gfro_rot_rows(_p(x), k, _p(r), len(r), _p(s), k, _p(out))
+    return out
+
+
+def gateup_epilogue_rows(g, u, svh_g, svh_u, suh_d, limit=10.0):
+    """gfro_gateup_epilogue of each row of g, u [rows][n] fp32 (copies; the inputs are left alone) -> xd fp16 bits."""
+    g = np.array(g, np.float32, copy=True, order="C")
+    u = np.array(u, np.float32, copy=True, order="C")
+    rows, n = g.shape
+    xd = np.empty((rows, n), np.uint16)
+    vecs = [np.ascontiguousarray(a, np.uint16) for a in (svh_g, svh_u, suh_d)]
+    lib().gfro_gateup_epilogue_rows(_p(g), _p(u), *[_p(v) for v in vecs], rows, n, limit, _p(xd))
+    return xd
+
+
+def down_epilogue_rows(z, svh_d):
+    """gfro_down_epilogue of each row of z [rows][d] fp32 (a copy) -> y fp32 [rows][d]."""
+    z = np.array(z, np.float32, copy=True, order="C")
+    rows, d = z.shape
+    y = np.empty((rows, d), np.float32)
+    lib().gfro_down_epilogue_rows(_p(z), _p(np.ascontiguousarray(svh_d, np.uint16)), rows, d, _p(y))
+    return y
 
 
 def expert_row(x_bf16, wg, wu, wd, suh_g, suh_u, suh_d, svh_g, svh_u, svh_d, sk_gu=4, sk_d=1, warps=4, limit=10.0):

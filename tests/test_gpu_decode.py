@@ -4,7 +4,7 @@ import numpy as np
 import pytest
 import torch
 
-from refs import DecodedExperts, assert_close, assert_decode_close, np_u16, np_u32
+from refs import DecodedExperts, assert_close, assert_decode_close, assert_rows_close, np_u16, np_u32, window_reference
 
 pytestmark = pytest.mark.gpu
 
@@ -290,8 +290,11 @@ def test_moe_layer_verify_window_vs_oracle(gfr, oracle, rows):
     torch.cuda.synchronize()
     p, wt = oracle.route(lg.cpu().numpy(), topk, E)
     assert np.array_equal(m.picks[:rows].cpu().numpy(), p)
-    _check_tokens(oracle, w, x, p, wt, m.output[:rows].cpu().numpy(), range(rows) if rows <= 4 else (0, 7, rows - 1),
-                  topk + 1)
+    out = m.output[:rows].cpu().numpy()
+    _check_tokens(oracle, w, x, p, wt, out, range(rows) if rows <= 4 else (0, 7, rows - 1), topk + 1)
+    if rows > 4:     # every token of the window
+        y = window_reference(oracle, w, x, p, workers=16)
+        assert_rows_close(out, oracle.combine(y, wt, rows, topk + 1), what=f"{rows}-token window, every token")
 
 
 def test_rotation_bitexact(gfr, oracle):

@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from refs import DecodedExperts, assert_close, np_u16
+from refs import DecodedExperts, assert_close, assert_rows_close, np_u16, window_reference
 
 pytestmark = pytest.mark.gpu
 
@@ -41,13 +41,11 @@ def test_fast_experts_reference_cases(gfr, oracle, weights, rows, maxm):
     assert np.all(np.isfinite(y))
     dec = DecodedExperts(oracle, w)
     xb = np_u16(x)
-    check = [(r, s) for r in range(rows) for s in range(slots)]
-    if len(check) > 24:
-        rng = np.random.default_rng(rows)
-        check = [check[i] for i in rng.choice(len(check), 24, replace=False)] + [check[-1]]
-    for r, s in check:
+    for r, s in [(0, 0), (rows - 1, slots - 1)]:
         want, _ = dec.row(xb[r], int(picks_np[r, s]), sk_gu=1, sk_d=1, warps=1)
         assert_close(y[r * slots + s], want, what=f"rows {rows} row {r} slot {s}")
+    # every (row, slot) output (fast_experts.rs:353-361 compares every output of the window)
+    assert_rows_close(y, window_reference(oracle, w, x, picks_np).reshape(rows * slots, D), what=f"rows {rows}")
 
 
 def test_shared_x_equals_separate_x(gfr, weights):
@@ -94,7 +92,8 @@ def test_prefill_graph_replays(gfr, weights):
 
 
 def test_moe_prefill_config4_tokens(gfr, oracle):
-    """Config 4 shape: 8192 tokens, 64 routed + 1 shared, top-4, uniform routing; sampled tokens vs the oracle."""
+    """Config 4 shape: 8192 tokens, 64 routed + 1 shared, top-4, uniform routing: routing exact; three tokens against
+    the oracle's own row order, and every token's output against the whole-window reference."""
     import synth
     E, topk, rows = 64, 4, 8192
     w = synth.experts(E + 1, D, N, BITS, seed=5)
@@ -113,14 +112,16 @@ def test_moe_prefill_config4_tokens(gfr, oracle):
         ys = np.stack([dec.row(xb[r], int(e), sk_gu=1, sk_d=1, warps=1)[0] for e in p[r]])
         want = oracle.combine(ys, wt[r:r + 1], 1, topk + 1)
         assert_close(out[r], want[0], what=f"token {r}")
+    y = window_reference(oracle, w, x, p, workers=16)
+    assert_rows_close(out, oracle.combine(y, wt, rows, topk + 1), what="config 4, every token")
 
 
 @pytest.mark.parametrize("bits", [2, 3, 4, 5])
 @pytest.mark.parametrize("rows", [40, 320])
 def test_fast_experts_bit_widths(gfr, oracle, bits, rows):
-    """K = 2, 3, 4, 5 (config 5's mixed bit rates) at C5's hidden size against the oracle: K = 4's decode straight
-    into MFMA fragments, the others' generic decode (one trellis lane a thread, pieces handed to their MFMA lanes
-    through LDS). 40 rows (360 pairs) run the split-K programs, 320 rows (2880 pairs) the full-K items with the fused
+    """K = 2, 3, 4, 5 (config 5's mixed bit rates) at C5's hidden size against the oracle: every width decodes its
+    trellis straight into MFMA A fragments (K = 4 from word pairs, the others through one funnel shift a group of four
+    values). 40 rows (360 pairs) run the split-K programs, 320 rows (2880 pairs) the full-K items with the fused
     epilogues."""
     import synth
     Dk, Nk, E, slots, maxm = 5120, 1536, 9, 9, rows
@@ -139,17 +140,21 @@ def test_fast_experts_bit_widths(gfr, oracle, bits, rows):
     assert np.all(np.isfinite(y))
     dec = DecodedExperts(oracle, w)
     xb = np_u16(x)
-    for r, s in [(0, 0), (7, 3), (19, slots - 1), (rows - 1, 5)]:
+    for r, s in [(0, 0), (rows - 1, 5)]:
         want, _ = dec.row(xb[r], int(picks_np[r, s]), sk_gu=1, sk_d=1, warps=1)
         assert_close(y[r * slots + s], want, what=f"K={bits} row {r} slot {s}")
+    assert_rows_close(y, window_reference(oracle, w, x, picks_np).reshape(rows * slots, Dk),
+                      what=f"K={bits} rows {rows}, every (row, slot)")
 
 
-def test_moe_prefill_config5_chunk(gfr, oracle):
-    """Config 5's prefill chunk: 16384 tokens, hidden 5120, 160 routed + 1 shared, top-8, Zipf(1.1) routing, K = 3;
-    routing exact, sampled tokens against the oracle."""
+@pytest.mark.parametrize("bits", [2, 3, 4, 5])
+def test_moe_prefill_config5_chunk(gfr, oracle, bits):
+    """Config 5's prefill chunk at each of the stack's bit widths: 16384 tokens, hidden 5120, 160 routed + 1 shared,
+    top-8, Zipf(1.1) routing; routing exact, the first, a middle and the last token against the oracle, and 64 spread
+    tokens against the whole-window reference."""
     import synth
-    E, Dk, Nk, topk, rows, bits = 160, 5120, 1536, 8, 16384, 3
-    w = synth.experts(E + 1, Dk, Nk, bits, seed=71)
+    E, Dk, Nk, topk, rows = 160, 5120, 1536, 8, 16384
+    w = synth.experts(E + 1, Dk, Nk, bits, seed=71 if bits == 3 else 71 + 10 * bits)
     x = synth.activations(rows, Dk, 72)
     lg = synth.zipf_logits(rows, E, topk, 1.1, 73)
     m = gfr.Moe(Dk, Nk, E, topk, rows)
@@ -161,10 +166,13 @@ def test_moe_prefill_config5_chunk(gfr, oracle):
     assert np.array_equal(m.picks[:rows].cpu().numpy(), p)
     dec = DecodedExperts(oracle, w)
     xb = np_u16(x)
-    for r in (0, rows - 1):
+    for r in (0, rows // 2 + 1, rows - 1):
         ys = np.stack([dec.row(xb[r], int(e), sk_gu=1, sk_d=1, warps=1)[0] for e in p[r]])
         want = oracle.combine(ys, wt[r:r + 1], 1, topk + 1)
-        assert_close(out[r], want[0], what=f"config 5 token {r}")
+        assert_close(out[r], want[0], what=f"config 5 K={bits} token {r}")
+    sel = np.linspace(0, rows - 1, 64).astype(np.int64)
+    y = window_reference(oracle, w, x[torch.from_numpy(sel).cuda()], p[sel], workers=16)
+    assert_rows_close(out[sel], oracle.combine(y, wt[sel], len(sel), topk + 1), what=f"config 5 K={bits}, 64 tokens")
 
 
 def _unpair(rows_u16):
@@ -233,3 +241,5 @@ def test_split_window_with_many_experts(gfr, oracle):
         ys = np.stack([dec.row(xb[r], int(e), sk_gu=1, sk_d=1, warps=1)[0] for e in p[r]])
         want = oracle.combine(ys, wt[r:r + 1], 1, topk + 1)
         assert_close(out[r], want[0], what=f"token {r}")
+    y = window_reference(oracle, w, x, p, workers=16)
+    assert_rows_close(out, oracle.combine(y, wt, rows, topk + 1), what="1023 experts, every token")

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from refs import DecodedExperts, assert_close, assert_decode_close, np_u16
+from refs import DecodedExperts, assert_close, assert_decode_close, assert_rows_close, np_u16, window_reference
 
 pytestmark = pytest.mark.gpu
 
@@ -72,14 +72,15 @@ def test_fast_experts_probe_reference_geometry(gfr, oracle, weights, rows, maxm)
     out = fx.output[:rows * SLOTS].cpu().numpy()
     dec = DecodedExperts(oracle, weights)
     xb = np_u16(x)
-    rng = np.random.default_rng(rows)
-    check = [(0, 0), (rows - 1, EXL3_SLOTS - 1)] + [(int(r), int(s)) for r, s in
-                                                    zip(rng.integers(0, rows, 10), rng.integers(0, EXL3_SLOTS, 10))]
-    for r, s in check:
+    for r, s in [(0, 0), (rows - 1, EXL3_SLOTS - 1)]:
         want, _ = dec.row(xb[r], int(picked[r, s]), sk_gu=1, sk_d=1, warps=1)
         assert_close(out[r * SLOTS + s], want, what=f"rows {rows} row {r} slot {s}")
     shared_rows = out.reshape(rows, SLOTS, D)[:, SLOTS - 1]
     assert np.all(shared_rows == 7.0), "the non-EXL3 slot's output must stay untouched"
+    # every EXL3 (row, slot) output of the window, as fast_experts.rs:353-361 checks every byte of its windows
+    want = window_reference(oracle, weights, x, picked, exl3_slots=EXL3_SLOTS, workers=16)
+    assert_rows_close(out.reshape(rows, SLOTS, D)[:, :EXL3_SLOTS], want[:, :EXL3_SLOTS],
+                      what=f"rows {rows}, every EXL3 (row, slot)")
 
 
 @pytest.mark.parametrize("rows,routed,hidden", [(1, 64, 2048), (3, 288, 4096), (70, 64, 2048), (5, 160, 5120)])

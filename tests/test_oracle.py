@@ -371,3 +371,53 @@ def test_linear_vs_float64(oracle):
         want_exact = Hb(Hb(x.astype(np.float64) * suh.astype(np.float64)) @ w.astype(np.float64)) * svh.astype(np.float64)
         err2 = np.sqrt(np.mean((y - want_exact) ** 2) / np.mean(want_exact ** 2))
         assert err2 < 2e-3, (kin, n, err2)
+
+
+def test_row_batches_are_loops_of_the_row_functions(oracle):
+    """gfro_rot_rows / gfro_gateup_epilogue_rows / gfro_down_epilogue_rows equal the single-row functions, bit for
+    bit, row by row (including a repeated and an out-of-order row index)."""
+    rng = np.random.default_rng(21)
+    D, N = 384, 256
+    x = (rng.standard_normal((6, D)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    suh = ((rng.integers(0, 2, D) * 2 - 1) * (rng.random(D) + 0.5)).astype(np.float16).view(np.uint16)
+    rows = np.array([4, 0, 4, 2], np.int32)
+    got = oracle.rot_rows(x, rows, suh)
+    for i, r in enumerate(rows):
+        assert np.array_equal(got[i], oracle.rot(x[r], suh))
+    sc = lambda n: ((rng.integers(0, 2, n) * 2 - 1) * (rng.random(n) + 0.5)).astype(np.float16).view(np.uint16)
+    svh_g, svh_u, suh_d, svh_d = sc(N), sc(N), sc(N), sc(D)
+    g = rng.standard_normal((3, N)).astype(np.float32) * 4
+    u = rng.standard_normal((3, N)).astype(np.float32) * 4
+    xd = oracle.gateup_epilogue_rows(g, u, svh_g, svh_u, suh_d)
+    z = rng.standard_normal((3, D)).astype(np.float32)
+    y = oracle.down_epilogue_rows(z, svh_d)
+    L = oracle.lib()
+    for r in range(3):
+        gg, uu, one = g[r].copy(), u[r].copy(), np.empty(N, np.uint16)
+        L.gfro_gateup_epilogue(gg.ctypes.data, uu.ctypes.data, svh_g.ctypes.data, svh_u.ctypes.data, suh_d.ctypes.data,
+                               N, 10.0, one.ctypes.data)
+        assert np.array_equal(xd[r], one)
+        zz, yy = z[r].copy(), np.empty(D, np.float32)
+        L.gfro_down_epilogue(zz.ctypes.data, svh_d.ctypes.data, D, yy.ctypes.data)
+        assert np.array_equal(y[r], yy)
+
+
+def test_window_reference_matches_expert_row(oracle):
+    """The whole-window checker of the GPU tests (refs.window_reference: per-expert fp32 GEMMs of the oracle's decoded
+    fp16 weights around the oracle's rotation and epilogues) against gfro_expert_row on every (row, slot), with a
+    non-EXL3 slot left NaN."""
+    import sys, os
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "glm-flash-rs_amd"))
+    import synth
+    from refs import DecodedExperts, assert_rows_close, window_reference
+    E, D, N, bits, rows = 4, 256, 256, 3, 5
+    w = synth.experts(E, D, N, bits, seed=3, device="cpu")
+    x = synth.activations(rows, D, 4, device="cpu")
+    picks = np.array([[0, 2, 4], [1, 3, 4], [3, 0, 4], [2, 2, 4], [1, 0, 4]], np.int32)   # id 4: not EXL3
+    y = window_reference(oracle, w, x, picks, workers=2)
+    assert np.all(np.isnan(y[:, 2]))
+    dec = DecodedExperts(oracle, w)
+    xb = x.view(torch.int16).numpy().view(np.uint16)
+    want = np.stack([np.stack([dec.row(xb[r], int(picks[r, s]), sk_gu=1, sk_d=1, warps=1)[0] for s in range(2)])
+                     for r in range(rows)])
+    assert_rows_close(y[:, :2], want, what="window reference")

@@ -47,3 +47,44 @@ def test_token_static_rejects_oversize(gfr):
     rc = L.gfr_moe_token_static(0, ctypes.byref(ws), E, 8, dummy.data_ptr(), dummy.data_ptr(), dummy.data_ptr(),
                                 None, None)
     assert rc == gfr.GFR_EINVAL and b"static array" in L.gfr_last_error(), L.gfr_last_error()
+
+
+def test_token_static_captures_and_allocates_nothing(gfr):
+    """The property the entry point exists for: once warm, a call changes no device memory figure, and a captured
+    call replays to the eager bytes (graph replays with eager work and synchronisations between them)."""
+    L = gfr.lib()
+    E, D, N, topk, bits = 64, 2048, 1536, 4, 4
+    w, x, lg = _layer(gfr, E, D, N, topk, bits, 700)
+    ws = w.struct()
+    out = torch.full((D,), float("nan"), device="cuda")
+    picks = torch.full((topk + 1,), -9, dtype=torch.int32, device="cuda")
+    weights = torch.full((topk + 1,), float("nan"), device="cuda")
+
+    def call(stream):
+        rc = L.gfr_moe_token_static(stream.cuda_stream, ctypes.byref(ws), E, topk, x.data_ptr(), lg.data_ptr(),
+                                    out.data_ptr(), picks.data_ptr(), weights.data_ptr())
+        assert rc == 0, L.gfr_last_error()
+
+    s = torch.cuda.Stream()
+    call(s)                                   # warm: the library's per-device set-up happens here
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    call(s)
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    assert free0 - free1 < 1 << 20, f"an eager call took {free0 - free1} bytes of device memory"
+    eager = out.clone()
+    eager_picks = picks.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            call(s)
+    for _ in range(3):
+        out.fill_(float("nan"))
+        picks.fill_(-9)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        assert torch.equal(picks, eager_picks)
