@@ -52,7 +52,7 @@ def graph_of(fn_steps, stream):
 def time_graphs(plan, stream, lead=()):
     """plan: list of graphs replayed in order; returns seconds between HIP events recorded on `stream`. lead: graphs
     replayed (untimed) right before the start event with no synchronisation in between, so that the GPU is still
-    busy while the host submits the timed replays (no host-launch gap at the start of a short timed region)."""
+    busy while the host submits the timed replays."""
     import torch
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -79,20 +79,16 @@ def ramp(graph, stream, seconds):
             stream.synchronize()
 
 
-def replay_plan(steps, glen, full, rest):
-    plan = [full] * (steps // glen)
-    if steps % glen:
-        plan.append(rest)
-    return plan
-
-
 def decode_bench(args):
-    """Config 2: `args.steps` bs=1 layer steps as graph replays. Step j uses weight copy j % copies and routing
-    j % routings. Before each timed replay: `--warmup` steps plus a fixed-time clock ramp (`--ramp-ms` of replays,
-    whatever --warmup is), both on routings the timed steps do not use, so the timed replay does not start on weights
-    it just touched; the last warm replay is still running when the timed replay is submitted. Also times the
-    layer's first launch alone and its first two launches (the same steps, gfr_moe_set_launches), which gives each
-    launch's share of a step inside the layer's own sequence."""
+    """Config 2: `args.steps` bs=1 layer steps as the replay of one HIP graph of exactly those steps. Step j uses
+    weight copy j % copies and routing j % routings. First an untimed clock ramp (`--ramp-ms` of graph replays of
+    `--warmup` steps on routings the timed steps do not use, whatever --warmup is: the first tens of ms of a layer loop
+    run measurably slower on MI355X); then, unsynchronised, a graph of the LEAD steps that precede step 0 in the cycle,
+    still running when the timed replay is submitted, so that the first timed step meets the cache and queue state of
+    any step of a long run. Both graphs are replayed once before the ramp: the first replay of a graph is several us
+    slower on this stack, which a 20-step timed run would otherwise charge to its few steps. Also times the layer's first launch alone and its
+    first two launches (the same steps, gfr_moe_set_launches), which gives each launch's share of a step inside the
+    layer's own sequence."""
     import torch
     import gfr_moe
     import synth
@@ -102,7 +98,7 @@ def decode_bench(args):
     xs = synth.activations(R, D, 5)
     logits = synth.logits(R, E, 6)
     moe = gfr_moe.Moe(D, N, E, TOPK, 1)
-    glen = min(args.steps, 8 * args.copies)
+    lead = 32
 
     def step(j, r=None):
         r = j % R if r is None else r % R
@@ -112,25 +108,24 @@ def decode_bench(args):
         for j in range(len(copies)):
             step(j)()
     stream.synchronize()
-    warm0 = glen // 2
     per_launch = {}
     for launches in (1, 2, 0):
         moe.set_launches(launches)
-        full = graph_of([step(j) for j in range(glen)], stream)
-        rest = graph_of([step(j) for j in range(args.steps % glen)], stream) if args.steps % glen else None
-        # warm steps: copies from the middle of the cycle, routings past the ones the timed steps use
         nw = max(args.warmup, 1)
-        warm = graph_of([step(warm0 + j, glen + j) for j in range(min(nw, glen))], stream)
+        warm = graph_of([step(len(copies) // 2 + j, R // 2 + j) for j in range(min(nw, 64))], stream)
+        pre = graph_of([step(j) for j in range(-lead, 0)], stream)
+        timed = graph_of([step(j) for j in range(args.steps)], stream)
+        # the first replay of a graph is slower (its launch set-up): one untimed replay of each, before the ramp
+        time_graphs([pre, timed], stream)
         ramp(warm, stream, args.ramp_ms / 1e3)
-        per_launch[launches] = time_graphs(replay_plan(args.steps, glen, full, rest), stream,
-                                           lead=[warm] * max(nw // glen, 4))
-        del full, rest, warm
+        per_launch[launches] = time_graphs([timed], stream, lead=[pre])
+        del warm, pre, timed
     moe.set_launches(0)
     secs = per_launch[0]
-    # the replayed layer computed what an eager run of the last replayed step computes
+    # the replayed layer computed what an eager run of the last timed step computes
     replayed = moe.output[0].clone()
     with torch.cuda.stream(stream):
-        step((args.steps % glen or glen) - 1)()
+        step(args.steps - 1)()
     stream.synchronize()
     if not (torch.isfinite(replayed).all() and torch.equal(replayed, moe.output[0])):
         raise RuntimeError("graph-replayed MoE layer differs from the eager run")
