@@ -436,54 +436,23 @@ __device__ inline void xcd_grouped(int& bx, int& by, int& bz) {
     bz = g / (gy * gx);
 }
 
-template <int K, int RB, int HB>
+template <int K, int RB, int HB, bool TOKEN>
 __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t xs[RB][128];   // the k block's activations, each twice
     __shared__ float red[4][RB][128 * HB];
     __shared__ float2 psum[4][RB][2][64];                            // each wave's quarter of the gate / up splits
     int bx, hb, kb;
     xcd_grouped(bx, hb, kb);
-    const int u = bx % a.ucap, c0 = (bx / a.ucap) * RB;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, t = lane >> 3, i = lane & 7;
     const int KT = a.Kin >> 4, NT = a.N >> 4;
-    const int cntu = a.ucount[0];
-    const int e = a.uids[u];
-    const int code = lane < a.maxm ? a.members[(size_t)u * a.maxm + lane] : -1;
-    if (u >= cntu || e >= a.E || (c0 > 0 && __builtin_amdgcn_readlane(code, c0 & 63) < 0)) return;
-    const int cnt = __popcll(__ballot(code >= 0));
-    const int nr = cnt - c0 < RB ? cnt - c0 : RB;
-    const int pair_l = code >= 0 ? (code >> 5) * a.slots + (code & 31) : 0;
-
-    // ---- the gate/up epilogue inputs: every wave loads and adds its quarter of the K splits of every member
-    // (splits [w * SPW, (w + 1) * SPW), in order) into LDS, so that the partials take one round trip; then the wave
-    // building member m adds the four quarters in wave order. Members w and w + 4 are built by wave w.
-    constexpr int EM = RB > 4 ? 2 : 1;                  // members a wave builds
     const int n = kb * 128 + 2 * lane;
-    const size_t so = (size_t)e * a.Kin + n;
-    const bool builds = wave < nr;
     const int spw = (a.SKgu + 3) >> 2, s0 = wave * spw, s1 = s0 + spw < a.SKgu ? s0 + spw : a.SKgu;
-    uint32_t sg = 0, su = 0, sd = 0;
-    if (builds) {
-        sg = *reinterpret_cast<const uint32_t*>(a.svh_g + so);
-        su = *reinterpret_cast<const uint32_t*>(a.svh_u + so);
-        sd = *reinterpret_cast<const uint32_t*>(a.suh0 + so);
-    }
-    // HB output blocks of 128: the same two k tiles of each (column tiles (hb HB + h) 8 + t); the first block's
-    // words decoded before the barrier, the others' kept as words and decoded after the first block's dots
-    uint32_t wr[HB][2][K];
-    {
-        const uint32_t* src = a.t0 + (((size_t)e * KT + kb * 8 + 2 * wave) * NT + hb * HB * 8 + t) * (8 * K) + i * K;
-#pragma unroll
-        for (int h = 0; h < HB; ++h) {
-            load_words<K>(src + h * 8 * (8 * K), wr[h][0]);
-            load_words<K>(src + (size_t)NT * (8 * K) + h * 8 * (8 * K), wr[h][1]);
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    for (int m = 0; m < nr; ++m) {
-        const int p = __builtin_amdgcn_readlane(pair_l, (c0 + m) & 63);
+    // the gate/up epilogue inputs: every wave loads its quarter of the K splits of every member (splits
+    // [w * SPW, (w + 1) * SPW), four in flight, added in order) into LDS; the wave building member m then adds the
+    // four quarters in wave order (members w and w + 4 are built by wave w)
+    auto load_partials = [&](int m, int p) {
         float2 g = make_float2(0.f, 0.f), u = make_float2(0.f, 0.f);
-        for (int k0 = s0; k0 < s1; k0 += 4) {             // four splits in flight, added in order
+        for (int k0 = s0; k0 < s1; k0 += 4) {
             float2 zg[4], zu[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -500,6 +469,79 @@ __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
         }
         psum[wave][m][0][lane] = g;
         psum[wave][m][1][lane] = u;
+    };
+    int e, nr, c0, pair_l;
+    float2 tzg[4], tzu[4];                              // TOKEN: this wave's split partials, in flight
+    if constexpr (TOKEN) {
+        // a one-token window routed by the gate/up launch (RB 1): program bx is the token's slot bx, pair bx. The
+        // slot's partials need no table, so they are loaded at once, next to the slot's expert (the shared expert,
+        // id `routed` in the last slot, needs no load at all); only the trellis and scale loads wait for the id.
+        // (the host sends at most 16 splits here: a wave's quarter, at most 4, is held in registers)
+        const int slot = bx;
+        c0 = 0;
+        nr = 1;
+        pair_l = slot;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int kk = s0 + k < s1 ? s0 + k : 0;
+            tzg[k] = *reinterpret_cast<const float2*>(a.zgu + ((size_t)kk * a.P + slot) * a.Kin + n);
+            tzu[k] = *reinterpret_cast<const float2*>(a.zgu + ((size_t)(a.SKgu + kk) * a.P + slot) * a.Kin + n);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        e = slot == a.slots - 1 ? a.routed : a.pick_out[slot];
+        if (e >= a.E) return;
+    } else {
+        const int u = bx % a.ucap;
+        c0 = (bx / a.ucap) * RB;
+        const int cntu = a.ucount[0];
+        e = a.uids[u];
+        const int code = lane < a.maxm ? a.members[(size_t)u * a.maxm + lane] : -1;
+        if (u >= cntu || e >= a.E || (c0 > 0 && __builtin_amdgcn_readlane(code, c0 & 63) < 0)) return;
+        const int cnt = __popcll(__ballot(code >= 0));
+        nr = cnt - c0 < RB ? cnt - c0 : RB;
+        pair_l = code >= 0 ? (code >> 5) * a.slots + (code & 31) : 0;
+    }
+
+    constexpr int EM = RB > 4 ? 2 : 1;                  // members a wave builds
+    const size_t so = (size_t)e * a.Kin + n;
+    const bool builds = wave < nr;
+    uint32_t sg = 0, su = 0, sd = 0;
+    if (builds) {
+        sg = *reinterpret_cast<const uint32_t*>(a.svh_g + so);
+        su = *reinterpret_cast<const uint32_t*>(a.svh_u + so);
+        sd = *reinterpret_cast<const uint32_t*>(a.suh0 + so);
+    }
+    // the down epilogue's output scales of this wave's (member, block) parts (wave q < nr HB takes part q), loaded
+    // with the other scales instead of after the dots
+    uint32_t svd = 0;
+    if (wave < nr * HB) {
+        const int h = wave % HB;
+        svd = *reinterpret_cast<const uint32_t*>(a.x1 + (size_t)e * a.N + (hb * HB + h) * 128 + 2 * lane);
+    }
+    // HB output blocks of 128: the same two k tiles of each (column tiles (hb HB + h) 8 + t); the first block's
+    // words decoded before the barrier, the others' kept as words and decoded after the first block's dots
+    uint32_t wr[HB][2][K];
+    {
+        const uint32_t* src = a.t0 + (((size_t)e * KT + kb * 8 + 2 * wave) * NT + hb * HB * 8 + t) * (8 * K) + i * K;
+#pragma unroll
+        for (int h = 0; h < HB; ++h) {
+            load_words<K>(src + h * 8 * (8 * K), wr[h][0]);
+            load_words<K>(src + (size_t)NT * (8 * K) + h * 8 * (8 * K), wr[h][1]);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (TOKEN) {
+        float2 g = make_float2(0.f, 0.f), u = make_float2(0.f, 0.f);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (s0 + k < s1) {
+                g.x += tzg[k].x; g.y += tzg[k].y;
+                u.x += tzu[k].x; u.y += tzu[k].y;
+            }
+        psum[wave][0][0][lane] = g;
+        psum[wave][0][1][lane] = u;
+    } else {
+        for (int m = 0; m < nr; ++m) load_partials(m, __builtin_amdgcn_readlane(pair_l, (c0 + m) & 63));
     }
     __syncthreads();
     if (builds) {
@@ -572,7 +614,7 @@ __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
     // block) a wave
     for (int q = wave; q < nr * HB; q += 4) {
         const int m = q / HB, h = q - m * HB, ob = (hb * HB + h) * 128;
-        const uint32_t sv = *reinterpret_cast<const uint32_t*>(a.x1 + (size_t)e * a.N + ob + 2 * lane);
+        const uint32_t sv = q < 4 ? svd : *reinterpret_cast<const uint32_t*>(a.x1 + (size_t)e * a.N + ob + 2 * lane);
         float v[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -954,7 +996,7 @@ hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, int SKgu, 
                               const uint16_t* svh_u, const uint16_t* suh_d, float limit, uint16_t* xd,
                               const uint32_t* dt, const uint16_t* svh_d, const int* uids, const int* ucount,
                               const int* members, float* Zd, int N, int P, int rows, int maxm, int slots, int E,
-                              int bits, int maxu) {
+                              int bits, int maxu, const RouteOne* route) {
     GemvArgs a{};
     a.zgu = Zgu; a.SKgu = SKgu; a.svh_g = svh_g; a.svh_u = svh_u; a.suh0 = suh_d; a.limit = limit;
     a.xd = xd; a.t0 = dt; a.t1 = dt; a.x1 = svh_d; a.uids = uids; a.ucount = ucount; a.members = members; a.z = Zd;
@@ -964,12 +1006,19 @@ hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, int SKgu, 
     // two 128-output blocks a workgroup at wide outputs (one gate/up epilogue build and one workgroup's setup for
     // twice the trellis); the sums are the same either way
     const int hbw = (D / 128) % 2 == 0 && D >= DOWN_HB2_MIN ? 2 : 1;
-    const dim3 grid(chunks_x(maxu, rows < maxm ? rows : maxm, rb), D / 128 / hbw, N / 128);
+    // a one-token window routed inside the gate/up launch: one program a slot (TOKEN), no grouping tables
+    const bool token = route != nullptr && SKgu <= 16;
+    if (token) {
+        a.pick_out = route->picks;
+        a.routed = route->routed;
+    }
+    const dim3 grid(token ? (unsigned)slots : chunks_x(maxu, rows < maxm ? rows : maxm, rb), D / 128 / hbw, N / 128);
 #define GFR_DOWN_HB(KB, HB)                                                                                       \
-    if (rb == 1) down_gemv_kernel<KB, 1, HB><<<grid, 256, 0, s>>>(a);                                               \
-    else if (rb == 2) down_gemv_kernel<KB, 2, HB><<<grid, 256, 0, s>>>(a);                                          \
-    else if (rb == 4) down_gemv_kernel<KB, 4, HB><<<grid, 256, 0, s>>>(a);                                          \
-    else down_gemv_kernel<KB, 8, HB><<<grid, 256, 0, s>>>(a);
+    if (token) down_gemv_kernel<KB, 1, HB, true><<<grid, 256, 0, s>>>(a);                                          \
+    else if (rb == 1) down_gemv_kernel<KB, 1, HB, false><<<grid, 256, 0, s>>>(a);                                  \
+    else if (rb == 2) down_gemv_kernel<KB, 2, HB, false><<<grid, 256, 0, s>>>(a);                                  \
+    else if (rb == 4) down_gemv_kernel<KB, 4, HB, false><<<grid, 256, 0, s>>>(a);                                  \
+    else down_gemv_kernel<KB, 8, HB, false><<<grid, 256, 0, s>>>(a);
 #define GFR_DOWN(KB)                                                                                              \
     case KB:                                                                                                    \
         if (hbw == 2) { GFR_DOWN_HB(KB, 2) } else { GFR_DOWN_HB(KB, 1) }                                          \

@@ -189,7 +189,7 @@ int experts_run(gfr_experts* ex, hipStream_t stream, const gfr_exl3_experts* w, 
     if ((e = gfr::launch_expert_down(stream, ex->zgu, D, skgu, w->svh_g, w->svh_u, w->suh_d, 10.f, ex->xd, w->dt,
                                      w->svh_d,
                                      ids, count, members, ex->zd, N, P, rows, maxm, ex->slots, w->experts, w->bits,
-                                     maxu)) != hipSuccess)
+                                     maxu, route)) != hipSuccess)
         return hip_fail(e, "down gemv");
     if (launches == 2) return 0;
     // the shared branch joins here: only the finish (down epilogue + combine) reads its output

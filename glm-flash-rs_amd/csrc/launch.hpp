@@ -66,7 +66,9 @@ hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, int SKgu, 
                               const uint16_t* svh_u, const uint16_t* suh_d, float limit, uint16_t* xd,
                               const uint32_t* dt, const uint16_t* svh_d, const int* uids, const int* ucount,
                               const int* members, float* Zd, int N, int P, int rows, int maxm, int slots, int E,
-                              int bits, int maxu);
+                              int bits, int maxu, const RouteOne* route = nullptr);
+// route: the one-token window was routed by the gate/up launch (its picks); the down launch then runs one program a
+// slot and reads no grouping table
 // Finish of the decode path: Zd's transformed k-block parts [N / 128][P][D] added in order -> y; with weights the
 // slot-ordered combine -> out
 hipError_t launch_sum_finish(hipStream_t s, const float* Zd, float* y, int rows, int P, int D, int SK, int slots,
