@@ -422,6 +422,7 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
 //   output scales, a.t0 the down trellis, a.zgu / SKgu the gate/up partials, a.z = Zd, a.x1 (reused) = svh_d.
 // hidden sizes from which a down workgroup covers two 128-output blocks
 constexpr int DOWN_HB2_MIN = 4096;
+
 // The dispatcher hands workgroup L (linear launch order) to XCD L % 8, and each XCD has its own L2. Renumber the grid
 // so that XCD x runs the logical range [x T/8, (x+1) T/8) with y (the output row block) fastest, then x, then z: the
 // row blocks of one (unit, k block) then share one L2 for the partials and scales they all read. Grids whose size
@@ -436,17 +437,19 @@ __device__ inline void xcd_grouped(int& bx, int& by, int& bz) {
     bz = g / (gy * gx);
 }
 
-template <int K, int RB, int HB, bool TOKEN>
-__global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
+template <int K, int RB, int HB, bool TOKEN, int NW>
+__global__ void __launch_bounds__(NW * 64) down_gemv_kernel(const GemvArgs a) {
+    constexpr int TPW = 8 / NW;                          // k tiles a wave of the 128-k block
+    static_assert(NW == 2 || NW == 4, "waves a workgroup");
     __shared__ __attribute__((aligned(16))) uint32_t xs[RB][128];   // the k block's activations, each twice
-    __shared__ float red[4][RB][128 * HB];
-    __shared__ float2 psum[4][RB][2][64];                            // each wave's quarter of the gate / up splits
+    __shared__ float red[NW][RB][128 * HB];
+    __shared__ float2 psum[NW][RB][2][64];                           // each wave's share of the gate / up splits
     int bx, hb, kb;
     xcd_grouped(bx, hb, kb);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, t = lane >> 3, i = lane & 7;
     const int KT = a.Kin >> 4, NT = a.N >> 4;
     const int n = kb * 128 + 2 * lane;
-    const int spw = (a.SKgu + 3) >> 2, s0 = wave * spw, s1 = s0 + spw < a.SKgu ? s0 + spw : a.SKgu;
+    const int spw = (a.SKgu + NW - 1) / NW, s0 = wave * spw, s1 = s0 + spw < a.SKgu ? s0 + spw : a.SKgu;
     // the gate/up epilogue inputs: every wave loads its quarter of the K splits of every member (splits
     // [w * SPW, (w + 1) * SPW), four in flight, added in order) into LDS; the wave building member m then adds the
     // four quarters in wave order (members w and w + 4 are built by wave w)
@@ -471,18 +474,19 @@ __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
         psum[wave][m][1][lane] = u;
     };
     int e, nr, c0, pair_l;
-    float2 tzg[4], tzu[4];                              // TOKEN: this wave's split partials, in flight
+    constexpr int TZ = 4;                               // TOKEN: this wave's split partials, in flight
+    float2 tzg[TZ], tzu[TZ];
     if constexpr (TOKEN) {
         // a one-token window routed by the gate/up launch (RB 1): program bx is the token's slot bx, pair bx. The
         // slot's partials need no table, so they are loaded at once, next to the slot's expert (the shared expert,
         // id `routed` in the last slot, needs no load at all); only the trellis and scale loads wait for the id.
-        // (the host sends at most 16 splits here: a wave's quarter, at most 4, is held in registers)
+        // (the host sends at most 4 NW splits here: a wave's share, at most 4, is held in registers)
         const int slot = bx;
         c0 = 0;
         nr = 1;
         pair_l = slot;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < TZ; ++k) {
             const int kk = s0 + k < s1 ? s0 + k : 0;
             tzg[k] = *reinterpret_cast<const float2*>(a.zgu + ((size_t)kk * a.P + slot) * a.Kin + n);
             tzu[k] = *reinterpret_cast<const float2*>(a.zgu + ((size_t)(a.SKgu + kk) * a.P + slot) * a.Kin + n);
@@ -520,20 +524,20 @@ __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
     }
     // HB output blocks of 128: the same two k tiles of each (column tiles (hb HB + h) 8 + t); the first block's
     // words decoded before the barrier, the others' kept as words and decoded after the first block's dots
-    uint32_t wr[HB][2][K];
+    uint32_t wr[HB][TPW][K];
     {
-        const uint32_t* src = a.t0 + (((size_t)e * KT + kb * 8 + 2 * wave) * NT + hb * HB * 8 + t) * (8 * K) + i * K;
+        const uint32_t* src = a.t0 + (((size_t)e * KT + kb * 8 + TPW * wave) * NT + hb * HB * 8 + t) * (8 * K) + i * K;
 #pragma unroll
         for (int h = 0; h < HB; ++h) {
-            load_words<K>(src + h * 8 * (8 * K), wr[h][0]);
-            load_words<K>(src + (size_t)NT * (8 * K) + h * 8 * (8 * K), wr[h][1]);
+#pragma unroll
+            for (int kk = 0; kk < TPW; ++kk) load_words<K>(src + (size_t)kk * NT * (8 * K) + h * 8 * (8 * K), wr[h][kk]);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (TOKEN) {
         float2 g = make_float2(0.f, 0.f), u = make_float2(0.f, 0.f);
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
+        for (int k = 0; k < TZ; ++k)
             if (s0 + k < s1) {
                 g.x += tzg[k].x; g.y += tzg[k].y;
                 u.x += tzu[k].x; u.y += tzu[k].y;
@@ -550,11 +554,11 @@ __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
         const float sdd[2] = {f16_to_f32((uint16_t)sd), f16_to_f32((uint16_t)(sd >> 16))};
 #pragma unroll
         for (int q = 0; q < EM; ++q) {
-            const int m = wave + 4 * q;
+            const int m = wave + NW * q;
             if (m < nr) {
                 float gv[2] = {0.f, 0.f}, uv[2] = {0.f, 0.f};
 #pragma unroll
-                for (int w = 0; w < 4; ++w) {
+                for (int w = 0; w < NW; ++w) {
                     const float2 g = psum[w][m][0][lane], u = psum[w][m][1][lane];
                     gv[0] += g.x; gv[1] += g.y;
                     uv[0] += u.x; uv[1] += u.y;
@@ -580,10 +584,10 @@ __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
         }
     }
     // ---- this wave's two tiles of the first block decoded (they wait for their own words only)
-    uint32_t cw[2][32];
+    uint32_t cw[TPW][32];
     auto decode_block = [&](int h) {
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
+        for (int kk = 0; kk < TPW; ++kk) {
 #pragma unroll
             for (int j = 0; j < K; ++j) __asm__ volatile("" : "+v"(wr[h][kk][j]));
             lane_words<K>(wr[h][kk], prev_word(wr[h][kk][K - 1], i), cw[kk]);
@@ -599,9 +603,9 @@ __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
             if (m < nr) {
                 float acc[2] = {0.f, 0.f};
 #pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
+                for (int kk = 0; kk < TPW; ++kk) {
                     uint32_t xd[16];
-                    load_tile_acts(&xs[m][(2 * wave + kk) * 16], xd);
+                    load_tile_acts(&xs[m][(TPW * wave + kk) * 16], xd);
                     tile_dot(cw[kk], xd, acc);
                 }
                 red[wave][m][128 * h + 16 * t + i] = acc[0];
@@ -612,14 +616,16 @@ __global__ void __launch_bounds__(256) down_gemv_kernel(const GemvArgs a) {
     __syncthreads();
     // ---- the four waves in order, then the down epilogue's transform and scale of this k block's part, a (member,
     // block) a wave
-    for (int q = wave; q < nr * HB; q += 4) {
+    for (int q = wave; q < nr * HB; q += NW) {
         const int m = q / HB, h = q - m * HB, ob = (hb * HB + h) * 128;
-        const uint32_t sv = q < 4 ? svd : *reinterpret_cast<const uint32_t*>(a.x1 + (size_t)e * a.N + ob + 2 * lane);
+        const uint32_t sv = q < NW ? svd : *reinterpret_cast<const uint32_t*>(a.x1 + (size_t)e * a.N + ob + 2 * lane);
         float v[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int c = 128 * h + 2 * lane + j;
-            v[j] = red[0][m][c] + red[1][m][c] + red[2][m][c] + red[3][m][c];
+            v[j] = red[0][m][c];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) v[j] += red[w][m][c];
         }
         fwht128_w64(v, lane);
         const int p = __builtin_amdgcn_readlane(pair_l, (c0 + m) & 63);
@@ -1008,17 +1014,21 @@ hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, int SKgu, 
     const int hbw = (D / 128) % 2 == 0 && D >= DOWN_HB2_MIN ? 2 : 1;
     // a one-token window routed inside the gate/up launch: one program a slot (TOKEN), no grouping tables
     const bool token = route != nullptr && SKgu <= 16;
+    // one-token windows: 2-wave workgroups (4 k tiles a wave, half the waves to launch) where a wave's share of the
+    // gate/up splits fits its 4 registers
+    const bool token2 = token && SKgu <= 8;
     if (token) {
         a.pick_out = route->picks;
         a.routed = route->routed;
     }
     const dim3 grid(token ? (unsigned)slots : chunks_x(maxu, rows < maxm ? rows : maxm, rb), D / 128 / hbw, N / 128);
 #define GFR_DOWN_HB(KB, HB)                                                                                       \
-    if (token) down_gemv_kernel<KB, 1, HB, true><<<grid, 256, 0, s>>>(a);                                          \
-    else if (rb == 1) down_gemv_kernel<KB, 1, HB, false><<<grid, 256, 0, s>>>(a);                                  \
-    else if (rb == 2) down_gemv_kernel<KB, 2, HB, false><<<grid, 256, 0, s>>>(a);                                  \
-    else if (rb == 4) down_gemv_kernel<KB, 4, HB, false><<<grid, 256, 0, s>>>(a);                                  \
-    else down_gemv_kernel<KB, 8, HB, false><<<grid, 256, 0, s>>>(a);
+    if (token2) down_gemv_kernel<KB, 1, HB, true, 2><<<grid, 128, 0, s>>>(a);                                     \
+    else if (token) down_gemv_kernel<KB, 1, HB, true, 4><<<grid, 256, 0, s>>>(a);                                  \
+    else if (rb == 1) down_gemv_kernel<KB, 1, HB, false, 4><<<grid, 256, 0, s>>>(a);                               \
+    else if (rb == 2) down_gemv_kernel<KB, 2, HB, false, 4><<<grid, 256, 0, s>>>(a);                               \
+    else if (rb == 4) down_gemv_kernel<KB, 4, HB, false, 4><<<grid, 256, 0, s>>>(a);                               \
+    else down_gemv_kernel<KB, 8, HB, false, 4><<<grid, 256, 0, s>>>(a);
 #define GFR_DOWN(KB)                                                                                              \
     case KB:                                                                                                    \
         if (hbw == 2) { GFR_DOWN_HB(KB, 2) } else { GFR_DOWN_HB(KB, 1) }                                          \
