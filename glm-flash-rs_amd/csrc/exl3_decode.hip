@@ -437,10 +437,10 @@ __device__ inline void xcd_grouped(int& bx, int& by, int& bz) {
     bz = g / (gy * gx);
 }
 
-template <int K, int RB, int HB, bool TOKEN, int NW>
+template <int K, int RB, int HB, bool TOKEN, int NW, int TZ = 4>
 __global__ void __launch_bounds__(NW * 64) down_gemv_kernel(const GemvArgs a) {
     constexpr int TPW = 8 / NW;                          // k tiles a wave of the 128-k block
-    static_assert(NW == 2 || NW == 4, "waves a workgroup");
+    static_assert(NW == 1 || NW == 4, "waves a workgroup");
     __shared__ __attribute__((aligned(16))) uint32_t xs[RB][128];   // the k block's activations, each twice
     __shared__ float red[NW][RB][128 * HB];
     __shared__ float2 psum[NW][RB][2][64];                           // each wave's share of the gate / up splits
@@ -474,20 +474,20 @@ __global__ void __launch_bounds__(NW * 64) down_gemv_kernel(const GemvArgs a) {
         psum[wave][m][1][lane] = u;
     };
     int e, nr, c0, pair_l;
-    constexpr int TZ = 4;                               // TOKEN: this wave's split partials, in flight
-    float2 tzg[TZ], tzu[TZ];
+    float2 tzg[TZ], tzu[TZ];                            // TOKEN: this wave's split partials, in flight
     if constexpr (TOKEN) {
         // a one-token window routed by the gate/up launch (RB 1): program bx is the token's slot bx, pair bx. The
         // slot's partials need no table, so they are loaded at once, next to the slot's expert (the shared expert,
         // id `routed` in the last slot, needs no load at all); only the trellis and scale loads wait for the id.
-        // (the host sends at most 4 NW splits here: a wave's share, at most 4, is held in registers)
+        // (TZ >= the wave's share of the splits, set by the host; every wave issues TZ loads, past its share
+        // re-reading its first split)
         const int slot = bx;
         c0 = 0;
         nr = 1;
         pair_l = slot;
 #pragma unroll
         for (int k = 0; k < TZ; ++k) {
-            const int kk = s0 + k < s1 ? s0 + k : 0;
+            const int kk = s0 + k < s1 ? s0 + k : (s0 < a.SKgu ? s0 : 0);
             tzg[k] = *reinterpret_cast<const float2*>(a.zgu + ((size_t)kk * a.P + slot) * a.Kin + n);
             tzu[k] = *reinterpret_cast<const float2*>(a.zgu + ((size_t)(a.SKgu + kk) * a.P + slot) * a.Kin + n);
         }
@@ -1014,17 +1014,22 @@ hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, int SKgu, 
     const int hbw = (D / 128) % 2 == 0 && D >= DOWN_HB2_MIN ? 2 : 1;
     // a one-token window routed inside the gate/up launch: one program a slot (TOKEN), no grouping tables
     const bool token = route != nullptr && SKgu <= 16;
-    // one-token windows: 2-wave workgroups (4 k tiles a wave, half the waves to launch) where a wave's share of the
-    // gate/up splits fits its 4 registers
-    const bool token2 = token && SKgu <= 8;
+    // One-token windows with at most 4 gate/up splits and one output block a workgroup (config 2's shape) run
+    // one-wave workgroups (all 8 k tiles of the block in the wave, a quarter of the waves to launch): the layer
+    // measured 18.43 against 18.53 (2 waves) and 18.69 us (4 waves) on one box. With more splits or two output blocks
+    // (config 5: 10 splits, hidden 5120) four waves share the work: 53.4 against 55.0 (2) and 57.4 us (1) a layer.
+    const bool one = token && SKgu <= 4 && hbw == 1;
+    const int tz = one ? SKgu : (SKgu + 3) / 4;         // a wave's share of the gate/up splits
     if (token) {
         a.pick_out = route->picks;
         a.routed = route->routed;
     }
     const dim3 grid(token ? (unsigned)slots : chunks_x(maxu, rows < maxm ? rows : maxm, rb), D / 128 / hbw, N / 128);
 #define GFR_DOWN_HB(KB, HB)                                                                                       \
-    if (token2) down_gemv_kernel<KB, 1, HB, true, 2><<<grid, 128, 0, s>>>(a);                                     \
-    else if (token) down_gemv_kernel<KB, 1, HB, true, 4><<<grid, 256, 0, s>>>(a);                                  \
+    if (one) down_gemv_kernel<KB, 1, HB, true, 1, 4><<<grid, 64, 0, s>>>(a);                                       \
+    else if (token && tz <= 1) down_gemv_kernel<KB, 1, HB, true, 4, 1><<<grid, 256, 0, s>>>(a);                   \
+    else if (token && tz <= 2) down_gemv_kernel<KB, 1, HB, true, 4, 2><<<grid, 256, 0, s>>>(a);                   \
+    else if (token) down_gemv_kernel<KB, 1, HB, true, 4, 4><<<grid, 256, 0, s>>>(a);                              \
     else if (rb == 1) down_gemv_kernel<KB, 1, HB, false, 4><<<grid, 256, 0, s>>>(a);                               \
     else if (rb == 2) down_gemv_kernel<KB, 2, HB, false, 4><<<grid, 256, 0, s>>>(a);                               \
     else if (rb == 4) down_gemv_kernel<KB, 4, HB, false, 4><<<grid, 256, 0, s>>>(a);                               \
