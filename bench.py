@@ -593,7 +593,7 @@ def main():
                                    "memory-side cache for the down launch: in this launch's time and traffic, not in "
                                    "bytes_per_launch (they are the down launch's operand bytes)",
                            "gbs_incl": round((nbytes["gate_up"] + read_ahead) / launches_us["gate_up"] / 1e3, 1)},
-            "down": {"kernel": "down_gemv_kernel<4,1>", "bytes_per_launch": nbytes["down"],
+            "down": {"kernel": "down_gemv_kernel<4,1,1,true,1,4> (one-wave workgroups: a slot, a 128-output block, a 128-k block)", "bytes_per_launch": nbytes["down"],
                      "us_per_launch": round(launches_us["down"], 3),
                      "gbs": round(nbytes["down"] / launches_us["down"] / 1e3, 1),
                      "frac": round(nbytes["down"] / launches_us["down"] / 1e3 / HBM_PEAK_GBS, 4)},
