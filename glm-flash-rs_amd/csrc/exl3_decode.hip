@@ -409,15 +409,17 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
 }
 
 // ---- down GEMV of the decode path ------------------------------------------------------------------------------
-// Program (chunk * ucap + distinct expert u, 128-column block hb of the hidden size, 128-k block kb of the
-// intermediate size), 4 waves. The k block's activations are the gate/up epilogue (exl3.cu:260-296) of its 128
-// intermediate values: the gate / up split partials summed in split order, transforms, svh scales, GLM's limited
-// SwiGLU with its bf16 roundings, suh_d, transform -> fp16 (stored to xd by the hb == 0 programs). Wave w builds the
-// epilogue of members w and w + 4 into LDS while every wave streams and decodes its own two k tiles (kb * 8 + 2w,
-// + 1) of the block's 8 column tiles into registers; after one barrier each wave dots its tiles, the four waves are
-// added in order and the k block's sum goes through the down epilogue's transform and svh_d scale (exl3.cu:300-321;
-// linear, so it applies to each k block's part) into Zd[kb][pair][hidden]. The finish launch adds the k blocks in
-// order. Every sum has a fixed order, and a row's result never depends on the other rows.
+// Program (unit, 128-column block hb of the hidden size, 128-k block kb of the intermediate size), NW waves. A unit is
+// (member chunk, distinct expert u) of the grouping tables, or with TOKEN (a one-token window routed by the gate/up
+// launch) the token's slot, whose expert is its pick and whose pair is the slot itself. The k block's activations are
+// the gate/up epilogue (exl3.cu:260-296) of its 128 intermediate values: the gate / up split partials summed in split
+// order, transforms, svh scales, GLM's limited SwiGLU with its bf16 roundings, suh_d, transform -> fp16 (stored to xd
+// by the hb == 0 programs). Wave w builds the epilogue of members w and w + NW into LDS while every wave streams and
+// decodes its own 8 / NW k tiles (kb * 8 + w * 8 / NW, ...) of the block's 8 column tiles into registers; after one
+// barrier each wave dots its tiles, the waves are added in order and the k block's sum goes through the down
+// epilogue's transform and svh_d scale (exl3.cu:300-321; linear, so it applies to each k block's part) into
+// Zd[kb][pair][hidden]. The finish launch adds the k blocks in order. Every sum has a fixed order, and a row's result
+// never depends on the other rows (NW, which sets the order of the waves' sums, is fixed by the shape and by TOKEN).
 //   a.Kin = intermediate size (the down input), a.N = hidden size; a.suh0 = suh_d, a.svh_g / svh_u the gate / up
 //   output scales, a.t0 the down trellis, a.zgu / SKgu the gate/up partials, a.z = Zd, a.x1 (reused) = svh_d.
 // hidden sizes from which a down workgroup covers two 128-output blocks
