@@ -83,3 +83,16 @@ def test_moe_create_rejects():
     assert L.gfr_moe_create(ctypes.byref(h), 2048, 1536, 64, 0, 1) == gfr_moe.GFR_EINVAL
     assert L.gfr_moe_create(ctypes.byref(h), 2048, 1536, 64, 65, 1) == gfr_moe.GFR_EINVAL
     assert L.gfr_moe_create(ctypes.byref(h), 2048, 1536, 2000, 4, 1) == gfr_moe.GFR_EINVAL
+
+
+@pytest.mark.parametrize("stride,ptr_off", [(2044, 0), (2048, 8)])
+def test_router_logits_row_alignment(stride, ptr_off):
+    """The logits kernel reads input and weight rows 16 bytes at a time: an input stride that is not a multiple of 8
+    or an input pointer off 16-byte alignment is refused before any device work."""
+    import gfr_moe
+    L = gfr_moe.lib()
+    x = ctypes.c_void_p(0x10000 + ptr_off)     # never dereferenced on the refused paths
+    w = ctypes.c_void_p(0x20000)
+    out = ctypes.c_void_p(0x30000)
+    rc = L.gfr_router_logits(None, x, stride, w, 2040, 64, 1, out)
+    assert rc == gfr_moe.GFR_EINVAL and "16-byte aligned" in L.gfr_last_error().decode()

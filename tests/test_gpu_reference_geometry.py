@@ -113,6 +113,9 @@ def test_moe_reference_layout_shared_output(gfr, oracle, weights, rows):
     shared = torch.randn((rows, D + 16), generator=g, device="cuda")    # a strided caller buffer
     m = gfr.Moe(D, N, E, topk, max(rows, 4), shared_exl3=False)
     m.set_router(bias, 2.5)
+    # the combine reads the shared rows 16 bytes at a time: a view one float in (4-byte aligned) is refused
+    with pytest.raises(gfr.GfrError, match="16-byte aligned"):
+        m.run_router(weights, x, router_w, rows, shared=shared[:, 1:])
     m.run_router(weights, x, router_w, rows, shared=shared)
     torch.cuda.synchronize()
     out = m.output[:rows].cpu().numpy()
