@@ -6,7 +6,8 @@ from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
-SOURCES = ["grouping.hip", "exl3_decode.hip", "exl3_prefill.hip", "router.hip", "gfr_moe_api.hip", "prepared.hip", "prefetch.hip"]
+SOURCES = ["grouping.hip", "exl3_decode.hip", "exl3_prefill.hip", "router.hip", "gfr_moe_api.hip", "prepared.hip", "prefetch.hip",
+           "shared_fp8.hip"]
 LIB = os.path.join(PKG, "libgfr_moe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

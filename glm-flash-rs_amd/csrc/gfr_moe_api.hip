@@ -111,6 +111,14 @@ struct gfr_moe {
                                // caller's (gfr_moe_run_shared), weights hold the routed experts only
     float* logits;             // [max_rows][routed] router logits of gfr_moe_run_router
     int launches;              // measurement: rows == 1 issues only the first `launches` launches (0: all)
+    gfr_shared_fp8* sfp8;      // shared_exl3 = 0: the FP8 shared expert's engine and output [max_rows][hidden]
+    float* shared_out;
+};
+
+struct gfr_shared_fp8 {
+    int hidden, inter, max_rows;
+    uint16_t* gu;    // [max_rows][2 inter] bf16
+    uint16_t* act;   // [max_rows][inter] bf16
 };
 
 extern "C" {
@@ -428,7 +436,7 @@ int gfr_moe_create_shared(gfr_moe** out, int hidden, int inter, int routed, int 
     gfr_moe* m = new gfr_moe{hidden, inter, routed, topk, topk + 1, max_rows,
                              MOE_DECODE_ROWS < max_rows ? MOE_DECODE_ROWS : max_rows,
                              nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 1.f,
-                             shared_exl3 ? 1 : 0, nullptr, 0};
+                             shared_exl3 ? 1 : 0, nullptr, 0, nullptr, nullptr};
     const int exl3_slots = shared_exl3 ? topk + 1 : topk, experts = shared_exl3 ? routed + 1 : routed;
     m->route_bias = nullptr;   // the softmax gate until gfr_moe_set_router
     m->route_scale = 1.f;
@@ -438,6 +446,13 @@ int gfr_moe_create_shared(gfr_moe** out, int hidden, int inter, int routed, int 
         (rc = alloc_zero(&m->logits, (size_t)max_rows * routed, "moe logits")) ||
         (rc = gfr_grouping_create(&m->group_dec, routed + 1, m->slots, dec_cap)) ||
         (rc = gfr_experts_create(&m->dec, hidden, inter, m->slots, exl3_slots, dec_cap))) {
+        gfr_moe_destroy(m);
+        return rc;
+    }
+    // the reference's layout: the FP8 shared expert's engine, for gfr_moe_run_fp8 / gfr_moe_run_router_fp8
+    if (!shared_exl3 && hidden % 512 == 0 &&
+        ((rc = gfr_shared_fp8_create(&m->sfp8, hidden, inter, max_rows)) ||
+         (rc = alloc_zero(&m->shared_out, (size_t)max_rows * hidden, "moe shared output")))) {
         gfr_moe_destroy(m);
         return rc;
     }
@@ -667,6 +682,101 @@ int gfr_moe_run_router(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w
     return moe_run(m, stream, w, input, m->logits, shared, shared_stride, rows);
 }
 
+// ---- the FP8 shared expert --------------------------------------------------------------------------------------
+namespace {
+bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+int check_fp8_weights(const gfr_fp8_shared_weights* w, int hidden, int inter) {
+    if (!w) return fail(GFR_EINVAL, "null FP8 shared weights");
+    if (w->hidden != hidden || w->inter != inter)
+        return fail(GFR_EINVAL, "FP8 shared weights %dx%d, engine %dx%d", w->hidden, w->inter, hidden, inter);
+    if (!w->gu || !w->gu_scale || !w->down || !w->down_scale) return fail(GFR_EINVAL, "null FP8 shared tensor");
+    if (!al16(w->gu) || !al16(w->gu_scale) || !al16(w->down) || !al16(w->down_scale))
+        return fail(GFR_EINVAL, "FP8 shared tensors must be 16-byte aligned");
+    return 0;
+}
+int shared_fp8_run(gfr_shared_fp8* sh, hipStream_t stream, const gfr_fp8_shared_weights* w, const uint16_t* input,
+                   int input_stride, int rows, float* out, int out_stride) {
+    if (!sh) return fail(GFR_EINVAL, "null FP8 shared engine");
+    int rc = check_fp8_weights(w, sh->hidden, sh->inter);
+    if (rc) return rc;
+    if (rows <= 0 || rows > sh->max_rows) return fail(GFR_EINVAL, "rows %d outside 1..%d", rows, sh->max_rows);
+    if (!input || !out) return fail(GFR_EINVAL, "null input or output");
+    // rows are read 16 bytes at a time and written 16 bytes at a time
+    if (input_stride < sh->hidden || input_stride % 8 || !al16(input))
+        return fail(GFR_EINVAL, "input stride %d: at least hidden %d, a multiple of 8, the pointer 16-byte aligned",
+                    input_stride, sh->hidden);
+    if (out_stride < sh->hidden || out_stride % 4 || !al16(out))
+        return fail(GFR_EINVAL, "output stride %d: at least hidden %d, a multiple of 4, the pointer 16-byte aligned",
+                    out_stride, sh->hidden);
+    hipError_t e = gfr::launch_shared_fp8(stream, w->gu, w->gu_scale, w->down, w->down_scale, input, input_stride,
+                                          rows, sh->hidden, sh->inter, sh->gu, sh->act, out, out_stride);
+    if (e != hipSuccess) return hip_fail(e, "FP8 shared expert");
+    return 0;
+}
+int moe_fp8_ready(gfr_moe* m, const gfr_fp8_shared_weights* sw) {
+    if (!m) return fail(GFR_EINVAL, "null moe");
+    if (m->shared_exl3 || !m->sfp8)
+        return fail(GFR_EINVAL, "the layer has no FP8 shared expert (made with shared_exl3 = 1, or hidden %d is not "
+                    "a multiple of 512)", m->hidden);
+    return check_fp8_weights(sw, m->hidden, m->inter);
+}
+}  // namespace
+
+int gfr_shared_fp8_create(gfr_shared_fp8** out, int hidden, int inter, int max_rows) {
+    if (!out) return fail(GFR_EINVAL, "null out");
+    *out = nullptr;
+    if (hidden <= 0 || hidden % 512 || hidden > (1 << 20) || inter <= 0 || inter % 64 || inter > (1 << 20))
+        return fail(GFR_EINVAL, "FP8 shared expert: hidden %d a multiple of 512, inter %d of 64", hidden, inter);
+    if (max_rows <= 0 || max_rows > (1 << 16)) return fail(GFR_EINVAL, "max_rows %d", max_rows);
+    gfr_shared_fp8* sh = new gfr_shared_fp8{hidden, inter, max_rows, nullptr, nullptr};
+    int rc;
+    if ((rc = alloc_zero(&sh->gu, (size_t)max_rows * 2 * inter, "FP8 shared gu")) ||
+        (rc = alloc_zero(&sh->act, (size_t)max_rows * inter, "FP8 shared activation"))) {
+        gfr_shared_fp8_destroy(sh);
+        return rc;
+    }
+    *out = sh;
+    return 0;
+}
+
+int gfr_shared_fp8_run(gfr_shared_fp8* sh, hipStream_t stream, const gfr_fp8_shared_weights* w,
+                       const uint16_t* input, int input_stride, int rows, float* out, int out_stride) {
+    return shared_fp8_run(sh, stream, w, input, input_stride, rows, out, out_stride);
+}
+
+uint16_t* gfr_shared_fp8_gu(const gfr_shared_fp8* sh) { return sh ? sh->gu : nullptr; }
+uint16_t* gfr_shared_fp8_act(const gfr_shared_fp8* sh) { return sh ? sh->act : nullptr; }
+
+int gfr_shared_fp8_destroy(gfr_shared_fp8* sh) {
+    if (!sh) return 0;
+    free_all({sh->gu, sh->act});
+    delete sh;
+    return 0;
+}
+
+int gfr_moe_run_fp8(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
+                    const float* logits, const gfr_fp8_shared_weights* sw, int rows) {
+    int rc = moe_fp8_ready(m, sw);
+    if (rc) return rc;
+    if (rows <= 0 || rows > m->max_rows) return fail(GFR_EINVAL, "rows %d outside 1..%d", rows, m->max_rows);
+    if ((rc = shared_fp8_run(m->sfp8, stream, sw, input, m->hidden, rows, m->shared_out, m->hidden))) return rc;
+    return moe_run(m, stream, w, input, logits, m->shared_out, m->hidden, rows);
+}
+
+int gfr_moe_run_router_fp8(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
+                           const uint16_t* router_weight, const gfr_fp8_shared_weights* sw, int rows) {
+    int rc = moe_fp8_ready(m, sw);
+    if (rc) return rc;
+    if (!input || !router_weight) return fail(GFR_EINVAL, "null input or router weight");
+    if (rows <= 0 || rows > m->max_rows) return fail(GFR_EINVAL, "rows %d outside 1..%d", rows, m->max_rows);
+    if ((rc = gfr_router_logits(stream, input, m->hidden, router_weight, m->hidden, m->routed, rows, m->logits)))
+        return rc;
+    if ((rc = shared_fp8_run(m->sfp8, stream, sw, input, m->hidden, rows, m->shared_out, m->hidden))) return rc;
+    return moe_run(m, stream, w, input, m->logits, m->shared_out, m->hidden, rows);
+}
+
+float* gfr_moe_shared_output(const gfr_moe* m) { return m ? m->shared_out : nullptr; }
+
 int gfr_router_logits(hipStream_t stream, const uint16_t* input, int input_stride, const uint16_t* router_weight,
                       int hidden, int routed, int rows, float* logits) {
     if (!input || !router_weight || !logits) return fail(GFR_EINVAL, "null argument");
@@ -709,7 +819,8 @@ int gfr_moe_destroy(gfr_moe* m) {
     gfr_grouping_destroy(m->group_pre);
     gfr_experts_destroy(m->dec);
     gfr_fast_experts_destroy(m->pre);
-    free_all({m->weights, m->picks, m->out, m->logits});
+    gfr_shared_fp8_destroy(m->sfp8);
+    free_all({m->weights, m->picks, m->out, m->logits, m->shared_out});
     delete m;
     return 0;
 }

@@ -103,4 +103,13 @@ int router_logits_max_hidden();
 hipError_t launch_router_logits(hipStream_t s, const uint16_t* x, int x_stride, const uint16_t* W, int D, int E,
                                 int rows, float* logits);
 
+// shared_fp8.hip
+// The reference's FP8 shared expert (moe.rs:132-167) for rows [rows][x_stride] bf16: gate/up (8 K slices, bf16 gu
+// [rows][2 inter], limited SwiGLU -> act [rows][inter] bf16), then down -> out [rows][out_stride] fp32. hidden a
+// multiple of 512, inter of 64; x, out, the weights and the scales 16-byte aligned, x_stride % 8 == 0,
+// out_stride % 4 == 0.
+hipError_t launch_shared_fp8(hipStream_t s, const uint8_t* wgu, const uint16_t* sgu, const uint8_t* wd,
+                             const uint16_t* sd, const uint16_t* x, int x_stride, int rows, int hidden, int inter,
+                             uint16_t* gu, uint16_t* act, float* out, int out_stride);
+
 }  // namespace gfr

@@ -769,6 +769,29 @@ int gfr_prepared_experts(const gfr_prepared* p, int layer, gfr_exl3_experts* out
     return 0;
 }
 
+int gfr_prepared_shared_fp8(const gfr_prepared* p, int layer, gfr_fp8_shared_weights* out) {
+    if (!p || !out || layer < 0) return err("bad arguments");
+    const std::string stem = "weights.layers[" + std::to_string(layer) + "].moe.shared.";
+    const Tensor* gu = find(p, (stem + "gu.weight").c_str());
+    if (!gu) return err("missing tensor " + stem + "gu.weight");
+    if (gu->shape.size() != 2 || gu->shape[0] % 2 || gu->shape[0] > (2u << 20) || gu->shape[1] > (1u << 20))
+        return err("unsupported tensor " + stem + "gu.weight");
+    const uint64_t I = gu->shape[0] / 2, H = gu->shape[1];
+    const struct { const char* name; const char* dtype; std::vector<uint64_t> shape; } want[] = {
+        {"gu.weight", "float8_e4m3fn", {2 * I, H}}, {"gu.scale", "bfloat16", {2 * I}},
+        {"down.weight", "float8_e4m3fn", {H, I}}, {"down.scale", "bfloat16", {H}}};
+    void* ptr[4];
+    for (int i = 0; i < 4; ++i) {
+        const std::string path = stem + want[i].name;
+        if (int rc = gfr_prepared_expect(p, path.c_str(), want[i].dtype, want[i].shape.data(), (int)want[i].shape.size()))
+            return rc;
+        if (int rc = gfr_prepared_pointer(p, path.c_str(), &ptr[i])) return rc;
+    }
+    *out = gfr_fp8_shared_weights{(int)H, (int)I, (const uint8_t*)ptr[0], (const uint16_t*)ptr[1],
+                                  (const uint8_t*)ptr[2], (const uint16_t*)ptr[3]};
+    return 0;
+}
+
 int gfr_prepared_destroy(gfr_prepared* p) {
     if (!p) return 0;
     release(p);

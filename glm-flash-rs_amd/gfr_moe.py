@@ -66,6 +66,15 @@ def _load() -> ctypes.CDLL:
         "gfr_moe_set_launches": ([VP, I], I),
         "gfr_moe_token_static": ([P, ctypes.POINTER(_Exl3Struct), I, I, P, P, P, P, P], I),
         "gfr_moe_destroy": ([VP], I),
+        "gfr_shared_fp8_create": ([ctypes.POINTER(VP), I, I, I], I),
+        "gfr_shared_fp8_run": ([VP, P, ctypes.POINTER(_Fp8Struct), P, I, I, P, I], I),
+        "gfr_shared_fp8_gu": ([VP], P),
+        "gfr_shared_fp8_act": ([VP], P),
+        "gfr_shared_fp8_destroy": ([VP], I),
+        "gfr_moe_run_fp8": ([VP, P, ctypes.POINTER(_Exl3Struct), P, P, ctypes.POINTER(_Fp8Struct), I], I),
+        "gfr_moe_run_router_fp8": ([VP, P, ctypes.POINTER(_Exl3Struct), P, P, ctypes.POINTER(_Fp8Struct), I], I),
+        "gfr_moe_shared_output": ([VP], P),
+        "gfr_prepared_shared_fp8": ([VP, I, ctypes.POINTER(_Fp8Struct)], I),
         "gfr_linear_create": ([ctypes.POINTER(VP), I, I, I], I),
         "gfr_linear_run": ([VP, P, P, P, P, P, P], I),
         "gfr_linear_destroy": ([VP], I),
@@ -135,11 +144,13 @@ class _DeviceArray:
                                          "version": 3, "strides": None}
 
 
-_TYPESTR = {torch.float32: "<f4", torch.int32: "<i4", torch.float16: "<f2"}
+_TYPESTR = {torch.float32: "<f4", torch.int32: "<i4", torch.float16: "<f2", torch.int16: "<i2", torch.uint8: "|u1"}
 
 
 def _view(ptr: int, shape, dtype, device) -> torch.Tensor:
     """A torch tensor over library-owned device memory (no copy; valid while the engine lives)."""
+    if dtype == torch.bfloat16:
+        return _view(ptr, shape, torch.int16, device).view(torch.bfloat16)
     t = torch.as_tensor(_DeviceArray(ptr, shape, _TYPESTR[dtype]), device=device)
     assert t.data_ptr() == ptr
     return t
@@ -198,6 +209,45 @@ class Exl3Experts:
 class _Exl3Struct(ctypes.Structure):
     _fields_ = [("experts", ctypes.c_int), ("hidden", ctypes.c_int), ("inter", ctypes.c_int), ("bits", ctypes.c_int)] + [
         (n, ctypes.c_void_p) for n in ("gt", "ut", "dt", "suh_g", "suh_u", "suh_d", "svh_g", "svh_u", "svh_d")]
+
+
+@dataclass
+class Fp8SharedWeights:
+    """The reference's FP8 shared expert, weights.layers[L].moe.shared.{gu,down}.{weight,scale} (moe.rs:136-161):
+    gu [2 inter, hidden] and down [hidden, inter] float8_e4m3fn bytes (torch.uint8 or torch.float8_e4m3fn),
+    gu_scale [2 inter] and down_scale [hidden] bf16; contiguous on the GPU, 16-byte aligned."""
+
+    gu: torch.Tensor
+    gu_scale: torch.Tensor
+    down: torch.Tensor
+    down_scale: torch.Tensor
+
+    @property
+    def hidden(self) -> int:
+        return self.gu.shape[1]
+
+    @property
+    def inter(self) -> int:
+        return self.gu.shape[0] // 2
+
+    def check(self):
+        H, I = self.hidden, self.inter
+        want = {"gu": (2 * I, H), "gu_scale": (2 * I,), "down": (H, I), "down_scale": (H,)}
+        for name, shape in want.items():
+            t = getattr(self, name)
+            ok_dtype = t.dtype == torch.bfloat16 if name.endswith("scale") else t.element_size() == 1
+            if tuple(t.shape) != shape or not ok_dtype or not t.is_contiguous() or t.device.type != "cuda":
+                raise ValueError(f"{name}: {tuple(t.shape)} {t.dtype}, want {shape} contiguous on GPU")
+
+    def struct(self) -> "_Fp8Struct":
+        self.check()
+        return _Fp8Struct(self.hidden, self.inter, *(_ptr(getattr(self, n))
+                                                     for n in ("gu", "gu_scale", "down", "down_scale")))
+
+
+class _Fp8Struct(ctypes.Structure):
+    _fields_ = [("hidden", ctypes.c_int), ("inter", ctypes.c_int)] + [
+        (n, ctypes.c_void_p) for n in ("gu", "gu_scale", "down", "down_scale")]
 
 
 class _Engine:
@@ -334,6 +384,29 @@ class Moe(_Engine):
         else:
             _check(lib().gfr_moe_run_shared(self._h, _stream(stream), ctypes.byref(ws), _ptr(input), _ptr(logits),
                                             _ptr(shared), shared.stride(0), rows))
+
+    def run_fp8(self, w: Exl3Experts, input: torch.Tensor, logits: torch.Tensor, sw: Fp8SharedWeights, rows: int,
+                stream=None):
+        """Moe::run_prefetched with its FP8 shared expert (a layer made with shared_exl3=False): the shared expert
+        into shared_output, then the routed layer and the combine."""
+        ws, ss = w.struct(), sw.struct()
+        _check(lib().gfr_moe_run_fp8(self._h, _stream(stream), ctypes.byref(ws), _ptr(input), _ptr(logits),
+                                     ctypes.byref(ss), rows))
+
+    def run_router_fp8(self, w: Exl3Experts, input: torch.Tensor, router_weight: torch.Tensor,
+                       sw: Fp8SharedWeights, rows: int, stream=None):
+        """run_fp8 with the router logits computed from the hidden rows first (router_weight [routed, hidden])."""
+        ws, ss = w.struct(), sw.struct()
+        _check(lib().gfr_moe_run_router_fp8(self._h, _stream(stream), ctypes.byref(ws), _ptr(input),
+                                            _ptr(router_weight), ctypes.byref(ss), rows))
+
+    @property
+    def shared_output(self) -> torch.Tensor:
+        """[max_rows, hidden] fp32: the FP8 shared expert's output of the last run_fp8 (shared_exl3=False)."""
+        p = lib().gfr_moe_shared_output(self._h)
+        if not p:
+            raise ValueError("the layer has no FP8 shared expert")
+        return _view(p, (self.max_rows, self.hidden), torch.float32, self.output.device)
 
     def run_router(self, w: Exl3Experts, input: torch.Tensor, router_weight: torch.Tensor, rows: int, stream=None,
                    shared: torch.Tensor = None):
@@ -663,6 +736,31 @@ def tensor_extent(dtype: str, shape, stride, off: int) -> int:
     return out.value
 
 
+class SharedFp8(_Engine):
+    """The reference's FP8 shared expert (moe.rs:132-167: shared_gu, reduce8_bf16, shared_swiglu, shared_down) in
+    two launches; gu [max_rows, 2 inter] and act [max_rows, inter] bf16 views of the last run's intermediates."""
+
+    _destroy = "gfr_shared_fp8_destroy"
+
+    def __init__(self, hidden: int, inter: int, max_rows: int, device="cuda"):
+        super().__init__()
+        _check(lib().gfr_shared_fp8_create(ctypes.byref(self._h), hidden, inter, max_rows))
+        self.hidden, self.inter, self.max_rows = hidden, inter, max_rows
+        self.gu = _view(lib().gfr_shared_fp8_gu(self._h), (max_rows, 2 * inter), torch.bfloat16, device)
+        self.act = _view(lib().gfr_shared_fp8_act(self._h), (max_rows, inter), torch.bfloat16, device)
+
+    def run(self, w: Fp8SharedWeights, input: torch.Tensor, rows: int, out: torch.Tensor = None, stream=None):
+        """input [rows, >= hidden] bf16 -> out [rows, >= hidden] fp32 (allocated when None; returned)."""
+        if input.dtype != torch.bfloat16:
+            raise ValueError("input must be bf16 [rows, stride]")
+        if out is None:
+            out = torch.empty((rows, self.hidden), dtype=torch.float32, device=input.device)
+        ws = w.struct()
+        _check(lib().gfr_shared_fp8_run(self._h, _stream(stream), ctypes.byref(ws), _ptr(input), input.stride(0),
+                                        rows, _ptr(out), out.stride(0)))
+        return out
+
+
 class Prepared(_Engine):
     """Prepared::open / tensor / expect / read_tensor / load_selected + Loaded::pointer (src/prepared.rs) over the
     library's loader. open and read_tensor need no GPU; load copies the selected storages into device memory."""
@@ -725,10 +823,23 @@ class Prepared(_Engine):
                            svh_u=v("svh_u", (E, N), torch.float16), svh_d=v("svh_d", (E, D), torch.float16), bits=b)
 
 
-def write_prepared(directory: str, layers, chunk: int = 64 << 20) -> str:
+    def shared_fp8(self, layer: int, device="cuda") -> Fp8SharedWeights:
+        """weights.layers[layer].moe.shared.* as Fp8SharedWeights of views into the loaded storages."""
+        st = _Fp8Struct()
+        _check(lib().gfr_prepared_shared_fp8(self._h, layer, ctypes.byref(st)))
+        H, I = st.hidden, st.inter
+        return Fp8SharedWeights(gu=_view(st.gu, (2 * I, H), torch.uint8, device),
+                                gu_scale=_view(st.gu_scale, (2 * I,), torch.bfloat16, device),
+                                down=_view(st.down, (H, I), torch.uint8, device),
+                                down_scale=_view(st.down_scale, (H,), torch.bfloat16, device))
+
+
+def write_prepared(directory: str, layers, chunk: int = 64 << 20, shared=None) -> str:
     """Write expert tensors in the reference's prepared format (src/prepared.rs:15-40): manifest.json + data.bin, one
     storage per tensor, tree weights.layers[L].moe.experts.{gt, ut, dt, suh_*, svh_*}, chunk hashes by hashlib.
-    `layers`: a list of Exl3Experts (or dicts name -> numpy array). Returns the manifest path (for Prepared)."""
+    `layers`: a list of Exl3Experts (or dicts name -> numpy array). `shared`: optionally, per layer, the FP8 shared
+    expert (Fp8SharedWeights or None) as weights.layers[L].moe.shared.{gu,down}.{weight,scale}. Returns the manifest
+    path (for Prepared)."""
     import hashlib
     import json
     names = ("gt", "ut", "dt", "suh_g", "suh_u", "suh_d", "svh_g", "svh_u", "svh_d")
@@ -737,28 +848,41 @@ def write_prepared(directory: str, layers, chunk: int = 64 << 20) -> str:
     storages, nodes, off = [], [], 0
     hashes, pending = [], bytearray()
     with open(data_path, "wb") as f:
-        for layer in layers:
-            fields = {}
-            for name in names:
-                t = layer[name] if isinstance(layer, dict) else getattr(layer, name)
-                arr = t.cpu().numpy() if isinstance(t, torch.Tensor) else t
-                blob = arr.tobytes()
+        def put(t):
+            nonlocal off, pending
+            if isinstance(t, torch.Tensor):
+                dtype = {torch.int32: "int32", torch.float16: "float16", torch.bfloat16: "bfloat16",
+                         torch.uint8: "float8_e4m3fn", torch.float8_e4m3fn: "float8_e4m3fn"}[t.dtype]
+                arr = t.contiguous().view(torch.int16 if t.element_size() == 2 else
+                                          torch.uint8 if t.element_size() == 1 else torch.int32).cpu().numpy()
+            else:
+                arr = t
                 dtype = {"int32": "int32", "float16": "float16"}[str(arr.dtype)]
-                shape = list(arr.shape)
-                stride, acc = [], 1
-                for n in reversed(shape):
-                    stride.insert(0, acc)
-                    acc *= n
-                fields[name] = {"T": len(storages), "dtype": dtype, "shape": shape, "stride": stride, "off": 0,
-                                "dev": "cuda"}
-                storages.append({"offset": off, "nbytes": len(blob), "dev": "cuda"})
-                f.write(blob)
-                off += len(blob)
-                pending += blob
-                while len(pending) >= chunk:
-                    hashes.append(hashlib.sha256(bytes(pending[:chunk])).hexdigest())
-                    del pending[:chunk]
-            nodes.append({"O": "Layer", "f": {"moe": {"O": "Moe", "f": {"experts": {"O": "Experts", "f": fields}}}}})
+            blob = arr.tobytes()
+            shape = list(arr.shape)
+            stride, acc = [], 1
+            for n in reversed(shape):
+                stride.insert(0, acc)
+                acc *= n
+            node = {"T": len(storages), "dtype": dtype, "shape": shape, "stride": stride, "off": 0, "dev": "cuda"}
+            storages.append({"offset": off, "nbytes": len(blob), "dev": "cuda"})
+            f.write(blob)
+            off += len(blob)
+            pending += blob
+            while len(pending) >= chunk:
+                hashes.append(hashlib.sha256(bytes(pending[:chunk])).hexdigest())
+                del pending[:chunk]
+            return node
+
+        for li, layer in enumerate(layers):
+            fields = {name: put(layer[name] if isinstance(layer, dict) else getattr(layer, name)) for name in names}
+            moe = {"experts": {"O": "Experts", "f": fields}}
+            sw = shared[li] if shared is not None else None
+            if sw is not None:
+                moe["shared"] = {"O": "Shared", "f": {
+                    "gu": {"O": "Fp8", "f": {"weight": put(sw.gu), "scale": put(sw.gu_scale)}},
+                    "down": {"O": "Fp8", "f": {"weight": put(sw.down), "scale": put(sw.down_scale)}}}}
+            nodes.append({"O": "Layer", "f": {"moe": {"O": "Moe", "f": moe}}})
     if pending:
         hashes.append(hashlib.sha256(bytes(pending)).hexdigest())
     manifest = {"format": 1, "file_size": off, "chunk": chunk, "chunk_sha256": hashes, "storages": storages,

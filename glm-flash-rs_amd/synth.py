@@ -9,7 +9,7 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-from gfr_moe import Exl3Experts
+from gfr_moe import Exl3Experts, Fp8SharedWeights
 
 
 def _gen(seed: int, device) -> torch.Generator:
@@ -38,6 +38,22 @@ def experts(E: int, hidden: int, inter: int, bits: int, seed: int = 1234, device
         suh_g=scales((E, D), seed + 4, device), suh_u=scales((E, D), seed + 5, device),
         suh_d=scales((E, N), seed + 6, device), svh_g=scales((E, N), seed + 7, device),
         svh_u=scales((E, N), seed + 8, device), svh_d=scales((E, D), seed + 9, device), bits=bits)
+
+
+def fp8_shared(hidden: int, inter: int, seed: int = 4321, device="cuda") -> Fp8SharedWeights:
+    """An FP8 shared expert of the reference's layout (moe.shared.{gu,down}.{weight,scale}): weights N(0, 16^2)
+    rounded to float8_e4m3fn (by torch, on the CPU), scales U(0.5, 1.5) / (16 sqrt(k)) in bf16, so that outputs of
+    N(0, 1) inputs are of order one."""
+    g = torch.Generator().manual_seed(seed)
+
+    def mat(n, k):
+        return (torch.randn((n, k), generator=g) * 16).to(torch.float8_e4m3fn).view(torch.uint8).to(device)
+
+    def sc(n, k):
+        return ((torch.rand(n, generator=g) + 0.5) / (16 * k ** 0.5)).to(torch.bfloat16).to(device)
+
+    return Fp8SharedWeights(gu=mat(2 * inter, hidden), gu_scale=sc(2 * inter, hidden) * 2,
+                            down=mat(hidden, inter), down_scale=sc(hidden, inter))
 
 
 def activations(rows: int, hidden: int, seed: int, device="cuda") -> torch.Tensor:

@@ -158,6 +158,45 @@ int gfr_moe_set_router(gfr_moe* m, const float* bias, float scale);
 int gfr_moe_set_launches(gfr_moe* m, int launches);
 int gfr_moe_destroy(gfr_moe* m);
 
+/* ---- The FP8 shared expert (moe.rs:132-167: shared_gu -> reduce8_bf16 -> shared_swiglu -> shared_down) -------
+ * The reference's weights.layers[L].moe.shared.{gu,down}.{weight,scale} (front.rs:319-342 shapes; float8_e4m3fn,
+ * OCP e4m3): gu [2 inter][hidden] (gate rows, then up rows), gu_scale [2 inter] bf16, down [hidden][inter],
+ * down_scale [hidden] bf16; every pointer 16-byte aligned.
+ * gfr_shared_fp8_run: input [rows][input_stride] bf16 -> out [rows][out_stride] fp32, in two launches:
+ *   gu[r][n]  = bf16(sum over 8 contiguous K slices, in order, of gu_scale[n] * fp32 sum of input[r][k] * W[n][k])
+ *               (the reference's fmm(shared_gu, sk = 8) + reduce8_bf16; its scalar oracle front.rs:190-217)
+ *   act[r][i] = bf16(bf16(g / (1 + exp(-g))) * u), g = min(gu[r][i], 10), u = clamp(gu[r][inter + i], -10, 10)
+ *               (shared_swiglu with limit 10; the formula of front.rs:669-675)
+ *   out[r][n] = down_scale[n] * fp32 sum of act[r][k] * Wd[n][k]      (fmm(shared_down, sk = 1), fp32 output)
+ * The sums inside a slice run in MFMA order, not the oracle's k order (within 1e-3 relative of it). hidden a multiple
+ * of 512, inter of 64; input_stride a multiple of 8, out_stride of 4, both row pointers 16-byte aligned. The
+ * reference's shared_swiglu also writes a `sums` buffer that nothing in the reference reads; it is not produced.
+ * gfr_shared_fp8_gu / _act: the engine's last gu [max_rows][2 inter] and act [max_rows][inter] (bf16). */
+typedef struct gfr_fp8_shared_weights {
+    int hidden;
+    int inter;
+    const uint8_t* gu;
+    const uint16_t* gu_scale;
+    const uint8_t* down;
+    const uint16_t* down_scale;
+} gfr_fp8_shared_weights;
+typedef struct gfr_shared_fp8 gfr_shared_fp8;
+int gfr_shared_fp8_create(gfr_shared_fp8** out, int hidden, int inter, int max_rows);
+int gfr_shared_fp8_run(gfr_shared_fp8* sh, hipStream_t stream, const gfr_fp8_shared_weights* w,
+                       const uint16_t* input, int input_stride, int rows, float* out, int out_stride);
+uint16_t* gfr_shared_fp8_gu(const gfr_shared_fp8* sh);
+uint16_t* gfr_shared_fp8_act(const gfr_shared_fp8* sh);
+int gfr_shared_fp8_destroy(gfr_shared_fp8* sh);
+/* Moe::run_prefetched with its FP8 shared expert (moe.rs:66-182), for a layer made with gfr_moe_create_shared(...,
+ * shared_exl3 = 0) and hidden a multiple of 512: the shared expert into the layer's own buffer
+ * (gfr_moe_shared_output, [max_rows][hidden] fp32), then gfr_moe_run_shared with it. _router_fp8 computes the router
+ * logits first, as gfr_moe_run_router. Input rows [rows][hidden] bf16, 16-byte aligned. */
+int gfr_moe_run_fp8(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
+                    const float* logits, const gfr_fp8_shared_weights* sw, int rows);
+int gfr_moe_run_router_fp8(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
+                           const uint16_t* router_weight, const gfr_fp8_shared_weights* sw, int rows);
+float* gfr_moe_shared_output(const gfr_moe* m);
+
 /* ---- The router alone (the reference's Triton topk, moe.rs:89-100; source absent, semantics of the benchmark):
  * logits [rows][routed] fp32 -> picks / weights [rows][topk + 1]: top-k by logit (ties: lower id), weights the
  * softmax over the k picks (summed in slot order), then the shared expert id `routed` with weight 1. */
@@ -268,6 +307,9 @@ int gfr_prepared_load(gfr_prepared* p, const char* const* prefixes, int nprefixe
 int gfr_prepared_loaded(const gfr_prepared* p, uint64_t* device_bytes, double* seconds);
 int gfr_prepared_pointer(const gfr_prepared* p, const char* path, void** device_ptr);
 int gfr_prepared_experts(const gfr_prepared* p, int layer, gfr_exl3_experts* out);
+/* The weights.layers[L].moe.shared.{gu,down}.{weight,scale} lookups of moe.rs:136-161 (float8_e4m3fn weights, bf16
+ * scales, any hidden / inter); GFR_EINVAL when a tensor is missing or has another dtype or shape. */
+int gfr_prepared_shared_fp8(const gfr_prepared* p, int layer, gfr_fp8_shared_weights* out);
 int gfr_prepared_destroy(gfr_prepared* p);
 /* The format's hash: lowercase hex SHA-256 (FIPS 180-4) of a host buffer into out65 (64 digits + NUL). */
 int gfr_sha256_hex(const void* data, uint64_t len, char* out65);

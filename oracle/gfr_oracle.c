@@ -386,3 +386,35 @@ double gfro_baseline_decode(const uint16_t* x_bf16, int D, int N, int bits, int 
     free(wg); free(wu); free(wd);
     return t;
 }
+
+/* ---- the FP8 shared expert (moe.rs:132-167) ---- */
+float gfro_fp8(uint8_t v) {
+    const int e = (v >> 3) & 15, m = v & 7;
+    const float sign = (v & 128) ? -1.f : 1.f;
+    if (e == 0) return sign * (float)m * ldexpf(1.f, -9);
+    return sign * (1.f + (float)m / 8.f) * ldexpf(1.f, e - 7);
+}
+
+void gfro_fp8_matmul(const float* x, const uint8_t* w, const uint16_t* scale_bf16, int k, int n, int sk, int round,
+                     float* y) {
+    for (int r = 0; r < n; ++r) {
+        const float s = gfro_bf16_to_f32(scale_bf16[r]);
+        float sum = 0.f;
+        for (int part = 0; part < sk; ++part) {
+            float acc = 0.f;
+            const long j0 = (long)part * k / sk, j1 = (long)(part + 1) * k / sk;
+            for (long j = j0; j < j1; ++j) acc += x[j] * gfro_fp8(w[(size_t)r * k + j]);
+            const float partial = acc * s;
+            sum = part == 0 ? partial : sum + partial;
+        }
+        y[r] = round ? gfro_bf(sum) : sum;
+    }
+}
+
+void gfro_shared_swiglu(const float* gu, int inter, float limit, float* act) {
+    for (int j = 0; j < inter; ++j) {
+        const float g = fminf(gu[j], limit);
+        const float u = fminf(fmaxf(gu[inter + j], -limit), limit);
+        act[j] = gfro_bf(gfro_bf(g / (1.f + expf(-g))) * u);
+    }
+}

@@ -79,6 +79,17 @@ void gfro_route_biased(const float* logits, const float* bias, float scale, int 
 /* out[r][n] = sum over slots in order of weights[r][s] * y[r*slots+s][n] */
 void gfro_combine(const float* y, const float* weights, int rows, int slots, int D, float* out);
 
+/* The FP8 shared expert (moe.rs:132-167) as the reference's scalar oracle states it.
+ * front.rs:173-182 fp8: an e4m3 byte -> f32 (exponent 0: m * 2^-9; else (1 + m / 8) * 2^(e - 7); 0x7f -> 480 as
+ * there, although the format calls it NaN). */
+float gfro_fp8(uint8_t v);
+/* front.rs:190-217 reference_mm_at: y[n] = sum over sk contiguous K slices (in order) of (the slice's sequential fp32
+ * sum of x[j] * fp8(w[n][j])) * bf16 scale[n]; round != 0: y rounded to bf16 (as a float). w [n][k] bytes. */
+void gfro_fp8_matmul(const float* x, const uint8_t* w, const uint16_t* scale_bf16, int k, int n, int sk, int round,
+                     float* y);
+/* front.rs:669-675: act[j] = bf(bf(g / (1 + exp(-g))) * u), g = min(gu[j], limit), u = clamp(gu[inter + j], +-limit) */
+void gfro_shared_swiglu(const float* gu, int inter, float limit, float* act);
+
 /* The CPU baseline of bench.py: decode + fp32 matvec of the given experts for one token, timed inside C
  * (experts.rs:43-96 path: unpack, codebook, fixed-order matmul). Returns seconds; writes y [n_exp][D]. */
 double gfro_baseline_decode(const uint16_t* x_bf16, int D, int N, int bits, int n_exp, const int32_t* experts,

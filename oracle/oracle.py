@@ -41,6 +41,8 @@ def _load():
         "gfro_group": ([P, I, I, I, I, P, P, P], I), "gfro_route": ([P, I, I, I, I, P, P], None),
         "gfro_route_biased": ([P, P, ctypes.c_float, I, I, I, I, P, P], None),
         "gfro_combine": ([P, P, I, I, I, P], None),
+        "gfro_fp8": ([ctypes.c_uint8], F), "gfro_fp8_matmul": ([P, P, P, I, I, I, I, P], None),
+        "gfro_shared_swiglu": ([P, I, F, P], None),
         "gfro_baseline_decode": ([P, I, I, I, I, P, P, P, P, P, P, P, P, P, P, P], ctypes.c_double),
     }
     for n, (a, r) in sigs.items():
@@ -195,6 +197,40 @@ def route_biased(logits, bias, scale, topk, shared_id):
     weights = np.empty((rows, topk + 1), np.float32)
     lib().gfro_route_biased(_p(l), _p(b), scale, rows, E, topk, shared_id, _p(picks), _p(weights))
     return picks, weights
+
+
+def fp8_values():
+    """front.rs:173-182: the value of every e4m3 byte 0..255."""
+    return np.array([lib().gfro_fp8(v) for v in range(256)], np.float32)
+
+
+def fp8_matmul(x, w, scale_bf16, sk, round_bf16):
+    """front.rs:190-217 reference_mm_at for one row x [k] (f32) against w [n][k] (uint8) with bf16 scales [n]."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.uint8)
+    sc = np.ascontiguousarray(scale_bf16, np.uint16)
+    n, k = w.shape
+    y = np.empty(n, np.float32)
+    lib().gfro_fp8_matmul(_p(x), _p(w), _p(sc), k, n, sk, 1 if round_bf16 else 0, _p(y))
+    return y
+
+
+def shared_swiglu(gu, inter, limit=10.0):
+    gu = np.ascontiguousarray(gu, np.float32)
+    act = np.empty(inter, np.float32)
+    lib().gfro_shared_swiglu(_p(gu), inter, limit, _p(act))
+    return act
+
+
+def shared_fp8_row(x_bf16, w_gu, s_gu, w_d, s_d):
+    """The FP8 shared expert for one token row as moe.rs:132-167 runs it: fmm(shared_gu, sk 8) + reduce8_bf16 ->
+    gu (bf16), shared_swiglu (limit 10) -> act (bf16), fmm(shared_down, sk 1) -> fp32. Returns (gu, act, out)."""
+    x = (np.asarray(x_bf16, np.uint16).astype(np.uint32) << 16).view(np.float32)
+    inter = w_gu.shape[0] // 2
+    gu = fp8_matmul(x, w_gu, s_gu, 8, True)
+    act = shared_swiglu(gu, inter)
+    out = fp8_matmul(act, w_d, s_d, 1, False)
+    return gu, act, out
 
 
 def combine(y, weights, rows, slots):

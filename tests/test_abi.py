@@ -96,3 +96,20 @@ def test_router_logits_row_alignment(stride, ptr_off):
     out = ctypes.c_void_p(0x30000)
     rc = L.gfr_router_logits(None, x, stride, w, 2040, 64, 1, out)
     assert rc == gfr_moe.GFR_EINVAL and "16-byte aligned" in L.gfr_last_error().decode()
+
+
+@pytest.mark.parametrize("args,needle", [((4000, 512, 1), "multiple of 512"), ((4096, 500, 1), "of 64"),
+                                         ((4096, 512, 0), "max_rows")])
+def test_shared_fp8_create_rejects(args, needle):
+    import gfr_moe
+    h = ctypes.c_void_p()
+    rc = gfr_moe.lib().gfr_shared_fp8_create(ctypes.byref(h), *args)
+    assert rc == gfr_moe.GFR_EINVAL and not h and needle in gfr_moe.lib().gfr_last_error().decode()
+
+
+def test_shared_fp8_run_rejects_null_and_moe_fp8_without_engine():
+    import gfr_moe
+    L = gfr_moe.lib()
+    assert L.gfr_shared_fp8_run(None, None, None, None, 4096, 1, None, 4096) == gfr_moe.GFR_EINVAL
+    assert L.gfr_moe_run_fp8(None, None, None, None, None, None, 1) == gfr_moe.GFR_EINVAL
+    assert L.gfr_moe_run_router_fp8(None, None, None, None, None, None, 1) == gfr_moe.GFR_EINVAL

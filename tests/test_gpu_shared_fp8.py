@@ -1,0 +1,193 @@
+"""The reference's FP8 shared expert (moe.rs:132-167: fmm(shared_gu, sk 8) -> reduce8_bf16 -> shared_swiglu ->
+fmm(shared_down, sk 1)) through gfr_shared_fp8 and the layer entry points gfr_moe_run_fp8 / _run_router_fp8, at the
+reference's geometry (hidden 4096, intermediate 512, 288 routed experts top-8 + the shared one), against the CPU
+oracle's restatement of the reference's scalar oracle (front.rs:190-217, 669-675). Weights are seeded synthetic
+tensors of the reference's shapes (its checkpoint is not available here)."""
+import numpy as np
+import pytest
+import torch
+
+from refs import DecodedExperts, assert_close, assert_rows_close, np_u16
+
+pytestmark = pytest.mark.gpu
+
+D, N, E, TOPK, BITS = 4096, 512, 288, 8, 4
+
+
+@pytest.fixture(scope="module")
+def sw():
+    import synth
+    return synth.fp8_shared(D, N, seed=77)
+
+
+@pytest.fixture(scope="module")
+def host_sw(sw):
+    return (sw.gu.cpu().numpy(), np_u16(sw.gu_scale), sw.down.cpu().numpy(), np_u16(sw.down_scale))
+
+
+def bf16_floats(u16):
+    return (np.asarray(u16, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def assert_bf16_ulps(got, want, what, max_frac=0.02):
+    """bf16 results whose fp32 sums were added in another order: equal, or one bf16 step apart (a sum that sits next
+    to a rounding boundary), and such steps rare."""
+    got, want = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    step = np.abs(want) * 2.0 ** -7 + 1e-30
+    diff = np.abs(got - want)
+    assert np.all(diff <= step), f"{what}: {int(np.sum(diff > step))} values more than one bf16 step apart"
+    frac = float(np.mean(diff > 0))
+    assert frac <= max_frac, f"{what}: {frac:.3%} of the values differ"
+
+
+@pytest.mark.parametrize("rows", [1, 3, 16, 17, 40])
+def test_shared_fp8_vs_oracle(gfr, oracle, sw, host_sw, rows):
+    """Every row: gu (bf16) against reference_mm_at(sk 8, rounded), act against the SwiGLU of the kernel's own gu,
+    out against reference_mm_at(sk 1) of the kernel's own act (the fp32 sums within their accumulation error), and
+    the whole chain from x against the oracle's chain. 17 and 40 rows take partial 16-row blocks; the input has a
+    padded row stride."""
+    g = torch.Generator(device="cuda").manual_seed(rows)
+    xs = torch.randn((rows, D + 24), generator=g, device="cuda").to(torch.bfloat16)
+    x = xs[:, :D]
+    sh = gfr.SharedFp8(D, N, 64)
+    out = torch.full((rows, D + 8), float("nan"), device="cuda")
+    sh.run(sw, x, rows, out=out)
+    torch.cuda.synchronize()
+    wgu, sgu, wd, sd = host_sw
+    xb = np_u16(x)
+    gu_k = bf16_floats(np_u16(sh.gu[:rows]))
+    act_k = bf16_floats(np_u16(sh.act[:rows]))
+    out_k = out[:, :D].cpu().numpy()
+    assert np.all(np.isnan(out[:, D:].cpu().numpy())), "columns past hidden must stay untouched"
+    wdv = oracle.fp8_values().astype(np.float64)[wd]
+    sdv = bf16_floats(sd).astype(np.float64)
+    chain = []
+    for r in range(rows):
+        gu_o, act_o, out_o = oracle.shared_fp8_row(xb[r], wgu, sgu, wd, sd)
+        assert_bf16_ulps(gu_k[r], gu_o, f"rows {rows} row {r} gu")
+        assert_bf16_ulps(act_k[r], oracle.shared_swiglu(gu_k[r], N), f"rows {rows} row {r} act", max_frac=0.01)
+        want = oracle.fp8_matmul(act_k[r], wd, sd, 1, False)
+        bound = (np.abs(wdv) @ np.abs(act_k[r]).astype(np.float64)) * sdv * N * 2.0 ** -23 + 1e-30
+        assert np.all(np.abs(out_k[r] - want) <= bound), f"rows {rows} row {r} out"
+        chain.append(out_o)
+    assert_rows_close(out_k, np.stack(chain), rel_rms=1e-2, rel_max=5e-2, what=f"rows {rows} x -> out chain")
+
+
+def test_shared_fp8_limit_clamps(gfr, oracle, host_sw):
+    """Gate / up values far beyond the limit of 10 (scales x 64): the SwiGLU saturates as the oracle's does."""
+    import synth
+    big = synth.fp8_shared(D, N, seed=78)
+    big.gu_scale = (big.gu_scale.float() * 64).to(torch.bfloat16)
+    x = torch.randn((2, D), generator=torch.Generator(device="cuda").manual_seed(3), device="cuda").to(torch.bfloat16)
+    sh = gfr.SharedFp8(D, N, 2)
+    sh.run(big, x, 2)
+    torch.cuda.synchronize()
+    gu_k = bf16_floats(np_u16(sh.gu[:2]))
+    assert np.mean(np.abs(gu_k) > 10) > 0.2, "the test needs values beyond the limit"
+    for r in range(2):
+        assert_bf16_ulps(bf16_floats(np_u16(sh.act[r])), oracle.shared_swiglu(gu_k[r], N), f"row {r} act",
+                         max_frac=0.01)
+
+
+def test_shared_fp8_graph_replays(gfr, sw):
+    """Captured and replayed, the two launches give the eager bytes (no allocation, no host sync in run)."""
+    x = torch.randn((5, D), generator=torch.Generator(device="cuda").manual_seed(9), device="cuda").to(torch.bfloat16)
+    sh = gfr.SharedFp8(D, N, 8)
+    out = torch.zeros((5, D), device="cuda")
+    sh.run(sw, x, 5, out=out)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    s = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            sh.run(sw, x, 5, out=out, stream=s)
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
+def test_shared_fp8_rejects_misaligned(gfr, sw):
+    sh = gfr.SharedFp8(D, N, 2)
+    x = torch.zeros((2, D + 8), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(gfr.GfrError, match="16-byte aligned"):
+        sh.run(sw, x[:, 1:], 2)
+    out = torch.zeros((2, D + 4), device="cuda")
+    with pytest.raises(gfr.GfrError, match="16-byte aligned"):
+        sh.run(sw, x[:, :D], 2, out=out[:, 1:])
+
+
+@pytest.fixture(scope="module")
+def routed():
+    import synth
+    return synth.experts(E, D, N, BITS, seed=288)
+
+
+@pytest.mark.parametrize("rows", [1, 3, 40])
+def test_moe_run_fp8_reference_layout(gfr, oracle, sw, host_sw, routed, rows):
+    """Moe::run_prefetched with its FP8 shared expert: the layer's output equals the combine of the routed experts
+    with the shared expert's own output (byte for byte against gfr_moe_run_shared fed with gfr_shared_fp8's output),
+    and sampled tokens match the oracle's routed rows + shared row combined."""
+    g = torch.Generator(device="cuda").manual_seed(500 + rows)
+    x = torch.randn((rows, D), generator=g, device="cuda").to(torch.bfloat16)
+    router_w = (torch.randn((E, D), generator=g, device="cuda") * 0.05).to(torch.bfloat16)
+    bias = torch.randn(E, generator=g, device="cuda") * 0.05
+    m = gfr.Moe(D, N, E, TOPK, max(rows, 4), shared_exl3=False)
+    m.set_router(bias, 2.5)
+    m.run_router_fp8(routed, x, router_w, sw, rows)
+    torch.cuda.synchronize()
+    got = m.output[:rows].clone()
+    shared = m.shared_output[:rows].clone()
+    sh = gfr.SharedFp8(D, N, rows)
+    torch.testing.assert_close(sh.run(sw, x, rows), shared, rtol=0, atol=0)
+    m2 = gfr.Moe(D, N, E, TOPK, max(rows, 4), shared_exl3=False)
+    m2.set_router(bias, 2.5)
+    m2.run_router(routed, x, router_w, rows, shared=shared)
+    torch.cuda.synchronize()
+    assert torch.equal(m2.output[:rows], got)
+    # with the logits given (gfr_moe_run_fp8): the same bytes
+    logits = gfr.router_logits(x, router_w)
+    m.output.zero_()
+    m.run_fp8(routed, x, logits, sw, rows)
+    torch.cuda.synchronize()
+    assert torch.equal(m.output[:rows], got)
+    # sampled tokens against the oracle: routed rows (the reference's fp16 weights) + the oracle's shared row
+    gp, gw = m.picks[:rows].cpu().numpy(), m.weights[:rows].cpu().numpy()
+    assert np.all(gp[:, TOPK] == E)
+    dec = DecodedExperts(oracle, routed, rounded=rows > 4)
+    xb = np_u16(x)
+    wgu, sgu, wd, sd = host_sw
+    for r in sorted({0, rows - 1}):
+        ys = [dec.row(xb[r], int(e))[0] if rows <= 4 else dec.row(xb[r], int(e), sk_gu=1, sk_d=1, warps=1)[0]
+              for e in gp[r, :TOPK]]
+        ys.append(oracle.shared_fp8_row(xb[r], wgu, sgu, wd, sd)[2])
+        want = oracle.combine(np.stack(ys), gw[r:r + 1], 1, TOPK + 1)[0]
+        assert_close(got[r].cpu().numpy(), want, rel_rms=1e-2, rel_max=5e-2, what=f"rows {rows} token {r}")
+
+
+def test_prepared_shared_fp8(gfr, sw, routed, tmp_path):
+    """The prepared-weight format carries the shared expert (weights.layers[L].moe.shared.{gu,down}.{weight,scale},
+    float8_e4m3fn / bfloat16); gfr_prepared_shared_fp8 finds it and the loaded tensors give the same output."""
+    import synth
+    small = synth.experts(4, 512, 256, BITS, seed=3)
+    sw_small = synth.fp8_shared(512, 256, seed=5)
+    path = gfr.write_prepared(str(tmp_path / "p"), [small], shared=[sw_small])
+    p = gfr.Prepared(path)
+    p.expect("weights.layers[0].moe.shared.gu.weight", "float8_e4m3fn", [512, 512])
+    p.expect("weights.layers[0].moe.shared.down.scale", "bfloat16", [512])
+    p.load()
+    loaded = p.shared_fp8(0)
+    assert loaded.hidden == 512 and loaded.inter == 256
+    assert torch.equal(loaded.gu, sw_small.gu) and torch.equal(loaded.down_scale, sw_small.down_scale)
+    x = torch.randn((3, 512), generator=torch.Generator(device="cuda").manual_seed(1), device="cuda").to(torch.bfloat16)
+    sh = gfr.SharedFp8(512, 256, 3)
+    a = sh.run(loaded, x, 3)
+    b = sh.run(sw_small, x, 3)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    with pytest.raises(gfr.GfrError):
+        p.shared_fp8(1)

@@ -421,3 +421,65 @@ def test_window_reference_matches_expert_row(oracle):
     want = np.stack([np.stack([dec.row(xb[r], int(picks[r, s]), sk_gu=1, sk_d=1, warps=1)[0] for s in range(2)])
                      for r in range(rows)])
     assert_rows_close(y[:, :2], want, what="window reference")
+
+
+# ---- the FP8 shared expert (moe.rs:132-167) ----------------------------------------------------------------------
+def test_fp8_values_reference_cases_and_torch(oracle):
+    """front.rs:716-722 known answers, and every non-NaN e4m3 byte against torch's float8_e4m3fn conversion (an
+    independent decoder); the NaN codes 0x7f / 0xff decode to +-480 as front.rs:173-182 computes them."""
+    v = oracle.fp8_values()
+    assert v[0x38] == 1.0 and v[0xB8] == -1.0 and v[0x7E] == 448.0 and v[0x01] == 1.0 / 512.0
+    codes = np.array([c for c in range(256) if c not in (0x7F, 0xFF)], np.uint8)
+    want = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    np.testing.assert_array_equal(v[codes], want)
+    assert v[0x7F] == 480.0 and v[0xFF] == -480.0
+
+
+@pytest.mark.parametrize("sk", [1, 8])
+def test_fp8_matmul_vs_float64(oracle, sk):
+    """reference_mm_at (front.rs:190-217) within fp32 accumulation error of the float64 product, every output row,
+    with and without the bf16 rounding; a transposed operand, a dropped slice or a wrong scale index fails it."""
+    rng = np.random.default_rng(5 + sk)
+    n, k = 48, 1024
+    w = rng.integers(0, 256, (n, k), dtype=np.uint8)
+    w[(w & 0x7F) == 0x7F] = 0x38
+    x = torch.from_numpy(rng.standard_normal(k).astype(np.float32)).to(torch.bfloat16).float().numpy()
+    sc = torch.from_numpy((rng.random(n) + 0.5).astype(np.float32) / 64).to(torch.bfloat16)
+    s64 = sc.float().numpy().astype(np.float64)
+    wv = oracle.fp8_values().astype(np.float64)[w]
+    y64 = (wv @ x.astype(np.float64)) * s64
+    bound = (np.abs(wv) @ np.abs(x).astype(np.float64)) * s64 * k * 2.0 ** -23
+    y = oracle.fp8_matmul(x, w, sc.view(torch.int16).numpy().view(np.uint16), sk, False)
+    assert np.all(np.abs(y - y64) <= bound), np.max(np.abs(y - y64) / bound)
+    yr = oracle.fp8_matmul(x, w, sc.view(torch.int16).numpy().view(np.uint16), sk, True)
+    np.testing.assert_array_equal(yr, torch.from_numpy(y).to(torch.bfloat16).float().numpy())
+
+
+def test_fp8_matmul_exact_slices(oracle):
+    """Integer weights and activations with a power-of-two scale: every product and partial sum is exact in fp32, so
+    the slice sums, the scale and the ordered sum of slices must reproduce the float64 result bit for bit."""
+    rng = np.random.default_rng(11)
+    n, k, sk = 16, 512, 8
+    codes = np.array([0x38, 0x40, 0x44, 0x48, 0xB8, 0xC0, 0x00], np.uint8)   # 1, 2, 3, 4, -1, -2, 0
+    w = codes[rng.integers(0, len(codes), (n, k))]
+    x = rng.integers(-3, 4, k).astype(np.float32)
+    sc = np.full(n, 0x3E80, np.uint16)                                        # bf16 0.25
+    y = oracle.fp8_matmul(x, w, sc, sk, False)
+    wv = oracle.fp8_values().astype(np.float64)[w]
+    np.testing.assert_array_equal(y, ((wv @ x.astype(np.float64)) * 0.25).astype(np.float32))
+
+
+def test_shared_swiglu_closed_form(oracle):
+    """front.rs:669-675: act = bf16(bf16(silu(min(g, 10))) * clamp(u, -10, 10)) against the float64 formula to one
+    bf16 rounding, including gate values above the limit and up values beyond +-limit."""
+    inter = 64
+    g = np.concatenate([np.linspace(-12, 12, 48), [10.0, 10.5, 30.0, -30.0] * 4]).astype(np.float32)
+    u = np.concatenate([np.linspace(-14, 14, 48), [15.0, -15.0, 9.5, -9.75] * 4]).astype(np.float32)
+    act = oracle.shared_swiglu(np.concatenate([g, u]), inter)
+    gg = np.minimum(g.astype(np.float64), 10.0)
+    uu = np.clip(u.astype(np.float64), -10.0, 10.0)
+    want = gg / (1 + np.exp(-gg)) * uu
+    np.testing.assert_allclose(act, want, rtol=2 * 2.0 ** -8, atol=1e-30)
+    # above the limit the gate saturates at silu(10): g = 10.5 and g = 30 give the act of g = 10
+    np.testing.assert_array_equal(oracle.shared_swiglu(np.array([10.0, 30.0, 2.0, 2.0], np.float32), 2),
+                                  oracle.shared_swiglu(np.array([10.0, 10.0, 2.0, 2.0], np.float32), 2))

@@ -212,3 +212,23 @@ def test_package_writer_round_trip(tmp_path):
             t = p.tensor(path)
             assert list(t.shape[:t.rank]) == list(layer[n].shape)
     p.close()
+
+
+def test_shared_fp8_tensors_round_trip(tmp_path):
+    """write_prepared carries the FP8 shared expert as weights.layers[L].moe.shared.{gu,down}.{weight,scale}
+    (float8_e4m3fn bytes, bfloat16 scales, the shapes moe.rs:136-161 reads); the reader finds them and returns their
+    bytes, without a GPU."""
+    import torch
+    import synth
+    small = synth.experts(2, 512, 256, 4, seed=3, device="cpu")
+    sw = synth.fp8_shared(512, 256, seed=5, device="cpu")
+    p = gfr_moe.Prepared(gfr_moe.write_prepared(str(tmp_path / "p"), [small], shared=[sw]))
+    stem = "weights.layers[0].moe.shared."
+    assert sorted(n for n in p.names() if n.startswith(stem)) == [
+        stem + "down.scale", stem + "down.weight", stem + "gu.scale", stem + "gu.weight"]
+    p.expect(stem + "gu.weight", "float8_e4m3fn", [512, 512])
+    p.expect(stem + "gu.scale", "bfloat16", [512])
+    p.expect(stem + "down.weight", "float8_e4m3fn", [512, 256])
+    p.expect(stem + "down.scale", "bfloat16", [512])
+    assert p.read_tensor(stem + "down.weight") == sw.down.numpy().tobytes()
+    assert p.read_tensor(stem + "gu.scale") == sw.gu_scale.view(torch.int16).numpy().tobytes()
