@@ -47,7 +47,9 @@ __device__ __forceinline__ void fp8_fragments(const uint4 w, bf8_t& f0, bf8_t& f
 // One lane's share of an fp8 row segment times a bf16 token row: chunks c = 0 .. nch - 1 of 64 k, the lane's
 // 16 k at 64 c + 16 q of each; w and x point at the lane's first k. Eight chunks' loads are issued before their
 // MFMAs.
-__device__ __forceinline__ f4_t fp8_chain(const uint8_t* __restrict__ w, const uint16_t* __restrict__ x, int nch) {
+// wok / xok: the lane's weight row / token row exists (a missing one feeds zeros and loads nothing).
+__device__ __forceinline__ f4_t fp8_chain(const uint8_t* __restrict__ w, const uint16_t* __restrict__ x, int nch,
+                                          bool wok, bool xok) {
     constexpr int G = 8;
     f4_t acc = {0.f, 0.f, 0.f, 0.f};
     for (int c0 = 0; c0 < nch; c0 += G) {
@@ -55,9 +57,12 @@ __device__ __forceinline__ f4_t fp8_chain(const uint8_t* __restrict__ w, const u
 #pragma unroll
         for (int k = 0; k < G; ++k)
             if (c0 + k < nch) {
-                wv[k] = *reinterpret_cast<const uint4*>(w + 64 * (c0 + k));
-                x0[k] = *reinterpret_cast<const uint4*>(x + 64 * (c0 + k));
-                x1[k] = *reinterpret_cast<const uint4*>(x + 64 * (c0 + k) + 8);
+                wv[k] = x0[k] = x1[k] = make_uint4(0u, 0u, 0u, 0u);
+                if (wok) wv[k] = *reinterpret_cast<const uint4*>(w + 64 * (c0 + k));
+                if (xok) {
+                    x0[k] = *reinterpret_cast<const uint4*>(x + 64 * (c0 + k));
+                    x1[k] = *reinterpret_cast<const uint4*>(x + 64 * (c0 + k) + 8);
+                }
             }
 #pragma unroll
         for (int k = 0; k < G; ++k)
@@ -71,28 +76,36 @@ __device__ __forceinline__ f4_t fp8_chain(const uint8_t* __restrict__ w, const u
     return acc;
 }
 
-// Program (8-index block j of the intermediate size, 16-row block rb); wave s = K slice s.
+// Program (IDX-index block j of the intermediate size, 16-row block rb); wave s = K slice s. The A tile's rows 0..7
+// are gate rows, 8..15 up rows, of which the first IDX are the block's (IDX < 8: fewer weight bytes a workgroup and
+// more workgroups, for windows of a few rows, whose weight reads are spread over more CUs).
+template <int IDX>
 __global__ void __launch_bounds__(64 * FP8_SLICES) shared_gu_kernel(
     const uint8_t* __restrict__ w, const uint16_t* __restrict__ scale, const uint16_t* __restrict__ x, int x_stride,
     int rows, int hidden, int inter, uint16_t* __restrict__ gu, uint16_t* __restrict__ act) {
+    static_assert(IDX == 2 || IDX == 4 || IDX == 8, "indices a workgroup");
     __shared__ float part[FP8_SLICES][16][17];
     const int j = blockIdx.x, rb = blockIdx.y;
     const int s = threadIdx.x >> 6, lane = threadIdx.x & 63, a = lane & 15, q = lane >> 4;
     const int L = hidden / FP8_SLICES;                       // a slice's k
-    const int wrow = a < 8 ? 8 * j + a : inter + 8 * j + a - 8;
+    const int ia = a & 7;
+    const int wrow = (a < 8 ? 0 : inter) + IDX * j + ia;
     const int row = rb * 16 + a, rowc = row < rows ? row : rows - 1;
-    const f4_t acc = fp8_chain(w + (size_t)wrow * hidden + s * L + 16 * q,
-                               x + (size_t)rowc * x_stride + s * L + 16 * q, L / 64);
-    // D: weight row 4 q + e of the tile, token row a of the block; the slice's sum times the row's scale
+    // D holds weight rows 4 q + e of the tile: their scales, loaded with the operands
+    float sc[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        const int t = 4 * q + e;
-        const int n = t < 8 ? 8 * j + t : inter + 8 * j + t - 8;
-        part[s][t][a] = acc[e] * bf16_to_f32(scale[n]);
+        const int it = 4 * (q & 1) + e;
+        sc[e] = it < IDX ? bf16_to_f32(scale[(q < 2 ? 0 : inter) + IDX * j + it]) : 0.f;
     }
+    const f4_t acc = fp8_chain(w + (size_t)(ia < IDX ? wrow : 0) * hidden + s * L + 16 * q,
+                               x + (size_t)rowc * x_stride + s * L + 16 * q, L / 64, ia < IDX, row < rows);
+    // D: weight row 4 q + e of the tile, token row a of the block; the slice's sum times the row's scale
+#pragma unroll
+    for (int e = 0; e < 4; ++e) part[s][4 * q + e][a] = acc[e] * sc[e];
     __syncthreads();
-    if (threadIdx.x < 128) {
-        const int i = threadIdx.x & 7, r = threadIdx.x >> 3, orow = rb * 16 + r;
+    if (threadIdx.x < 16 * IDX) {
+        const int i = threadIdx.x % IDX, r = threadIdx.x / IDX, orow = rb * 16 + r;
         float g = part[0][i][r], u = part[0][8 + i][r];
 #pragma unroll
         for (int p = 1; p < FP8_SLICES; ++p) {
@@ -101,12 +114,12 @@ __global__ void __launch_bounds__(64 * FP8_SLICES) shared_gu_kernel(
         }
         if (orow < rows) {
             const float gb = bf16r(g), ub = bf16r(u);
-            gu[(size_t)orow * 2 * inter + 8 * j + i] = (uint16_t)(__builtin_bit_cast(uint32_t, gb) >> 16);
-            gu[(size_t)orow * 2 * inter + inter + 8 * j + i] = (uint16_t)(__builtin_bit_cast(uint32_t, ub) >> 16);
+            gu[(size_t)orow * 2 * inter + IDX * j + i] = (uint16_t)(__builtin_bit_cast(uint32_t, gb) >> 16);
+            gu[(size_t)orow * 2 * inter + inter + IDX * j + i] = (uint16_t)(__builtin_bit_cast(uint32_t, ub) >> 16);
             const float gg = fminf(gb, SHARED_LIMIT);
             const float uu = __builtin_amdgcn_fmed3f(ub, -SHARED_LIMIT, SHARED_LIMIT);
             const float v = bf16r(bf16r(gg / (1.f + expf(-gg))) * uu);
-            act[(size_t)orow * inter + 8 * j + i] = (uint16_t)(__builtin_bit_cast(uint32_t, v) >> 16);
+            act[(size_t)orow * inter + IDX * j + i] = (uint16_t)(__builtin_bit_cast(uint32_t, v) >> 16);
         }
     }
 }
@@ -118,11 +131,11 @@ __global__ void __launch_bounds__(64) shared_down_kernel(const uint8_t* __restri
                                                         int inter, float* __restrict__ out, int out_stride) {
     const int nt = blockIdx.x, rb = blockIdx.y, lane = threadIdx.x, a = lane & 15, q = lane >> 4;
     const int row = rb * 16 + a, rowc = row < rows ? row : rows - 1;
+    const int n = 16 * nt + 4 * q;
+    const uint2 sc = *reinterpret_cast<const uint2*>(scale + n);
     const f4_t acc = fp8_chain(w + (size_t)(16 * nt + a) * inter + 16 * q, act + (size_t)rowc * inter + 16 * q,
-                               inter / 64);
+                               inter / 64, true, row < rows);
     if (row < rows) {
-        const int n = 16 * nt + 4 * q;
-        const uint2 sc = *reinterpret_cast<const uint2*>(scale + n);
         const float4 v = make_float4(acc[0] * bf16_to_f32((uint16_t)sc.x), acc[1] * bf16_to_f32((uint16_t)(sc.x >> 16)),
                                      acc[2] * bf16_to_f32((uint16_t)sc.y), acc[3] * bf16_to_f32((uint16_t)(sc.y >> 16)));
         *reinterpret_cast<float4*>(out + (size_t)row * out_stride + n) = v;
@@ -134,8 +147,14 @@ hipError_t launch_shared_fp8(hipStream_t s, const uint8_t* wgu, const uint16_t* 
                              const uint16_t* sd, const uint16_t* x, int x_stride, int rows, int hidden, int inter,
                              uint16_t* gu, uint16_t* act, float* out, int out_stride) {
     const int rblocks = (rows + 15) / 16;
-    shared_gu_kernel<<<dim3(inter / 8, rblocks), 64 * FP8_SLICES, 0, s>>>(wgu, sgu, x, x_stride, rows, hidden, inter,
-                                                                         gu, act);
+    // a few rows: two intermediate indices a workgroup (the weights over 4x the CUs); more: eight (the token rows
+    // are read by 4x fewer workgroups)
+    if (rows <= 4)
+        shared_gu_kernel<2><<<dim3(inter / 2, rblocks), 64 * FP8_SLICES, 0, s>>>(wgu, sgu, x, x_stride, rows, hidden,
+                                                                               inter, gu, act);
+    else
+        shared_gu_kernel<8><<<dim3(inter / 8, rblocks), 64 * FP8_SLICES, 0, s>>>(wgu, sgu, x, x_stride, rows, hidden,
+                                                                               inter, gu, act);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     shared_down_kernel<<<dim3(hidden / 16, rblocks), 64, 0, s>>>(wd, sd, act, rows, hidden, inter, out, out_stride);
