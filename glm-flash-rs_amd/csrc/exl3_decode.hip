@@ -14,6 +14,7 @@
 #include "exl3_format.hpp"
 #include "route.hpp"
 #include "launch.hpp"
+#include "shared_fp8.hpp"
 
 #ifndef GFR_GEMV_PRE
 #define GFR_GEMV_PRE 2   // trellis tiles a wave issues before it waits for its activations
@@ -168,8 +169,8 @@ __device__ __forceinline__ void load_tile_acts(const uint32_t* tile, uint32_t (&
 //   ROUTE1  (one-token windows) the wave routes the token itself (route.hpp) from a.logits: the window's experts
 //           are the token's slots; program (0, 0, 0) stores picks / weights / ids / count / members for the later
 //           launches.
-template <int K, int KTW, int NW, int MATS, int XSRC, int RB, bool ROUTE1>
-__global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) {
+template <int K, int KTW, int NW, int MATS, int XSRC, int RB, bool ROUTE1, bool FP8>
+__device__ __forceinline__ void expert_gemv_body(const GemvArgs& a, const Fp8Args& f) {
     constexpr int KC = NW * KTW;
     static_assert(XSRC == 0 || KTW == 8 || KTW == 4 || KTW == 2,
                   "a wave that builds its activations covers one 128-point block or a part of one");
@@ -186,6 +187,20 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
     int e, code;
     uint32_t xearly = 0;   // ROUTE1 with the fused rotation: the token's input pair, loaded while it is routed
     if constexpr (ROUTE1) {
+        if constexpr (FP8) {
+            if (u == a.slots - 1) {
+                // the layer's shared expert is FP8: this unit's workgroups run its gate/up programs (8 intermediate
+                // indices each) instead of an EXL3 expert's
+                __shared__ Fp8Part fp8_part;
+                const int nb = gridDim.y * gridDim.z;
+                for (int j = blockIdx.y + gridDim.y * blockIdx.z; j < f.inter / 8; j += nb) {
+                    fp8_gu_program<8, NW, 4>(f.w, f.s, f.x, f.hidden, 1, 0, f.hidden, f.inter, j, wave, lane,
+                                             fp8_part, f.gu, f.act);
+                    __syncthreads();                      // fp8_part is the next program's
+                }
+                return;
+            }
+        }
         if constexpr (XSRC == 1)
             xearly = *reinterpret_cast<const uint32_t*>(a.x0 + (kt0 & ~7) * 16 + 2 * lane);
         if (u == a.slots - 1) {
@@ -408,6 +423,17 @@ __global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) 
     }
 }
 
+template <int K, int KTW, int NW, int MATS, int XSRC, int RB, bool ROUTE1>
+__global__ void __launch_bounds__(NW * 64) expert_gemv_kernel(const GemvArgs a) {
+    expert_gemv_body<K, KTW, NW, MATS, XSRC, RB, ROUTE1, false>(a, Fp8Args{});
+}
+// The one-token form with the layer's FP8 shared expert in the shared unit's workgroups (kept apart so that the
+// layers without one run the kernel above unchanged).
+template <int K, int KTW, int NW, int MATS, int XSRC, int RB, bool ROUTE1>
+__global__ void __launch_bounds__(NW * 64) expert_gemv_fp8_kernel(const GemvArgs a, const Fp8Args f) {
+    expert_gemv_body<K, KTW, NW, MATS, XSRC, RB, ROUTE1, true>(a, f);
+}
+
 // ---- down GEMV of the decode path ------------------------------------------------------------------------------
 // Program (unit, 128-column block hb of the hidden size, 128-k block kb of the intermediate size), NW waves. A unit is
 // (member chunk, distinct expert u) of the grouping tables, or with TOKEN (a one-token window routed by the gate/up
@@ -439,8 +465,8 @@ __device__ inline void xcd_grouped(int& bx, int& by, int& bz) {
     bz = g / (gy * gx);
 }
 
-template <int K, int RB, int HB, bool TOKEN, int NW, int TZ = 4>
-__global__ void __launch_bounds__(NW * 64) down_gemv_kernel(const GemvArgs a) {
+template <int K, int RB, int HB, bool TOKEN, int NW, int TZ, bool FP8>
+__device__ __forceinline__ void down_gemv_body(const GemvArgs& a, const Fp8Args& f) {
     constexpr int TPW = 8 / NW;                          // k tiles a wave of the 128-k block
     static_assert(NW == 1 || NW == 4, "waves a workgroup");
     __shared__ __attribute__((aligned(16))) uint32_t xs[RB][128];   // the k block's activations, each twice
@@ -484,6 +510,16 @@ __global__ void __launch_bounds__(NW * 64) down_gemv_kernel(const GemvArgs a) {
         // (TZ >= the wave's share of the splits, set by the host; every wave issues TZ loads, past its share
         // re-reading its first split)
         const int slot = bx;
+        if constexpr (FP8) {
+            if (slot == a.slots - 1) {
+                // the layer's shared expert is FP8: this slot's workgroups run its down programs (a 16-column tile
+                // a wave) instead of an EXL3 expert's
+                const int nb = gridDim.y * gridDim.z;
+                for (int nt = (hb + gridDim.y * kb) * NW + wave; nt < f.hidden / 16; nt += nb * NW)
+                    fp8_down_program<4>(f.w, f.s, f.x, 1, 0, f.inter, nt, lane, f.out, f.hidden);
+                return;
+            }
+        }
         c0 = 0;
         nr = 1;
         pair_l = slot;
@@ -634,6 +670,15 @@ __global__ void __launch_bounds__(NW * 64) down_gemv_kernel(const GemvArgs a) {
         *reinterpret_cast<float2*>(a.z + ((size_t)kb * a.P + p) * a.N + ob + 2 * lane) =
             make_float2(v[0] * HAD_SCALE * f16_to_f32((uint16_t)sv), v[1] * HAD_SCALE * f16_to_f32((uint16_t)(sv >> 16)));
     }
+}
+
+template <int K, int RB, int HB, bool TOKEN, int NW, int TZ = 4>
+__global__ void __launch_bounds__(NW * 64) down_gemv_kernel(const GemvArgs a) {
+    down_gemv_body<K, RB, HB, TOKEN, NW, TZ, false>(a, Fp8Args{});
+}
+template <int K, int RB, int HB, bool TOKEN, int NW, int TZ = 4>
+__global__ void __launch_bounds__(NW * 64) down_gemv_fp8_kernel(const GemvArgs a, const Fp8Args f) {
+    down_gemv_body<K, RB, HB, TOKEN, NW, TZ, true>(a, f);
 }
 
 // The combine's terms past the EXL3 slots (the reference's combine(y, shared, weights, out), moe.rs:171-181): the
@@ -932,8 +977,9 @@ int gemv_gateup_splits(int D) { return D / 16 / GFR_GU_KTW / nw_gateup(D); }
 int gemv_down_splits(int N) { return N / 128; }   // one part a 128-k block (down_gemv_kernel)
 
 template <int K, int KTW, int NW, int MATS, int XSRC, bool ROUTE1>
-static hipError_t gemv_go(int rb, dim3 grid, hipStream_t s, const GemvArgs& a) {
-    if (ROUTE1 || rb == 1) expert_gemv_kernel<K, KTW, NW, MATS, XSRC, 1, ROUTE1><<<grid, NW * 64, 0, s>>>(a);
+static hipError_t gemv_go(int rb, dim3 grid, hipStream_t s, const GemvArgs& a, const Fp8Args* f) {
+    if (ROUTE1 && f) expert_gemv_fp8_kernel<K, KTW, NW, MATS, XSRC, 1, ROUTE1><<<grid, NW * 64, 0, s>>>(a, *f);
+    else if (ROUTE1 || rb == 1) expert_gemv_kernel<K, KTW, NW, MATS, XSRC, 1, ROUTE1><<<grid, NW * 64, 0, s>>>(a);
     else if (rb == 2) expert_gemv_kernel<K, KTW, NW, MATS, XSRC, 2, false><<<grid, NW * 64, 0, s>>>(a);
     else if (rb == 4) expert_gemv_kernel<K, KTW, NW, MATS, XSRC, 4, false><<<grid, NW * 64, 0, s>>>(a);
     else expert_gemv_kernel<K, KTW, NW, MATS, XSRC, 8, false><<<grid, NW * 64, 0, s>>>(a);
@@ -946,12 +992,13 @@ static int rb_for(int rows) { return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ?
 static unsigned chunks_x(int maxu, int members, int rb) { return (unsigned)maxu * (unsigned)((members + rb - 1) / rb); }
 
 template <int KTW, int NW, int MATS, int XSRC, bool ROUTE1 = false>
-static hipError_t gemv_bits(int bits, int rb, dim3 grid, hipStream_t s, const GemvArgs& a) {
+static hipError_t gemv_bits(int bits, int rb, dim3 grid, hipStream_t s, const GemvArgs& a,
+                            const Fp8Args* f = nullptr) {
     switch (bits) {
-        case 2: return gemv_go<2, KTW, NW, MATS, XSRC, ROUTE1>(rb, grid, s, a);
-        case 3: return gemv_go<3, KTW, NW, MATS, XSRC, ROUTE1>(rb, grid, s, a);
-        case 4: return gemv_go<4, KTW, NW, MATS, XSRC, ROUTE1>(rb, grid, s, a);
-        case 5: return gemv_go<5, KTW, NW, MATS, XSRC, ROUTE1>(rb, grid, s, a);
+        case 2: return gemv_go<2, KTW, NW, MATS, XSRC, ROUTE1>(rb, grid, s, a, f);
+        case 3: return gemv_go<3, KTW, NW, MATS, XSRC, ROUTE1>(rb, grid, s, a, f);
+        case 4: return gemv_go<4, KTW, NW, MATS, XSRC, ROUTE1>(rb, grid, s, a, f);
+        case 5: return gemv_go<5, KTW, NW, MATS, XSRC, ROUTE1>(rb, grid, s, a, f);
         default: return hipErrorInvalidValue;
     }
 }
@@ -979,8 +1026,10 @@ hipError_t launch_expert_gateup(hipStream_t s, const uint16_t* x, int x_stride, 
                                 const uint16_t* suh_u, const uint32_t* gt, const uint32_t* ut, const int* uids,
                                 const int* ucount, const int* members, float* Zgu, int D, int N, int P, int rows,
                                 int maxm, int slots, int E, int bits, int maxu, const RouteOne* route,
-                                const uint32_t* dt_next) {
+                                const uint32_t* dt_next, const Fp8Shared* fp8) {
     GemvArgs a{};
+    Fp8Args f{};
+    if (fp8) f = Fp8Args{fp8->gu_w, fp8->gu_s, x, fp8->gu, fp8->act, nullptr, fp8->hidden, fp8->inter};
     a.tnext = dt_next;
     a.next_words = (size_t)(N / 16) * (D / 16) * 8 * bits;
     a.x0 = x; a.x_stride = x_stride; a.suh0 = suh_g; a.suh1 = suh_u; a.t0 = gt; a.t1 = ut;
@@ -993,9 +1042,10 @@ hipError_t launch_expert_gateup(hipStream_t s, const uint16_t* x, int x_stride, 
         a.logits = route->logits; a.routed = route->routed; a.pick_out = route->picks; a.weight_out = route->weights;
         a.route_bias = route->bias; a.route_scale = route->scale;
         a.ids_out = route->ids; a.count_out = route->count; a.members_out = route->members;
-        return nw == 4 ? gemv_bits<GFR_GU_KTW, 4, 2, 1, true>(bits, 1, grid, s, a)
-                       : gemv_bits<GFR_GU_KTW, 2, 2, 1, true>(bits, 1, grid, s, a);
+        return nw == 4 ? gemv_bits<GFR_GU_KTW, 4, 2, 1, true>(bits, 1, grid, s, a, fp8 ? &f : nullptr)
+                       : gemv_bits<GFR_GU_KTW, 2, 2, 1, true>(bits, 1, grid, s, a, fp8 ? &f : nullptr);
     }
+    if (fp8) return hipErrorInvalidValue;               // the FP8 shared expert rides on one-token launches only
     return nw == 4 ? gemv_bits<GFR_GU_KTW, 4, 2, 1>(bits, rb, grid, s, a)
                    : gemv_bits<GFR_GU_KTW, 2, 2, 1>(bits, rb, grid, s, a);
 }
@@ -1004,7 +1054,7 @@ hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, int SKgu, 
                               const uint16_t* svh_u, const uint16_t* suh_d, float limit, uint16_t* xd,
                               const uint32_t* dt, const uint16_t* svh_d, const int* uids, const int* ucount,
                               const int* members, float* Zd, int N, int P, int rows, int maxm, int slots, int E,
-                              int bits, int maxu, const RouteOne* route) {
+                              int bits, int maxu, const RouteOne* route, const Fp8Shared* fp8) {
     GemvArgs a{};
     a.zgu = Zgu; a.SKgu = SKgu; a.svh_g = svh_g; a.svh_u = svh_u; a.suh0 = suh_d; a.limit = limit;
     a.xd = xd; a.t0 = dt; a.t1 = dt; a.x1 = svh_d; a.uids = uids; a.ucount = ucount; a.members = members; a.z = Zd;
@@ -1025,10 +1075,18 @@ hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, int SKgu, 
     if (token) {
         a.pick_out = route->picks;
         a.routed = route->routed;
+    } else if (fp8) {
+        return hipErrorInvalidValue;                    // the FP8 shared expert rides on one-token launches only
     }
+    Fp8Args f{};
+    if (fp8) f = Fp8Args{fp8->d_w, fp8->d_s, fp8->act, nullptr, nullptr, fp8->out, fp8->hidden, fp8->inter};
     const dim3 grid(token ? (unsigned)slots : chunks_x(maxu, rows < maxm ? rows : maxm, rb), D / 128 / hbw, N / 128);
 #define GFR_DOWN_HB(KB, HB)                                                                                       \
-    if (one) down_gemv_kernel<KB, 1, HB, true, 1, 4><<<grid, 64, 0, s>>>(a);                                       \
+    if (fp8 && one) down_gemv_fp8_kernel<KB, 1, HB, true, 1, 4><<<grid, 64, 0, s>>>(a, f);                         \
+    else if (fp8 && tz <= 1) down_gemv_fp8_kernel<KB, 1, HB, true, 4, 1><<<grid, 256, 0, s>>>(a, f);               \
+    else if (fp8 && tz <= 2) down_gemv_fp8_kernel<KB, 1, HB, true, 4, 2><<<grid, 256, 0, s>>>(a, f);               \
+    else if (fp8) down_gemv_fp8_kernel<KB, 1, HB, true, 4, 4><<<grid, 256, 0, s>>>(a, f);                          \
+    else if (one) down_gemv_kernel<KB, 1, HB, true, 1, 4><<<grid, 64, 0, s>>>(a);                                  \
     else if (token && tz <= 1) down_gemv_kernel<KB, 1, HB, true, 4, 1><<<grid, 256, 0, s>>>(a);                   \
     else if (token && tz <= 2) down_gemv_kernel<KB, 1, HB, true, 4, 2><<<grid, 256, 0, s>>>(a);                   \
     else if (token) down_gemv_kernel<KB, 1, HB, true, 4, 4><<<grid, 256, 0, s>>>(a);                              \

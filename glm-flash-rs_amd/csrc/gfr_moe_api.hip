@@ -183,13 +183,13 @@ int experts_run(gfr_experts* ex, hipStream_t stream, const gfr_exl3_experts* w, 
                 int input_stride, const int32_t* picks, const int32_t* ids, const int32_t* count,
                 const int32_t* members, int rows, int maxm, const float* weights, float* out,
                 const gfr::RouteOne* route = nullptr, const float* shared = nullptr, int shared_stride = 0,
-                int launches = 0, hipEvent_t shared_ready = nullptr) {
+                int launches = 0, hipEvent_t shared_ready = nullptr, const gfr::Fp8Shared* fp8 = nullptr) {
     const int P = rows * ex->slots, D = ex->hidden, N = ex->inter;
     const int maxu = P < w->experts ? P : w->experts;
     hipError_t e;
     if ((e = gfr::launch_expert_gateup(stream, input, input_stride, w->suh_g, w->suh_u, w->gt, w->ut, ids, count,
                                        members, ex->zgu, D, N, P, rows, maxm, ex->slots, w->experts, w->bits, maxu,
-                                       route, w->dt)) !=
+                                       route, w->dt, fp8)) !=
         hipSuccess)
         return hip_fail(e, "gate/up gemv");
     if (launches == 1) return 0;
@@ -197,7 +197,7 @@ int experts_run(gfr_experts* ex, hipStream_t stream, const gfr_exl3_experts* w, 
     if ((e = gfr::launch_expert_down(stream, ex->zgu, D, skgu, w->svh_g, w->svh_u, w->suh_d, 10.f, ex->xd, w->dt,
                                      w->svh_d,
                                      ids, count, members, ex->zd, N, P, rows, maxm, ex->slots, w->experts, w->bits,
-                                     maxu, route)) != hipSuccess)
+                                     maxu, route, fp8)) != hipSuccess)
         return hip_fail(e, "down gemv");
     if (launches == 2) return 0;
     // the shared branch joins here: only the finish (down epilogue + combine) reads its output
@@ -479,7 +479,8 @@ int gfr_moe_set_decode_rows(gfr_moe* m, int decode_rows) {
 
 namespace {
 int moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input, const float* logits,
-            const float* shared, int shared_stride, int rows, hipEvent_t shared_ready = nullptr) {
+            const float* shared, int shared_stride, int rows, hipEvent_t shared_ready = nullptr,
+            const gfr::Fp8Shared* fp8 = nullptr) {
     if (!m) return fail(GFR_EINVAL, "null moe");
     int rc = check_weights(w, m->hidden, m->inter);
     if (rc) return rc;
@@ -505,7 +506,7 @@ int moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uin
                                   g->count, g->members};
             return experts_run(m->dec, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members, 1,
                                g->max_rows, m->weights, m->out, &r, shared, shared_stride, m->launches,
-                               shared_ready);
+                               shared_ready, fp8);
         }
         // four launches: route + group, gate/up (+ rotation), down (+ gate/up epilogue), down epilogue (+ combine)
         if ((e = gfr::launch_route_group(stream, logits, rows, m->routed, m->topk, m->picks, m->weights, g->ids,
@@ -754,13 +755,33 @@ int gfr_shared_fp8_destroy(gfr_shared_fp8* sh) {
     return 0;
 }
 
+namespace {
+// The layer with its FP8 shared expert. A one-token window whose launches have the shared slot's workgroups (the
+// grid's last unit exists: the weights hold at least `slots` experts) runs the shared expert inside the gate/up and
+// down launches (three launches in all); other windows run its two launches first.
+int moe_run_fp8(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
+                const float* logits, const gfr_fp8_shared_weights* sw, int rows) {
+    if (rows <= 0 || rows > m->max_rows) return fail(GFR_EINVAL, "rows %d outside 1..%d", rows, m->max_rows);
+    if (!w || !input) return fail(GFR_EINVAL, "null weights or input");
+    if (!al16(input)) return fail(GFR_EINVAL, "input rows must be 16-byte aligned");
+    const bool fused = rows == 1 && rows <= m->decode_rows && w->experts >= m->slots &&
+                       gfr::gemv_gateup_splits(m->hidden) <= 16;
+    if (!fused) {
+        int rc = shared_fp8_run(m->sfp8, stream, sw, input, m->hidden, rows, m->shared_out, m->hidden);
+        if (rc) return rc;
+        return moe_run(m, stream, w, input, logits, m->shared_out, m->hidden, rows);
+    }
+    const gfr::Fp8Shared job{sw->gu, sw->gu_scale, sw->down, sw->down_scale, m->sfp8->gu, m->sfp8->act,
+                             m->shared_out, m->hidden, m->inter};
+    return moe_run(m, stream, w, input, logits, m->shared_out, m->hidden, rows, nullptr, &job);
+}
+}  // namespace
+
 int gfr_moe_run_fp8(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
                     const float* logits, const gfr_fp8_shared_weights* sw, int rows) {
     int rc = moe_fp8_ready(m, sw);
     if (rc) return rc;
-    if (rows <= 0 || rows > m->max_rows) return fail(GFR_EINVAL, "rows %d outside 1..%d", rows, m->max_rows);
-    if ((rc = shared_fp8_run(m->sfp8, stream, sw, input, m->hidden, rows, m->shared_out, m->hidden))) return rc;
-    return moe_run(m, stream, w, input, logits, m->shared_out, m->hidden, rows);
+    return moe_run_fp8(m, stream, w, input, logits, sw, rows);
 }
 
 int gfr_moe_run_router_fp8(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uint16_t* input,
@@ -771,8 +792,7 @@ int gfr_moe_run_router_fp8(gfr_moe* m, hipStream_t stream, const gfr_exl3_expert
     if (rows <= 0 || rows > m->max_rows) return fail(GFR_EINVAL, "rows %d outside 1..%d", rows, m->max_rows);
     if ((rc = gfr_router_logits(stream, input, m->hidden, router_weight, m->hidden, m->routed, rows, m->logits)))
         return rc;
-    if ((rc = shared_fp8_run(m->sfp8, stream, sw, input, m->hidden, rows, m->shared_out, m->hidden))) return rc;
-    return moe_run(m, stream, w, input, m->logits, m->shared_out, m->hidden, rows);
+    return moe_run_fp8(m, stream, w, input, m->logits, sw, rows);
 }
 
 float* gfr_moe_shared_output(const gfr_moe* m) { return m ? m->shared_out : nullptr; }

@@ -54,11 +54,23 @@ struct RouteOne {
     int* count;
     int* members;
 };
+// The layer's FP8 shared expert when it rides on a one-token window's launches (shared_fp8.hpp): the shared slot's
+// workgroups of the gate/up launch write gu / act, those of the down launch out [hidden] (fp32).
+struct Fp8Shared {
+    const uint8_t* gu_w;
+    const uint16_t* gu_s;
+    const uint8_t* d_w;
+    const uint16_t* d_s;
+    uint16_t* gu;
+    uint16_t* act;
+    float* out;
+    int hidden, inter;
+};
 hipError_t launch_expert_gateup(hipStream_t s, const uint16_t* x, int x_stride, const uint16_t* suh_g,
                                 const uint16_t* suh_u, const uint32_t* gt, const uint32_t* ut, const int* uids,
                                 const int* ucount, const int* members, float* Zgu, int D, int N, int P, int rows,
                                 int maxm, int slots, int E, int bits, int maxu, const RouteOne* route,
-                                const uint32_t* dt_next = nullptr);
+                                const uint32_t* dt_next = nullptr, const Fp8Shared* fp8 = nullptr);
 // dt_next: the layer's down trellis; the gate waves read each window expert's down matrix once into the caches
 // after their own work (expert_gemv_kernel), so the down launch's first loads hit the memory-side cache
 // SKgu: the gate/up partials' K splits (gemv_gateup_splits)
@@ -66,7 +78,7 @@ hipError_t launch_expert_down(hipStream_t s, const float* Zgu, int D, int SKgu, 
                               const uint16_t* svh_u, const uint16_t* suh_d, float limit, uint16_t* xd,
                               const uint32_t* dt, const uint16_t* svh_d, const int* uids, const int* ucount,
                               const int* members, float* Zd, int N, int P, int rows, int maxm, int slots, int E,
-                              int bits, int maxu, const RouteOne* route = nullptr);
+                              int bits, int maxu, const RouteOne* route = nullptr, const Fp8Shared* fp8 = nullptr);
 // route: the one-token window was routed by the gate/up launch (its picks); the down launch then runs one program a
 // slot and reads no grouping table
 // Finish of the decode path: Zd's transformed k-block parts [N / 128][P][D] added in order -> y; with weights the
