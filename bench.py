@@ -15,7 +15,8 @@ Also measured in the same run:
   cpu_baseline  the scalar CPU oracle (decode + fp32 matvec of the token's 5 experts, oracle/gfr_oracle.c) on a
                 bounded sample of tokens, 1 thread;
   prefill       config 4 (8192 tokens, uniform top-4) through the prefill path, against the fp16 MFMA peak;
-  other_configs configs 1, 3 and 5 (decode and prefill), each against its HBM or MFMA roofline.
+  other_configs configs 1, 3 and 5 (decode and prefill), each against its HBM or MFMA roofline, and the reference's
+                own layer geometry with its FP8 shared expert.
 Prints one JSON line.
 """
 import argparse
@@ -261,6 +262,41 @@ def other_configs(args, copies, stream):
     del graph, moe
     torch.cuda.empty_cache()
 
+    # ---- the reference's own layer geometry (experts.rs:146-156, moe.rs:132-167): hidden 4096, intermediate 512,
+    # 288 routed EXL3 experts (K = 4) top-8 with GLM's gate + the FP8 shared expert, one token, Zipf(1.1) routing
+    Dr, Nr, Er, Kr = 4096, 512, 288, 8
+    rc = [synth.experts(Er, Dr, Nr, BITS, seed=960 + c) for c in range(4)]
+    rs = [synth.fp8_shared(Dr, Nr, seed=970 + c) for c in range(4)]
+    bias = torch.zeros(Er, device="cuda")
+    mr = gfr_moe.Moe(Dr, Nr, Er, Kr, 1, shared_exl3=False)
+    mr.set_router(bias, 2.5)
+    R = 16
+    xr = synth.activations(R, Dr, 971)
+    lr = synth.zipf_logits(R, Er, Kr, 1.1, 972)
+    glen = 4 * R
+    graph = graph_of([(lambda j=j: mr.run_fp8(rc[j % 4], xr[j % R:j % R + 1], lr[j % R:j % R + 1], rs[j % 4], 1,
+                                              stream=stream)) for j in range(glen)], stream)
+    time_graphs([graph], stream)
+    reps = 8
+    secs = time_graphs([graph] * reps, stream) / (reps * glen)
+    shared_bytes = 3 * Dr * Nr + 2 * (2 * Nr + Dr) + Dr * 2 + Dr * 4
+    tok_bytes = Kr * (3 * Dr * Nr * BITS // 8 + (3 * Dr + 3 * Nr) * 2) + shared_bytes
+    sh = gfr_moe.SharedFp8(Dr, Nr, 1)
+    so = torch.empty((1, Dr), device="cuda")
+    g2 = graph_of([(lambda j=j: sh.run(rs[j % 4], xr[j % R:j % R + 1], 1, out=so, stream=stream))
+                   for j in range(glen)], stream)
+    time_graphs([g2], stream)
+    s2 = time_graphs([g2] * reps, stream) / (reps * glen)
+    out["reference_layout"] = {
+        "config": "the reference's layer geometry: hidden 4096, intermediate 512, 288 routed EXL3 experts (K=4) top-8 "
+                  "(GLM gate) + the FP8 shared expert (moe.rs:132-167), one token, Zipf(1.1); the shared expert "
+                  "runs inside the layer's gate/up and down launches", "us_per_token": round(secs * 1e6, 2),
+        "tok_per_s": round(1 / secs, 1), "bytes_per_token": tok_bytes, "gbs": round(tok_bytes / secs / 1e9, 1),
+        "hbm_frac": round(tok_bytes / secs / 1e9 / HBM_PEAK_GBS, 4),
+        "shared_fp8_alone_us": round(s2 * 1e6, 2), "shared_fp8_bytes": shared_bytes}
+    del graph, g2, mr, sh, rc, rs
+    torch.cuda.empty_cache()
+
     # ---- the shared-expert fork and the routed-expert read hints (shared_expert.rs, l2_prefetch.rs)
     out["shared_branch_and_hints"] = prefetch_leg(copies, stream)
     torch.cuda.empty_cache()
@@ -325,8 +361,8 @@ def other_configs(args, copies, stream):
 def prefetch_leg(copies, stream, reps=8):
     """The shared-expert fork and the routed-expert read hints of the reference's decode round (shared_expert.rs
     Branch::run, l2_prefetch.rs Owner::experts + l2pf.cu), at config 2's shape for one token: group the routed token,
-    then the shared expert's work (a bf16 stand-in of its gate/up and down products, 6.3 MB each, in place of the
-    reference's FP8 branch) and the routed experts (ExpertGpu, 4 EXL3 slots). Three forms, each a graph of 64 steps
+    then the shared expert's work (an FP8 shared expert of that shape, gfr_moe.SharedFp8: 9.4 MB of weights, two
+    launches) and the routed experts (ExpertGpu, 4 EXL3 slots). Three forms, each a graph of 64 steps
     over the 16 cold weight copies, timed alternately:
       serial   shared work, then the routed experts, on one stream;
       branch   the shared work on a forked stream (gfr_moe.SharedBranch), joined after the routed experts;
@@ -347,9 +383,9 @@ def prefetch_leg(copies, stream, reps=8):
     plan = pf.expert_plans[0][1]
     xs = synth.activations(R, D, 951)
     picks, _ = gfr_moe.route(synth.logits(R, E, 952), TOPK)
-    wgu = (torch.randn(D, 2 * N, device="cuda") * 0.02).to(torch.bfloat16)
-    wd = (torch.randn(N, D, device="cuda") * 0.02).to(torch.bfloat16)
-    shared = torch.empty(rows, D, device="cuda", dtype=torch.bfloat16)
+    sw = synth.fp8_shared(D, N, seed=953)
+    sh = gfr_moe.SharedFp8(D, N, rows)
+    shared = torch.empty(rows, D, device="cuda")
 
     def step(j, form):
         def f():
@@ -357,8 +393,7 @@ def prefetch_leg(copies, stream, reps=8):
             p = picks[r:r + 1]
 
             def shared_fn(st=None):
-                h = torch.matmul(xs[r:r + 1], wgu)
-                torch.matmul(h[:, :N], wd, out=shared)
+                sh.run(sw, xs[r:r + 1], rows, out=shared, stream=st if st is not None else stream)
 
             def routed(ready=None):
                 ex.run_rows(copies[c], xs[r:r + 1], p, g.ids, g.count, g.members, rows, rows, stream=stream)
@@ -376,7 +411,7 @@ def prefetch_leg(copies, stream, reps=8):
         return f
 
     forms = ("serial", "branch", "hinted")
-    with torch.cuda.stream(stream):            # library handles (hipBLASLt) are created outside the capture
+    with torch.cuda.stream(stream):
         for form in forms:
             step(0, form)()
     stream.synchronize()
@@ -389,8 +424,8 @@ def prefetch_leg(copies, stream, reps=8):
         for form in forms:
             us[form].append(time_graphs([graphs[form]] * 4, stream) / (4 * glen) * 1e6)
     med = {k: round(sorted(v)[len(v) // 2], 3) for k, v in us.items()}
-    return {"config": "config 2 shape, one token: grouping, shared-expert stand-in (bf16 gate/up + down products, "
-                      "12.6 MB), routed experts (ExpertGpu, 4 EXL3 slots); 16 cold weight copies",
+    return {"config": "config 2 shape, one token: grouping, an FP8 shared expert (SharedFp8, 9.4 MB), routed experts "
+                      "(ExpertGpu, 4 EXL3 slots); 16 cold weight copies",
             "us_per_step_serial": med["serial"], "us_per_step_shared_branch": med["branch"],
             "us_per_step_hinted": med["hinted"], "hint_bytes_per_step": 2 * TOPK * plan.bytes}
 

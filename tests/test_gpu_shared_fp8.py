@@ -191,3 +191,41 @@ def test_prepared_shared_fp8(gfr, sw, routed, tmp_path):
     assert torch.equal(a, b)
     with pytest.raises(gfr.GfrError):
         p.shared_fp8(1)
+
+
+@pytest.mark.parametrize("routed,topk", [(16, 4), (4, 4)])
+def test_moe_run_fp8_one_token_forms(gfr, oracle, routed, topk):
+    """One token: with at least `slots` routed experts the shared expert rides on the EXL3 gate/up and down launches
+    (the shared slot's workgroups); with fewer (4 routed, top-4: the grid has no shared unit) it runs its own two
+    launches first. Both give the bytes of gfr_moe_run_shared fed with gfr_shared_fp8's output, eagerly and in every
+    replay of a captured graph."""
+    import synth
+    H, I = 512, 256
+    w = synth.experts(routed, H, I, BITS, seed=routed)
+    sw1 = synth.fp8_shared(H, I, seed=routed + 1)
+    x = torch.randn((1, H), generator=torch.Generator(device="cuda").manual_seed(2), device="cuda").to(torch.bfloat16)
+    lg = synth.logits(1, routed, 3)
+    m = gfr.Moe(H, I, routed, topk, 1, shared_exl3=False)
+    m.run_fp8(w, x, lg, sw1, 1)
+    torch.cuda.synchronize()
+    got = m.output[:1].clone()
+    shared = gfr.SharedFp8(H, I, 1).run(sw1, x, 1)
+    torch.cuda.synchronize()
+    assert torch.equal(m.shared_output[:1], shared)
+    m2 = gfr.Moe(H, I, routed, topk, 1, shared_exl3=False)
+    m2.run(w, x, lg, 1, shared=shared)
+    torch.cuda.synchronize()
+    assert torch.equal(m2.output[:1], got)
+    s = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            m.run_fp8(w, x, lg, sw1, 1, stream=s)
+    for _ in range(3):
+        m.output.zero_()
+        m.shared_output.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(m.output[:1], got)
