@@ -2,6 +2,7 @@
 // on the caller's stream. Mirrors the reference's Rust owners (grouping.rs, experts.rs, fast_experts.rs, moe.rs):
 // same buffer contracts, same precondition checks, no allocation / free / host sync inside run.
 #include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
 #include <stdint.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -119,6 +120,8 @@ struct gfr_shared_fp8 {
     int hidden, inter, max_rows;
     uint16_t* gu;    // [max_rows][2 inter] bf16
     uint16_t* act;   // [max_rows][inter] bf16
+    rocblas_handle blas;   // the prefill form's GEMMs, with a workspace of its own (no allocation at run)
+    void* blas_ws;
 };
 
 extern "C" {
@@ -685,6 +688,9 @@ int gfr_moe_run_router(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w
 
 // ---- the FP8 shared expert --------------------------------------------------------------------------------------
 namespace {
+// windows of up to this many rows run the slice arithmetic of the reference's decode / verify path (fmm, moe.rs and
+// window_gemm.rs, MAX_ROWS 16 in kda_window.rs); larger ones its prefill form when the bf16 copies are given
+constexpr int FP8_SLICE_ROWS = 16;
 bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 int check_fp8_weights(const gfr_fp8_shared_weights* w, int hidden, int inter) {
     if (!w) return fail(GFR_EINVAL, "null FP8 shared weights");
@@ -709,8 +715,16 @@ int shared_fp8_run(gfr_shared_fp8* sh, hipStream_t stream, const gfr_fp8_shared_
     if (out_stride < sh->hidden || out_stride % 4 || !al16(out))
         return fail(GFR_EINVAL, "output stride %d: at least hidden %d, a multiple of 4, the pointer 16-byte aligned",
                     out_stride, sh->hidden);
-    hipError_t e = gfr::launch_shared_fp8(stream, w->gu, w->gu_scale, w->down, w->down_scale, input, input_stride,
-                                          rows, sh->hidden, sh->inter, sh->gu, sh->act, out, out_stride);
+    hipError_t e;
+    if (rows > FP8_SLICE_ROWS && w->gu_bf16 && w->down_bf16 && sh->blas) {
+        if (!al16(w->gu_bf16) || !al16(w->down_bf16))
+            return fail(GFR_EINVAL, "FP8 shared bf16 weight copies must be 16-byte aligned");
+        e = gfr::launch_shared_fp8_prefill(sh->blas, stream, w->gu_bf16, w->down_bf16, input, input_stride, rows,
+                                           sh->hidden, sh->inter, sh->gu, sh->act, out, out_stride);
+    } else {
+        e = gfr::launch_shared_fp8(stream, w->gu, w->gu_scale, w->down, w->down_scale, input, input_stride, rows,
+                                   sh->hidden, sh->inter, sh->gu, sh->act, out, out_stride);
+    }
     if (e != hipSuccess) return hip_fail(e, "FP8 shared expert");
     return 0;
 }
@@ -729,14 +743,44 @@ int gfr_shared_fp8_create(gfr_shared_fp8** out, int hidden, int inter, int max_r
     if (hidden <= 0 || hidden % 512 || hidden > (1 << 20) || inter <= 0 || inter % 64 || inter > (1 << 20))
         return fail(GFR_EINVAL, "FP8 shared expert: hidden %d a multiple of 512, inter %d of 64", hidden, inter);
     if (max_rows <= 0 || max_rows > (1 << 16)) return fail(GFR_EINVAL, "max_rows %d", max_rows);
-    gfr_shared_fp8* sh = new gfr_shared_fp8{hidden, inter, max_rows, nullptr, nullptr};
+    gfr_shared_fp8* sh = new gfr_shared_fp8{hidden, inter, max_rows, nullptr, nullptr, nullptr, nullptr};
     int rc;
     if ((rc = alloc_zero(&sh->gu, (size_t)max_rows * 2 * inter, "FP8 shared gu")) ||
         (rc = alloc_zero(&sh->act, (size_t)max_rows * inter, "FP8 shared activation"))) {
         gfr_shared_fp8_destroy(sh);
         return rc;
     }
+    if (max_rows > FP8_SLICE_ROWS) {
+        // windows past the verify size may take the prefill form (library GEMMs on the bf16 weight copies)
+        constexpr size_t WS = (size_t)64 << 20;
+        unsigned char* ws = nullptr;
+        if ((rc = alloc_zero(&ws, WS, "FP8 shared GEMM workspace"))) {
+            gfr_shared_fp8_destroy(sh);
+            return rc;
+        }
+        sh->blas_ws = ws;
+        if (rocblas_create_handle(&sh->blas) != rocblas_status_success ||
+            rocblas_set_workspace(sh->blas, sh->blas_ws, WS) != rocblas_status_success) {
+            gfr_shared_fp8_destroy(sh);
+            return fail(GFR_ENOMEM, "FP8 shared expert: rocBLAS handle");
+        }
+    }
     *out = sh;
+    return 0;
+}
+
+int gfr_fp8_prepare_bf16(hipStream_t stream, const gfr_fp8_shared_weights* w, uint16_t* gu_bf16,
+                         uint16_t* down_bf16) {
+    if (!w || !w->gu || !w->gu_scale || !w->down || !w->down_scale || !gu_bf16 || !down_bf16)
+        return fail(GFR_EINVAL, "null FP8 shared tensor or output");
+    if (w->hidden <= 0 || w->hidden % 16 || w->inter <= 0 || w->inter % 16)
+        return fail(GFR_EINVAL, "FP8 shared expert: hidden %d and inter %d multiples of 16", w->hidden, w->inter);
+    if (!al16(w->gu) || !al16(w->down) || !al16(gu_bf16) || !al16(down_bf16))
+        return fail(GFR_EINVAL, "FP8 weights and their bf16 copies must be 16-byte aligned");
+    hipError_t e;
+    if ((e = gfr::launch_fp8_b16_copy(stream, w->gu, w->gu_scale, gu_bf16, 2 * w->inter, w->hidden)) != hipSuccess ||
+        (e = gfr::launch_fp8_b16_copy(stream, w->down, w->down_scale, down_bf16, w->hidden, w->inter)) != hipSuccess)
+        return hip_fail(e, "FP8 -> bf16 weight copies");
     return 0;
 }
 
@@ -750,7 +794,8 @@ uint16_t* gfr_shared_fp8_act(const gfr_shared_fp8* sh) { return sh ? sh->act : n
 
 int gfr_shared_fp8_destroy(gfr_shared_fp8* sh) {
     if (!sh) return 0;
-    free_all({sh->gu, sh->act});
+    if (sh->blas) rocblas_destroy_handle(sh->blas);
+    free_all({sh->gu, sh->act, sh->blas_ws});
     delete sh;
     return 0;
 }

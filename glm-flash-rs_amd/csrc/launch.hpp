@@ -123,5 +123,11 @@ hipError_t launch_router_logits(hipStream_t s, const uint16_t* x, int x_stride, 
 hipError_t launch_shared_fp8(hipStream_t s, const uint8_t* wgu, const uint16_t* sgu, const uint8_t* wd,
                              const uint16_t* sd, const uint16_t* x, int x_stride, int rows, int hidden, int inter,
                              uint16_t* gu, uint16_t* act, float* out, int out_stride);
+// The prefill form: the reference's bf16 weight copies (f8_b16_copy, prefill.cu:7-17: bf16(fp8 * row scale)), and
+// the expert as two library GEMMs on them around shared_swiglu (blas: a rocblas_handle with its workspace set).
+hipError_t launch_fp8_b16_copy(hipStream_t s, const uint8_t* w, const uint16_t* scale, uint16_t* out, int n, int k);
+hipError_t launch_shared_fp8_prefill(void* blas, hipStream_t s, const uint16_t* wgu16, const uint16_t* wd16,
+                                     const uint16_t* x, int x_stride, int rows, int hidden, int inter, uint16_t* gu,
+                                     uint16_t* act, float* out, int out_stride);
 
 }  // namespace gfr

@@ -788,7 +788,7 @@ int gfr_prepared_shared_fp8(const gfr_prepared* p, int layer, gfr_fp8_shared_wei
         if (int rc = gfr_prepared_pointer(p, path.c_str(), &ptr[i])) return rc;
     }
     *out = gfr_fp8_shared_weights{(int)H, (int)I, (const uint8_t*)ptr[0], (const uint16_t*)ptr[1],
-                                  (const uint8_t*)ptr[2], (const uint16_t*)ptr[3]};
+                                  (const uint8_t*)ptr[2], (const uint16_t*)ptr[3], nullptr, nullptr};
     return 0;
 }
 

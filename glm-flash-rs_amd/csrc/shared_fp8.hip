@@ -18,6 +18,7 @@
 //     slice sums meet in LDS and are added in slice order.
 //   * down: one wave a 16-column tile of the hidden size, K = inter in one chain (the reference's sk = 1).
 #include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
 #include <stdint.h>
 #include "launch.hpp"
 #include "shared_fp8.hpp"
@@ -43,7 +44,83 @@ __global__ void __launch_bounds__(64) shared_down_kernel(const uint8_t* __restri
                                                         int inter, float* __restrict__ out, int out_stride) {
     fp8_down_program<8>(w, scale, act, rows, blockIdx.y, inter, blockIdx.x, threadIdx.x, out, out_stride);
 }
+
+// The prefill form's weight preparation (the reference's f8_b16_copy, prefill.cu:7-17): out[n][k] =
+// bf16_rn(fp8(w[n][k]) * scale[n]), sixteen weights a thread (k a multiple of 16, so they share a row). The e4m3
+// conversion is exact (0x7f / 0xff are NaN, as the reference makes them); the product of a 4-bit and an 8-bit
+// significand is exact in fp32, so the only rounding is the bf16 one.
+__global__ void __launch_bounds__(256) fp8_b16_copy_kernel(const uint8_t* __restrict__ w,
+                                                           const uint16_t* __restrict__ scale,
+                                                           uint16_t* __restrict__ out, long long count, int k) {
+    const long long i = ((long long)blockIdx.x * 256 + threadIdx.x) * 16;
+    if (i >= count) return;
+    const uint4 v = *reinterpret_cast<const uint4*>(w + i);
+    const float sc = bf16_to_f32(scale[i / k]);
+    const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+    uint32_t o[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(words[q], false);
+        const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(words[q], true);
+        o[2 * q] = (__builtin_bit_cast(uint32_t, bf16r(lo[0] * sc)) >> 16) |
+                   (__builtin_bit_cast(uint32_t, bf16r(lo[1] * sc)) & 0xffff0000u);
+        o[2 * q + 1] = (__builtin_bit_cast(uint32_t, bf16r(hi[0] * sc)) >> 16) |
+                       (__builtin_bit_cast(uint32_t, bf16r(hi[1] * sc)) & 0xffff0000u);
+    }
+    uint4* dst = reinterpret_cast<uint4*>(out + i);
+    dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+    dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
+// shared_swiglu over a window's bf16 gu rows (the prefill form): act[r][i] = bf16(bf16(silu(min(g, 10))) *
+// clamp(u, -10, 10)), g = gu[r][i], u = gu[r][inter + i].
+__global__ void __launch_bounds__(256) fp8_swiglu_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ act,
+                                                         int rows, int inter) {
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (long long)rows * inter) return;
+    const int r = (int)(idx / inter), i = (int)(idx % inter);
+    const float gg = fminf(bf16_to_f32(gu[(size_t)r * 2 * inter + i]), SHARED_LIMIT);
+    const float uu = __builtin_amdgcn_fmed3f(bf16_to_f32(gu[(size_t)r * 2 * inter + inter + i]), -SHARED_LIMIT,
+                                             SHARED_LIMIT);
+    const float v = bf16r(bf16r(gg / (1.f + expf(-gg))) * uu);
+    act[(size_t)r * inter + i] = (uint16_t)(__builtin_bit_cast(uint32_t, v) >> 16);
+}
 }  // namespace
+
+hipError_t launch_fp8_b16_copy(hipStream_t s, const uint8_t* w, const uint16_t* scale, uint16_t* out, int n, int k) {
+    const long long count = (long long)n * k;
+    fp8_b16_copy_kernel<<<(unsigned)((count / 16 + 255) / 256), 256, 0, s>>>(w, scale, out, count, k);
+    return hipGetLastError();
+}
+
+// The prefill form (the reference's prefill.rs Matrix::run with its prepared bf16 weights, batch.rs:1183-1195): gu =
+// x W_gu^T (bf16 out), shared_swiglu, out = act W_d^T (fp32 out); both GEMMs are rocBLAS gemm_ex (bf16 operands, fp32
+// accumulation), row-major operands as the transposed column-major products.
+hipError_t launch_shared_fp8_prefill(void* blas, hipStream_t s, const uint16_t* wgu16, const uint16_t* wd16,
+                                     const uint16_t* x, int x_stride, int rows, int hidden, int inter, uint16_t* gu,
+                                     uint16_t* act, float* out, int out_stride) {
+    rocblas_handle h = static_cast<rocblas_handle>(blas);
+    if (rocblas_set_stream(h, s) != rocblas_status_success) return hipErrorInvalidValue;
+    const float one = 1.f, zero = 0.f;
+    // gu^T [2 inter][rows] = W_gu [2 inter][hidden] (col-major hidden x 2 inter, transposed) x x^T (hidden x rows)
+    if (rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, 2 * inter, rows, hidden, &one, wgu16,
+                        rocblas_datatype_bf16_r, hidden, x, rocblas_datatype_bf16_r, x_stride, &zero, gu,
+                        rocblas_datatype_bf16_r, 2 * inter, gu, rocblas_datatype_bf16_r, 2 * inter,
+                        rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, rocblas_gemm_flags_none) !=
+        rocblas_status_success)
+        return hipErrorLaunchFailure;
+    const long long n = (long long)rows * inter;
+    fp8_swiglu_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(gu, act, rows, inter);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, hidden, rows, inter, &one, wd16,
+                        rocblas_datatype_bf16_r, inter, act, rocblas_datatype_bf16_r, inter, &zero, out,
+                        rocblas_datatype_f32_r, out_stride, out, rocblas_datatype_f32_r, out_stride,
+                        rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, rocblas_gemm_flags_none) !=
+        rocblas_status_success)
+        return hipErrorLaunchFailure;
+    return hipSuccess;
+}
 
 hipError_t launch_shared_fp8(hipStream_t s, const uint8_t* wgu, const uint16_t* sgu, const uint8_t* wd,
                              const uint16_t* sd, const uint16_t* x, int x_stride, int rows, int hidden, int inter,

@@ -67,6 +67,7 @@ def _load() -> ctypes.CDLL:
         "gfr_moe_token_static": ([P, ctypes.POINTER(_Exl3Struct), I, I, P, P, P, P, P], I),
         "gfr_moe_destroy": ([VP], I),
         "gfr_shared_fp8_create": ([ctypes.POINTER(VP), I, I, I], I),
+        "gfr_fp8_prepare_bf16": ([P, ctypes.POINTER(_Fp8Struct), P, P], I),
         "gfr_shared_fp8_run": ([VP, P, ctypes.POINTER(_Fp8Struct), P, I, I, P, I], I),
         "gfr_shared_fp8_gu": ([VP], P),
         "gfr_shared_fp8_act": ([VP], P),
@@ -221,10 +222,22 @@ class Fp8SharedWeights:
     gu_scale: torch.Tensor
     down: torch.Tensor
     down_scale: torch.Tensor
+    gu_bf16: torch.Tensor = None      # the prefill form's bf16 copies (prepare_bf16), or None
+    down_bf16: torch.Tensor = None
 
     @property
     def hidden(self) -> int:
         return self.gu.shape[1]
+
+    def prepare_bf16(self, stream=None) -> "Fp8SharedWeights":
+        """The reference's prefill weight copies (f8_b16_copy, prefill.cu:7-17: bf16(fp8 * row scale)) via
+        gfr_fp8_prepare_bf16; windows of more than 16 rows then run the reference's prefill arithmetic."""
+        H, I = self.hidden, self.inter
+        self.gu_bf16 = torch.empty((2 * I, H), dtype=torch.bfloat16, device=self.gu.device)
+        self.down_bf16 = torch.empty((H, I), dtype=torch.bfloat16, device=self.gu.device)
+        st = self.struct()
+        _check(lib().gfr_fp8_prepare_bf16(_stream(stream), ctypes.byref(st), _ptr(self.gu_bf16), _ptr(self.down_bf16)))
+        return self
 
     @property
     def inter(self) -> int:
@@ -233,21 +246,27 @@ class Fp8SharedWeights:
     def check(self):
         H, I = self.hidden, self.inter
         want = {"gu": (2 * I, H), "gu_scale": (2 * I,), "down": (H, I), "down_scale": (H,)}
+        if self.gu_bf16 is not None or self.down_bf16 is not None:
+            want.update({"gu_bf16": (2 * I, H), "down_bf16": (H, I)})
         for name, shape in want.items():
             t = getattr(self, name)
+            if name.endswith("bf16"):
+                if t is None or tuple(t.shape) != shape or t.dtype != torch.bfloat16 or not t.is_contiguous():
+                    raise ValueError(f"{name}: want {shape} bf16 contiguous on GPU")
+                continue
             ok_dtype = t.dtype == torch.bfloat16 if name.endswith("scale") else t.element_size() == 1
             if tuple(t.shape) != shape or not ok_dtype or not t.is_contiguous() or t.device.type != "cuda":
                 raise ValueError(f"{name}: {tuple(t.shape)} {t.dtype}, want {shape} contiguous on GPU")
 
     def struct(self) -> "_Fp8Struct":
         self.check()
-        return _Fp8Struct(self.hidden, self.inter, *(_ptr(getattr(self, n))
-                                                     for n in ("gu", "gu_scale", "down", "down_scale")))
+        return _Fp8Struct(self.hidden, self.inter, *(_ptr(getattr(self, n)) for n in (
+            "gu", "gu_scale", "down", "down_scale", "gu_bf16", "down_bf16")))
 
 
 class _Fp8Struct(ctypes.Structure):
     _fields_ = [("hidden", ctypes.c_int), ("inter", ctypes.c_int)] + [
-        (n, ctypes.c_void_p) for n in ("gu", "gu_scale", "down", "down_scale")]
+        (n, ctypes.c_void_p) for n in ("gu", "gu_scale", "down", "down_scale", "gu_bf16", "down_bf16")]
 
 
 class _Engine:

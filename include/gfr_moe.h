@@ -179,7 +179,16 @@ typedef struct gfr_fp8_shared_weights {
     const uint16_t* gu_scale;
     const uint8_t* down;
     const uint16_t* down_scale;
+    const uint16_t* gu_bf16;     /* optional (NULL): the prefill form's bf16 copies, gfr_fp8_prepare_bf16 */
+    const uint16_t* down_bf16;
 } gfr_fp8_shared_weights;
+/* The prefill form's weights (the reference's f8_b16_copy, prefill.cu:7-17, run by Gemms::prepare_f8,
+ * prefill.rs:55-108): gu_bf16 [2 inter][hidden] and down_bf16 [hidden][inter] = bf16_rn(fp8(w) * row scale), written on
+ * the stream; 16-byte aligned. Windows of more than 16 rows whose weights carry these copies run the reference's
+ * prefill arithmetic (prefill.rs:127-150, batch.rs:1183-1195): gu = bf16(x . gu_bf16^T) and out = act . down_bf16^T as
+ * library GEMMs (rocBLAS, fp32 accumulation) around the same SwiGLU; windows of up to 16 rows, or without the copies,
+ * run the slice arithmetic above. */
+int gfr_fp8_prepare_bf16(hipStream_t stream, const gfr_fp8_shared_weights* w, uint16_t* gu_bf16, uint16_t* down_bf16);
 typedef struct gfr_shared_fp8 gfr_shared_fp8;
 int gfr_shared_fp8_create(gfr_shared_fp8** out, int hidden, int inter, int max_rows);
 int gfr_shared_fp8_run(gfr_shared_fp8* sh, hipStream_t stream, const gfr_fp8_shared_weights* w,

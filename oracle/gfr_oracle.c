@@ -418,3 +418,17 @@ void gfro_shared_swiglu(const float* gu, int inter, float limit, float* act) {
         act[j] = gfro_bf(gfro_bf(g / (1.f + expf(-g))) * u);
     }
 }
+
+void gfro_fp8_b16_copy(const uint8_t* w, const uint16_t* scale_bf16, int n, int k, uint16_t* out) {
+    for (int r = 0; r < n; ++r) {
+        const float s = gfro_bf16_to_f32(scale_bf16[r]);
+        for (int j = 0; j < k; ++j) {
+            const uint8_t b = w[(size_t)r * k + j];
+            const int e = (b >> 3) & 15, m = b & 7;
+            float x = e == 0 ? (float)m * 0.001953125f : ldexpf((float)(8 + m), e - 10);
+            if (e == 15 && m == 7) x = NAN;
+            if (b & 128) x = -x;
+            out[(size_t)r * k + j] = gfro_f32_to_bf16(x * s);
+        }
+    }
+}

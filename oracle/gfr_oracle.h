@@ -87,6 +87,9 @@ float gfro_fp8(uint8_t v);
  * sum of x[j] * fp8(w[n][j])) * bf16 scale[n]; round != 0: y rounded to bf16 (as a float). w [n][k] bytes. */
 void gfro_fp8_matmul(const float* x, const uint8_t* w, const uint16_t* scale_bf16, int k, int n, int sk, int round,
                      float* y);
+/* prefill.cu:7-17 f8_b16_copy: out[n][k] = bf16_rn(fp8(w[n][k]) * bf16 scale[n]) (bf16 bits; exponent 15 mantissa 7
+ * -> NaN there) */
+void gfro_fp8_b16_copy(const uint8_t* w, const uint16_t* scale_bf16, int n, int k, uint16_t* out);
 /* front.rs:669-675: act[j] = bf(bf(g / (1 + exp(-g))) * u), g = min(gu[j], limit), u = clamp(gu[inter + j], +-limit) */
 void gfro_shared_swiglu(const float* gu, int inter, float limit, float* act);
 

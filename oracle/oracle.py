@@ -42,7 +42,7 @@ def _load():
         "gfro_route_biased": ([P, P, ctypes.c_float, I, I, I, I, P, P], None),
         "gfro_combine": ([P, P, I, I, I, P], None),
         "gfro_fp8": ([ctypes.c_uint8], F), "gfro_fp8_matmul": ([P, P, P, I, I, I, I, P], None),
-        "gfro_shared_swiglu": ([P, I, F, P], None),
+        "gfro_shared_swiglu": ([P, I, F, P], None), "gfro_fp8_b16_copy": ([P, P, I, I, P], None),
         "gfro_baseline_decode": ([P, I, I, I, I, P, P, P, P, P, P, P, P, P, P, P], ctypes.c_double),
     }
     for n, (a, r) in sigs.items():
@@ -213,6 +213,16 @@ def fp8_matmul(x, w, scale_bf16, sk, round_bf16):
     y = np.empty(n, np.float32)
     lib().gfro_fp8_matmul(_p(x), _p(w), _p(sc), k, n, sk, 1 if round_bf16 else 0, _p(y))
     return y
+
+
+def fp8_b16_copy(w, scale_bf16):
+    """prefill.cu:7-17 f8_b16_copy: bf16 bits [n][k] of bf16_rn(fp8(w) * row scale)."""
+    w = np.ascontiguousarray(w, np.uint8)
+    sc = np.ascontiguousarray(scale_bf16, np.uint16)
+    n, k = w.shape
+    out = np.empty((n, k), np.uint16)
+    lib().gfro_fp8_b16_copy(_p(w), _p(sc), n, k, _p(out))
+    return out
 
 
 def shared_swiglu(gu, inter, limit=10.0):

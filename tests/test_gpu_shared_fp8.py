@@ -229,3 +229,97 @@ def test_moe_run_fp8_one_token_forms(gfr, oracle, routed, topk):
             graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(m.output[:1], got)
+
+
+# ---- the prefill form (prefill.rs:55-150, batch.rs:1183-1195): bf16 weight copies and library GEMMs -----------------
+@pytest.fixture(scope="module")
+def sw_prepared():
+    import synth
+    w = synth.fp8_shared(D, N, seed=79)
+    w.prepare_bf16()
+    torch.cuda.synchronize()
+    return w
+
+
+def test_prepare_bf16_bit_exact(oracle, sw_prepared):
+    """gfr_fp8_prepare_bf16 against the oracle's f8_b16_copy, bit for bit, both matrices."""
+    w = sw_prepared
+    got_gu = np_u16(w.gu_bf16)
+    got_d = np_u16(w.down_bf16)
+    np.testing.assert_array_equal(got_gu, oracle.fp8_b16_copy(w.gu.cpu().numpy(), np_u16(w.gu_scale)))
+    np.testing.assert_array_equal(got_d, oracle.fp8_b16_copy(w.down.cpu().numpy(), np_u16(w.down_scale)))
+
+
+@pytest.mark.parametrize("rows", [17, 300, 2048])
+def test_shared_fp8_prefill_form(gfr, oracle, sw_prepared, rows):
+    """More than 16 rows with the bf16 copies: gu = bf16(x . gu_bf16^T) within one bf16 step of the float64 product
+    (the library's fp32 order), act within one step of the oracle's SwiGLU of the kernel's gu, out within the fp32
+    accumulation bound of act . down_bf16^T; sampled rows, first, middle and last, and every row's chain within 1e-2
+    of the slice arithmetic's (the two forms differ by the weights' bf16 rounding)."""
+    w = sw_prepared
+    g = torch.Generator(device="cuda").manual_seed(rows)
+    x = torch.randn((rows, D), generator=g, device="cuda").to(torch.bfloat16)
+    sh = gfr.SharedFp8(D, N, rows)
+    out = sh.run(w, x, rows)
+    torch.cuda.synchronize()
+    gu_k = bf16_floats(np_u16(sh.gu[:rows]))
+    act_k = bf16_floats(np_u16(sh.act[:rows]))
+    out_k = out.cpu().numpy()
+    wg = bf16_floats(np_u16(w.gu_bf16)).astype(np.float64)
+    wd = bf16_floats(np_u16(w.down_bf16)).astype(np.float64)
+    xf = bf16_floats(np_u16(x)).astype(np.float64)
+    for r in sorted({0, rows // 2, rows - 1}):
+        gu64 = wg @ xf[r]
+        gu_o = torch.from_numpy(gu64.astype(np.float32)).to(torch.bfloat16).float().numpy()
+        assert_bf16_ulps(gu_k[r], gu_o, f"rows {rows} row {r} gu")
+        assert_bf16_ulps(act_k[r], oracle.shared_swiglu(gu_k[r], N), f"rows {rows} row {r} act", max_frac=0.01)
+        want = wd @ act_k[r].astype(np.float64)
+        bound = np.abs(wd) @ np.abs(act_k[r]).astype(np.float64) * N * 2.0 ** -23 + 1e-30
+        assert np.all(np.abs(out_k[r] - want) <= bound), f"rows {rows} row {r} out"
+    slice_form = sh.run(gfr.Fp8SharedWeights(w.gu, w.gu_scale, w.down, w.down_scale), x, rows)
+    torch.cuda.synchronize()
+    assert_rows_close(out_k, slice_form.cpu().numpy(), rel_rms=1e-2, rel_max=5e-2, what=f"rows {rows} vs slices")
+
+
+def test_shared_fp8_prefill_form_graph_replays(gfr, sw_prepared):
+    """The library GEMMs captured into a graph (their workspace set at create) replay to the eager bytes."""
+    rows = 64
+    x = torch.randn((rows, D), generator=torch.Generator(device="cuda").manual_seed(4), device="cuda").to(torch.bfloat16)
+    sh = gfr.SharedFp8(D, N, rows)
+    out = torch.zeros((rows, D), device="cuda")
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        sh.run(sw_prepared, x, rows, out=out, stream=s)
+    s.synchronize()
+    eager = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            sh.run(sw_prepared, x, rows, out=out, stream=s)
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
+def test_moe_run_fp8_prefill_form(gfr, sw_prepared, routed):
+    """A 40-row window of the layer with the bf16 copies: the shared slot gets the prefill form's output, byte-equal
+    to gfr_moe_run_shared fed gfr_shared_fp8's."""
+    rows = 40
+    g = torch.Generator(device="cuda").manual_seed(41)
+    x = torch.randn((rows, D), generator=g, device="cuda").to(torch.bfloat16)
+    lg = torch.randn((rows, E), generator=g, device="cuda")
+    m = gfr.Moe(D, N, E, TOPK, rows, shared_exl3=False)
+    m.run_fp8(routed, x, lg, sw_prepared, rows)
+    torch.cuda.synchronize()
+    got = m.output[:rows].clone()
+    shared = gfr.SharedFp8(D, N, rows).run(sw_prepared, x, rows)
+    torch.cuda.synchronize()
+    assert torch.equal(m.shared_output[:rows], shared)
+    m2 = gfr.Moe(D, N, E, TOPK, rows, shared_exl3=False)
+    m2.run(routed, x, lg, rows, shared=shared)
+    torch.cuda.synchronize()
+    assert torch.equal(m2.output[:rows], got)

@@ -483,3 +483,19 @@ def test_shared_swiglu_closed_form(oracle):
     # above the limit the gate saturates at silu(10): g = 10.5 and g = 30 give the act of g = 10
     np.testing.assert_array_equal(oracle.shared_swiglu(np.array([10.0, 30.0, 2.0, 2.0], np.float32), 2),
                                   oracle.shared_swiglu(np.array([10.0, 10.0, 2.0, 2.0], np.float32), 2))
+
+
+def test_fp8_b16_copy_vs_torch(oracle):
+    """prefill.cu:7-17 (the prefill form's weight copies): bf16_rn(fp8 * row scale) against torch's float8_e4m3fn
+    decode, an fp32 product and torch's bf16 rounding, every non-NaN byte value times several scales; the NaN codes
+    stay NaN."""
+    codes = np.arange(256, dtype=np.uint8)
+    scales = torch.tensor([1.0, 0.3, -2.5, 1e-3, 3.1e4], dtype=torch.bfloat16)
+    w = np.tile(codes, (len(scales), 1))
+    got = oracle.fp8_b16_copy(w, scales.view(torch.int16).numpy().view(np.uint16))
+    vals = torch.from_numpy(codes).view(torch.float8_e4m3fn).float()
+    want = (vals[None, :] * scales.float()[:, None]).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    ok = (codes & 0x7F) != 0x7F
+    np.testing.assert_array_equal(got[:, ok], want[:, ok])
+    gotf = (got.astype(np.uint32) << 16).view(np.float32)
+    assert np.all(np.isnan(gotf[:, ~ok]))
