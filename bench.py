@@ -287,13 +287,29 @@ def other_configs(args, copies, stream):
                    for j in range(glen)], stream)
     time_graphs([g2], stream)
     s2 = time_graphs([g2] * reps, stream) / (reps * glen)
+    # the same layer on a 4096-row prefill window (the reference's FastExperts probe size), its shared expert in the
+    # prefill form (bf16 copies, library GEMMs)
+    rows_p = 4096
+    mp = gfr_moe.Moe(Dr, Nr, Er, Kr, rows_p, shared_exl3=False)
+    mp.set_router(bias, 2.5)
+    for w in rs:
+        w.prepare_bf16(stream)
+    xp = synth.activations(rows_p, Dr, 973)
+    lp = synth.zipf_logits(rows_p, Er, Kr, 1.1, 974)
+    gp = graph_of([(lambda c=c: mp.run_fp8(rc[c], xp, lp, rs[c], rows_p, stream=stream)) for c in range(4)], stream)
+    time_graphs([gp], stream)
+    sp = time_graphs([gp] * 2, stream) / 8
+    flop_p = rows_p * (Kr + 1) * 2 * 3 * Dr * Nr
+    del gp, mp
     out["reference_layout"] = {
         "config": "the reference's layer geometry: hidden 4096, intermediate 512, 288 routed EXL3 experts (K=4) top-8 "
                   "(GLM gate) + the FP8 shared expert (moe.rs:132-167), one token, Zipf(1.1); the shared expert "
                   "runs inside the layer's gate/up and down launches", "us_per_token": round(secs * 1e6, 2),
         "tok_per_s": round(1 / secs, 1), "bytes_per_token": tok_bytes, "gbs": round(tok_bytes / secs / 1e9, 1),
         "hbm_frac": round(tok_bytes / secs / 1e9 / HBM_PEAK_GBS, 4),
-        "shared_fp8_alone_us": round(s2 * 1e6, 2), "shared_fp8_bytes": shared_bytes}
+        "shared_fp8_alone_us": round(s2 * 1e6, 2), "shared_fp8_bytes": shared_bytes,
+        "prefill_4096_rows_ms": round(sp * 1e3, 3), "prefill_tflops": round(flop_p / sp / 1e12, 1),
+        "prefill_mfma_frac": round(flop_p / sp / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
     del graph, g2, mr, sh, rc, rs
     torch.cuda.empty_cache()
 
@@ -499,7 +515,7 @@ def cpu_model():
     return None
 
 
-def cpu_baseline_c1(tokens=16):
+def cpu_baseline_c1(tokens=16, threads=16):
     """Config 1 on the host: per token the 2048 x 1536 K = 4 trellis decoded (gfro_unpack_f32) and the linear
     (gfro_linear: input scales, transform, fixed-order fp32 matvec, output transform and scales), scalar C, 1 thread,
     on seeded weights and fp16 tokens of the config's shape."""
@@ -511,16 +527,30 @@ def cpu_baseline_c1(tokens=16):
     sc = lambda k: ((rng.integers(0, 2, k) * 2 - 1) * (rng.random(k) + 0.5)).astype(np.float16).view(np.uint16)
     suh, svh = sc(kin), sc(n)
     xs = rng.standard_normal((tokens, kin)).astype(np.float16).view(np.uint16)
+    def token(t):
+        oracle.linear(xs[t % tokens], oracle.unpack_f32(words, kin, n, BITS), suh, svh)
+
     t0 = time.perf_counter()
     for t in range(tokens):
-        oracle.linear(xs[t], oracle.unpack_f32(words, kin, n, BITS), suh, svh)
+        token(t)
     secs = time.perf_counter() - t0
-    return {"value": round(tokens / secs, 3), "unit": "tok/s", "cores": 1, "kind": "port", "cpu_model": cpu_model(),
-            "sample": f"{tokens} tokens of config 1: per token the trellis decode + linear (oracle/gfr_oracle.c, "
-                      "scalar, 1 thread)", "seconds": round(secs, 2)}
+    one = {"value": round(tokens / secs, 3), "unit": "tok/s", "cores": 1, "kind": "port", "cpu_model": cpu_model(),
+           "sample": f"{tokens} tokens of config 1: per token the trellis decode + linear (oracle/gfr_oracle.c, "
+                     "scalar, 1 thread)", "seconds": round(secs, 2)}
+    # every core the job may use: one token a thread (the C calls drop the GIL)
+    from concurrent.futures import ThreadPoolExecutor
+    nt = max(1, min(threads, len(os.sched_getaffinity(0))))
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(max_workers=nt) as ex:
+        list(ex.map(token, range(2 * nt)))
+    wall = time.perf_counter() - t0
+    many = {"value": round(2 * nt / wall, 3), "unit": "tok/s", "cores": nt, "kind": "port", "cpu_model": cpu_model(),
+            "sample": f"{2 * nt} tokens of config 1 over {nt} threads, one token a thread at a time, same scalar C path",
+            "seconds": round(wall, 2)}
+    return one, many
 
 
-def cpu_baseline_c3(copies, rows=32):
+def cpu_baseline_c3(copies, rows=32, threads=16):
     """Config 3 on the host, row-batched: one 32-token Zipf(1.1) window; each distinct expert's trellis decoded once
     (gfro_unpack_f32), then every member row through it (gfro_expert_row: rotation, fixed-order fp32 matvecs,
     epilogues), then the combine; scalar C, 1 thread."""
@@ -536,19 +566,34 @@ def cpu_baseline_c3(copies, rows=32):
     words = {e: (np_u32(w.gt[e]), np_u32(w.ut[e]), np_u32(w.dt[e])) for e in used}
     vec = {nm: np_u16(getattr(w, nm)) for nm in ("suh_g", "suh_u", "suh_d", "svh_g", "svh_u", "svh_d")}
     y = np.empty((rows, SLOTS, D), np.float32)
-    t0 = time.perf_counter()
-    for e in used:
+
+    def expert(e):
         wg, wu, wd = (oracle.unpack_f32(words[e][0], D, N, BITS), oracle.unpack_f32(words[e][1], D, N, BITS),
                       oracle.unpack_f32(words[e][2], N, D, BITS))
         for r, s in zip(*np.nonzero(picks == e)):
             y[r, s] = oracle.expert_row(x[r], wg, wu, wd, *(vec[nm][e] for nm in ("suh_g", "suh_u", "suh_d", "svh_g",
                                                                                    "svh_u", "svh_d")),
                                         sk_gu=1, sk_d=1, warps=1)[0]
+
+    t0 = time.perf_counter()
+    for e in used:
+        expert(e)
     oracle.combine(y, weights, rows, SLOTS)
     secs = time.perf_counter() - t0
-    return {"value": round(rows / secs, 3), "unit": "tok/s", "cores": 1, "kind": "port", "cpu_model": cpu_model(),
-            "sample": f"one {rows}-token window of config 3 ({len(used)} distinct experts, each decoded once, then "
-                      "its member rows; oracle/gfr_oracle.c, scalar, 1 thread)", "seconds": round(secs, 2)}
+    one = {"value": round(rows / secs, 3), "unit": "tok/s", "cores": 1, "kind": "port", "cpu_model": cpu_model(),
+           "sample": f"one {rows}-token window of config 3 ({len(used)} distinct experts, each decoded once, then "
+                     "its member rows; oracle/gfr_oracle.c, scalar, 1 thread)", "seconds": round(secs, 2)}
+    # every core the job may use: the window's experts dealt to the threads (the C calls drop the GIL)
+    from concurrent.futures import ThreadPoolExecutor
+    nt = max(1, min(threads, len(os.sched_getaffinity(0))))
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(max_workers=nt) as ex:
+        list(ex.map(expert, used))
+    oracle.combine(y, weights, rows, SLOTS)
+    wall = time.perf_counter() - t0
+    many = {"value": round(rows / wall, 3), "unit": "tok/s", "cores": nt, "kind": "port", "cpu_model": cpu_model(),
+            "sample": f"the same window with its {len(used)} experts dealt over {nt} threads", "seconds": round(wall, 2)}
+    return one, many
 
 
 def counter_summary(path):
@@ -646,11 +691,13 @@ def main():
     if not args.no_extra:
         extra = other_configs(args, copies, stream)
         log("other configs: " + json.dumps(extra))
-    cpu = cpu_all = cpu_c1 = cpu_c3 = None
+    cpu = cpu_all = cpu_c1 = cpu_c3 = cpu_c1_all = cpu_c3_all = None
     if not args.no_cpu:
         cpu, cpu_all = cpu_baseline(args, copies, xs, logits)
-        cpu_c1, cpu_c3 = cpu_baseline_c1(), cpu_baseline_c3(copies)
-        log(f"cpu baseline c1: {cpu_c1['value']} tok/s; c3: {cpu_c3['value']} tok/s")
+        (cpu_c1, cpu_c1_all), (cpu_c3, cpu_c3_all) = (cpu_baseline_c1(threads=args.cpu_threads),
+                                                      cpu_baseline_c3(copies, threads=args.cpu_threads))
+        log(f"cpu baseline c1: {cpu_c1['value']} tok/s ({cpu_c1_all['value']} on {cpu_c1_all['cores']} threads); "
+            f"c3: {cpu_c3['value']} tok/s ({cpu_c3_all['value']})")
         log(f"cpu baseline: {cpu['value']} tok/s over {cpu['seconds']} s; {cpu_all['cores']} threads "
             f"{cpu_all['value']} tok/s")
     out = {
@@ -662,7 +709,8 @@ def main():
                    "parallelism": "single-gpu", "weight_copies": args.copies, "routings": args.routings,
                    "weight_bytes_cycled": int(args.copies * (E + 1) * 3 * D * N * BITS // 8)},
         "roofline": roof, "cpu_baseline": cpu, "cpu_baseline_all_cores": cpu_all,
-        "cpu_baseline_other_configs": {"c1": cpu_c1, "c3": cpu_c3}, "prefill": prefill,
+        "cpu_baseline_other_configs": {"c1": cpu_c1, "c1_all_cores": cpu_c1_all, "c3": cpu_c3,
+                                       "c3_all_cores": cpu_c3_all}, "prefill": prefill,
         "other_configs": extra,
     }
     print(json.dumps(out), flush=True)
