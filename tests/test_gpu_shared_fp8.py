@@ -193,14 +193,15 @@ def test_prepared_shared_fp8(gfr, sw, routed, tmp_path):
         p.shared_fp8(1)
 
 
-@pytest.mark.parametrize("routed,topk", [(16, 4), (4, 4)])
-def test_moe_run_fp8_one_token_forms(gfr, oracle, routed, topk):
+@pytest.mark.parametrize("routed,topk,H,I", [(16, 4, 512, 256), (4, 4, 512, 256), (64, 4, 2048, 1536),
+                                             (24, 8, 5120, 1536)])
+def test_moe_run_fp8_one_token_forms(gfr, oracle, routed, topk, H, I):
     """One token: with at least `slots` routed experts the shared expert rides on the EXL3 gate/up and down launches
     (the shared slot's workgroups); with fewer (4 routed, top-4: the grid has no shared unit) it runs its own two
     launches first. Both give the bytes of gfr_moe_run_shared fed with gfr_shared_fp8's output, eagerly and in every
-    replay of a captured graph."""
+    replay of a captured graph; at config 2's shape (one-wave down programs) and config 5's (hidden 5120: two output
+    blocks a down workgroup, 10 gate/up splits) as well."""
     import synth
-    H, I = 512, 256
     w = synth.experts(routed, H, I, BITS, seed=routed)
     sw1 = synth.fp8_shared(H, I, seed=routed + 1)
     x = torch.randn((1, H), generator=torch.Generator(device="cuda").manual_seed(2), device="cuda").to(torch.bfloat16)
