@@ -324,3 +324,35 @@ def test_moe_run_fp8_prefill_form(gfr, sw_prepared, routed):
     m2.run(routed, x, lg, rows, shared=shared)
     torch.cuda.synchronize()
     assert torch.equal(m2.output[:rows], got)
+
+
+def test_moe_reference_prefill_window_with_fp8_shared(gfr, oracle, sw_prepared, routed):
+    """The reference's own prefill shape (4096 rows, fast_experts.rs:230-286's window size) through the whole layer
+    with its FP8 shared expert in the prefill form: sampled tokens (first, middle, last) against the oracle's routed
+    rows (the reference's fp16 weights, full-K order) plus the prefill form's shared row (float64 over the bf16
+    copies); and a row permutation of the window permutes the outputs bit for bit (rows are independent)."""
+    rows = 4096
+    g = torch.Generator(device="cuda").manual_seed(4096)
+    x = torch.randn((rows, D), generator=g, device="cuda").to(torch.bfloat16)
+    lg = torch.randn((rows, E), generator=g, device="cuda")
+    m = gfr.Moe(D, N, E, TOPK, rows, shared_exl3=False)
+    m.run_fp8(routed, x, lg, sw_prepared, rows)
+    torch.cuda.synchronize()
+    got = m.output[:rows].clone()
+    gp, gw = m.picks[:rows].cpu().numpy(), m.weights[:rows].cpu().numpy()
+    dec = DecodedExperts(oracle, routed)
+    xb = np_u16(x)
+    wg = bf16_floats(np_u16(sw_prepared.gu_bf16)).astype(np.float64)
+    wd = bf16_floats(np_u16(sw_prepared.down_bf16)).astype(np.float64)
+    for r in (0, rows // 2, rows - 1):
+        ys = [dec.row(xb[r], int(e), sk_gu=1, sk_d=1, warps=1)[0] for e in gp[r, :TOPK]]
+        gu = torch.from_numpy((wg @ bf16_floats(xb[r]).astype(np.float64)).astype(np.float32))
+        gu = gu.to(torch.bfloat16).float().numpy()
+        act = oracle.shared_swiglu(gu, N)
+        ys.append((wd @ act.astype(np.float64)).astype(np.float32))
+        want = oracle.combine(np.stack(ys), gw[r:r + 1], 1, TOPK + 1)[0]
+        assert_close(got[r].cpu().numpy(), want, rel_rms=1e-2, rel_max=5e-2, what=f"token {r}")
+    perm = torch.randperm(rows, generator=torch.Generator().manual_seed(7)).cuda()
+    m.run_fp8(routed, x[perm].contiguous(), lg[perm].contiguous(), sw_prepared, rows)
+    torch.cuda.synchronize()
+    assert torch.equal(m.output[:rows], got[perm])
