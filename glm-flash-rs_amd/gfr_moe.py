@@ -229,6 +229,10 @@ class Fp8SharedWeights:
     def hidden(self) -> int:
         return self.gu.shape[1]
 
+    @property
+    def inter(self) -> int:
+        return self.gu.shape[0] // 2
+
     def prepare_bf16(self, stream=None) -> "Fp8SharedWeights":
         """The reference's prefill weight copies (f8_b16_copy, prefill.cu:7-17: bf16(fp8 * row scale)) via
         gfr_fp8_prepare_bf16; windows of more than 16 rows then run the reference's prefill arithmetic."""
@@ -239,24 +243,22 @@ class Fp8SharedWeights:
         _check(lib().gfr_fp8_prepare_bf16(_stream(stream), ctypes.byref(st), _ptr(self.gu_bf16), _ptr(self.down_bf16)))
         return self
 
-    @property
-    def inter(self) -> int:
-        return self.gu.shape[0] // 2
-
     def check(self):
         H, I = self.hidden, self.inter
         want = {"gu": (2 * I, H), "gu_scale": (2 * I,), "down": (H, I), "down_scale": (H,)}
         if self.gu_bf16 is not None or self.down_bf16 is not None:
             want.update({"gu_bf16": (2 * I, H), "down_bf16": (H, I)})
-        for name, shape in want.items():
+        for name, shape in want.items():      # shapes and dtypes first, then where the tensors live
             t = getattr(self, name)
-            if name.endswith("bf16"):
-                if t is None or tuple(t.shape) != shape or t.dtype != torch.bfloat16 or not t.is_contiguous():
-                    raise ValueError(f"{name}: want {shape} bf16 contiguous on GPU")
-                continue
-            ok_dtype = t.dtype == torch.bfloat16 if name.endswith("scale") else t.element_size() == 1
-            if tuple(t.shape) != shape or not ok_dtype or not t.is_contiguous() or t.device.type != "cuda":
-                raise ValueError(f"{name}: {tuple(t.shape)} {t.dtype}, want {shape} contiguous on GPU")
+            bf = name.endswith("scale") or name.endswith("bf16")
+            if t is None or tuple(t.shape) != shape or (t.dtype == torch.bfloat16) != bf or t.element_size() != (
+                    2 if bf else 1):
+                got = "missing" if t is None else f"{tuple(t.shape)} {t.dtype}"
+                raise ValueError(f"{name}: {got}, want {shape} {'bf16' if bf else 'e4m3 bytes'}")
+        for name in want:
+            t = getattr(self, name)
+            if not t.is_contiguous() or t.device.type != "cuda":
+                raise ValueError(f"{name}: want a contiguous tensor on the GPU")
 
     def struct(self) -> "_Fp8Struct":
         self.check()

@@ -113,3 +113,32 @@ def test_shared_fp8_run_rejects_null_and_moe_fp8_without_engine():
     assert L.gfr_shared_fp8_run(None, None, None, None, 4096, 1, None, 4096) == gfr_moe.GFR_EINVAL
     assert L.gfr_moe_run_fp8(None, None, None, None, None, None, 1) == gfr_moe.GFR_EINVAL
     assert L.gfr_moe_run_router_fp8(None, None, None, None, None, None, 1) == gfr_moe.GFR_EINVAL
+
+
+def test_fp8_shared_weights_host_checks():
+    """Fp8SharedWeights refuses tensors of the wrong shape, dtype or device before any library call (no GPU)."""
+    import torch
+    import gfr_moe
+    H, I = 512, 64
+    ok = dict(gu=torch.zeros((2 * I, H), dtype=torch.uint8), gu_scale=torch.zeros(2 * I, dtype=torch.bfloat16),
+              down=torch.zeros((H, I), dtype=torch.uint8), down_scale=torch.zeros(H, dtype=torch.bfloat16))
+    w = gfr_moe.Fp8SharedWeights(**ok)
+    assert w.hidden == H and w.inter == I
+    with pytest.raises(ValueError, match="GPU"):          # host tensors
+        w.check()
+    bad = dict(ok, gu_scale=torch.zeros(2 * I, dtype=torch.float16))
+    with pytest.raises(ValueError, match="gu_scale"):
+        gfr_moe.Fp8SharedWeights(**bad).check()
+    bad = dict(ok, down=torch.zeros((I, H), dtype=torch.uint8))
+    with pytest.raises(ValueError, match="down"):
+        gfr_moe.Fp8SharedWeights(**bad).check()
+    half = gfr_moe.Fp8SharedWeights(**ok, gu_bf16=torch.zeros((2 * I, H), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="bf16"):          # one copy without the other
+        half.check()
+
+
+def test_fp8_prepare_and_prepared_lookup_reject():
+    import gfr_moe
+    L = gfr_moe.lib()
+    assert L.gfr_fp8_prepare_bf16(None, None, None, None) == gfr_moe.GFR_EINVAL
+    assert L.gfr_prepared_shared_fp8(None, 0, None) != 0
