@@ -187,7 +187,8 @@ typedef struct gfr_fp8_shared_weights {
  * the stream; 16-byte aligned. Windows of more than 16 rows whose weights carry these copies run the reference's
  * prefill arithmetic (prefill.rs:127-150, batch.rs:1183-1195): gu = bf16(x . gu_bf16^T) and out = act . down_bf16^T as
  * library GEMMs (rocBLAS, fp32 accumulation) around the same SwiGLU; windows of up to 16 rows, or without the copies,
- * run the slice arithmetic above. */
+ * run the slice arithmetic above. The library may load a GEMM's code on the first call of a shape: make one eager
+ * call of a window size before capturing it into a graph (the engine's workspace is set at create). */
 int gfr_fp8_prepare_bf16(hipStream_t stream, const gfr_fp8_shared_weights* w, uint16_t* gu_bf16, uint16_t* down_bf16);
 typedef struct gfr_shared_fp8 gfr_shared_fp8;
 int gfr_shared_fp8_create(gfr_shared_fp8** out, int hidden, int inter, int max_rows);
