@@ -172,6 +172,26 @@ def calibrate_copy():
     del src, dst
 
 
+def measure_copy(nbytes=1 << 30, reps=5):
+    """A plain device-to-device copy of 1 GiB (torch's copy kernel), timed with HIP events: the bytes it reads plus
+    the bytes it writes over its time, the part's achievable HBM rate beside the published 8 TB/s peak."""
+    import torch
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    secs = e0.elapsed_time(e1) / 1e3 / reps
+    del src, dst
+    torch.cuda.empty_cache()
+    return round(2 * nbytes / secs / 1e9, 1)
+
+
 def prefill_bench(args, copies, stream):
     """Config 4: one MoE layer on an 8192-token prefill chunk, uniform top-4 routing (+ the shared expert)."""
     import torch
@@ -663,6 +683,7 @@ def main():
     read_ahead = SLOTS * D * N * BITS // 8
     roof = {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+            "measured_copy_gbs": measure_copy(),
             "kernel": "expert_gemv_kernel<4,8,4,2,1,1,true> (the layer's gate/up launch: router, input rotation, "
                       "gate and up trellis GEMV)",
             "bytes_per_launch": nbytes["gate_up"], "us_per_launch": round(launches_us["gate_up"], 3),
