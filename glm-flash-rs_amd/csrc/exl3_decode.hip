@@ -330,6 +330,7 @@ __device__ __forceinline__ void expert_gemv_body(const GemvArgs& a, const Fp8Arg
     // loads into dependent rounds)
     __builtin_amdgcn_sched_barrier(0);
 
+    const CodewordConsts cc = codeword_consts<K>();
     // the chunk of up to RB members (its activations are already loading)
     auto chunk = [&](int r0, int nr) {
         build_acts(r0, nr, [&]() {
@@ -349,7 +350,7 @@ __device__ __forceinline__ void expert_gemv_body(const GemvArgs& a, const Fp8Arg
             for (int j = 0; j < K; ++j) __asm__ volatile("" : "+v"(wr[kk][j]));
             const uint32_t prev = prev_word(wr[kk][K - 1], i);
             uint32_t cw[32];
-            lane_words<K>(wr[kk], prev, cw);
+            lane_words<K>(wr[kk], prev, cw, cc);
 #pragma unroll
             for (int m = 0; m < RB; ++m) {
                 if (m < nr) {
@@ -622,13 +623,14 @@ __device__ __forceinline__ void down_gemv_body(const GemvArgs& a, const Fp8Args&
         }
     }
     // ---- this wave's two tiles of the first block decoded (they wait for their own words only)
+    const CodewordConsts cc = codeword_consts<K>();
     uint32_t cw[TPW][32];
     auto decode_block = [&](int h) {
 #pragma unroll
         for (int kk = 0; kk < TPW; ++kk) {
 #pragma unroll
             for (int j = 0; j < K; ++j) __asm__ volatile("" : "+v"(wr[h][kk][j]));
-            lane_words<K>(wr[h][kk], prev_word(wr[h][kk][K - 1], i), cw[kk]);
+            lane_words<K>(wr[h][kk], prev_word(wr[h][kk][K - 1], i), cw[kk], cc);
         }
     };
     decode_block(0);

@@ -30,6 +30,10 @@ __device__ __forceinline__ h2_t bits_h2(uint32_t v) { return __builtin_bit_cast(
 // x.hi = (s * 0xCBAC + ((s * 0x1FED) >> 16)) mod 2^16, with s * 0x1FED < 2^29 exact in a 24-bit multiply.
 // hipcc emits 8 VALU ops a pair: 2 v_mul_u32_u24 (SDWA word select), 2 v_perm, v_pk_mad_u16, 2 v_bitop3, v_pk_add_f16.
 typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+// (x & m) ^ f as one v_bitop3 (truth table over src0 = 0xF0, src1 = 0xCC, src2 = 0xAA: (0xF0 & 0xCC) ^ 0xAA = 0x6A)
+__device__ __forceinline__ uint32_t mask_flip(uint32_t x, uint32_t m, uint32_t f) {
+    return __builtin_amdgcn_bitop3_b32(x, m, f, 0x6A);
+}
 __device__ __forceinline__ h2_t decode_pair(uint32_t S) {
     const uint32_t pa = (S & 0xffffu) * 0x1FEDu;
     const uint32_t pb = (S >> 16) * 0x1FEDu;
@@ -116,23 +120,48 @@ __device__ __forceinline__ void decode_lane(const uint32_t (&w)[K], uint32_t pre
 // 0x3B603B60 (experts.rs:43-46) holds the two fp16 halves whose sum is the weight. The GEMV adds both halves times
 // the activation in one v_dot2_f32_f16 against the activation staged twice, (x, x): acc + x * m.lo + x * m.hi in
 // fp32. The reference rounds m.lo + m.hi to fp16 first; this sum keeps that rounding
-// out (a difference of at most half an fp16 ulp of each weight). Four VALU operations a weight:
-//   v_pk_mul_lo_u16  (0, s * 0xCBAC)                  (the high half of s * 0xCBAC0000)
-//   v_mad_u32_u16    s * 0x1FED + (s * 0xCBAC << 16) = s * 0xCBAC1FED mod 2^32
-//   v_bitop3         mask, flip
-//   v_dot2_f32_f16   acc += x * m.lo + x * m.hi
-// (op_sel on the v_dot2 operands is not encodable on gfx950, hence the doubled activations.)
-template <int SEL>
-__device__ __forceinline__ uint32_t codeword(uint32_t r) {
-    uint32_t t, x;
-    if constexpr (SEL == 0) {
-        __asm__("v_pk_mul_lo_u16 %0, %1, %2 op_sel:[0,0] op_sel_hi:[0,1]" : "=v"(t) : "v"(r), "s"(0xCBAC0000u));
-        __asm__("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(x) : "v"(r), "s"(0x1FEDu), "v"(t));
+// out (a difference of at most half an fp16 ulp of each weight). Four VALU operations a weight at K = 4:
+//   v_and_b32 / v_lshrrev_b32   the state's half of r, alone in a register
+//   v_mul_lo_u32                s * 0xCBAC1FED mod 2^32
+//   v_bitop3                    mask, flip
+//   v_dot2_f32_f16              acc += x * m.lo + x * m.hi
+// Every constant is a VGPR operand (CodewordConsts): on gfx950 an SGPR or literal operand makes a VALU operation of
+// two issue passes where the all-VGPR v_and / v_lshrrev / v_bitop3 take one. Measured per decoded state and SIMD,
+// three waves a SIMD: 8.62 ns for the earlier form (v_pk_mul_lo_u16 + v_mad_u32_u16 with SGPR constants, SGPR mask),
+// 7.82 ns for this one. The other widths: v_pk_mul_lo_u16 (0, s * 0xCBAC) and v_mad_u32_u16 s * 0x1FED + that, then
+// the mask and the dot. (op_sel on the v_dot2 operands is not encodable on gfx950, hence the doubled activations.)
+struct CodewordConsts {
+    uint32_t lo16, mul, mask, flip;
+};
+// Made once per kernel: at K = 4 the asm hides the values, so the compiler keeps them in VGPRs and does not fold
+// them (the other widths' codeword does not read them).
+template <int K>
+__device__ __forceinline__ CodewordConsts codeword_consts() {
+    CodewordConsts c{0xffffu, 0xCBAC1FEDu, 0x8FFF8FFFu, 0x3B603B60u};
+    if constexpr (K == 4) __asm__ volatile("" : "+v"(c.lo16), "+v"(c.mul), "+v"(c.mask), "+v"(c.flip));
+    return c;
+}
+// K = 4 (config 2's width) takes the v_mul_lo_u32 form with VGPR constants; the other widths keep v_pk_mul_lo_u16 +
+// v_mad_u32_u16, whose op_sel picks the state's half without a mask (measured: the mul form is 2 % faster on
+// config 2's layer, and 1-2 % slower at K = 2 and 3, whose kernels lose a resident wave to its two extra VGPRs).
+template <int SEL, int K>
+__device__ __forceinline__ uint32_t codeword(uint32_t r, const CodewordConsts& c) {
+    uint32_t x;
+    if constexpr (K == 4) {
+        const uint32_t s = SEL == 0 ? (r & c.lo16) : (r >> 16);
+        x = s * c.mul;
     } else {
-        __asm__("v_pk_mul_lo_u16 %0, %1, %2 op_sel:[1,0] op_sel_hi:[1,1]" : "=v"(t) : "v"(r), "s"(0xCBAC0000u));
-        __asm__("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[1,0,0,0]" : "=v"(x) : "v"(r), "s"(0x1FEDu), "v"(t));
+        uint32_t t;
+        if constexpr (SEL == 0) {
+            __asm__("v_pk_mul_lo_u16 %0, %1, %2 op_sel:[0,0] op_sel_hi:[0,1]" : "=v"(t) : "v"(r), "s"(0xCBAC0000u));
+            __asm__("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(x) : "v"(r), "s"(0x1FEDu), "v"(t));
+        } else {
+            __asm__("v_pk_mul_lo_u16 %0, %1, %2 op_sel:[1,0] op_sel_hi:[1,1]" : "=v"(t) : "v"(r), "s"(0xCBAC0000u));
+            __asm__("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[1,0,0,0]" : "=v"(x) : "v"(r), "s"(0x1FEDu), "v"(t));
+        }
+        return (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
     }
-    return (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
+    return mask_flip(x, c.mask, c.flip);
 }
 // The lane's stream shifted right so that the window of value Q ends at bit 0, all 32 bits (bits 16-31: the 16
 // stream bits before the window).
@@ -146,26 +175,28 @@ __device__ __forceinline__ uint32_t lane_window32(const uint32_t (&w)[K], uint32
 // Masked codebook words of the lane's 32 values, value order. K = 2 and 4: one 32-bit window holds the states of
 // values Q (low half) and Q - 16 / K (high half).
 template <int K, int Q>
-__device__ __forceinline__ void lane_word(const uint32_t (&w)[K], uint32_t prev, uint32_t (&m)[32]) {
+__device__ __forceinline__ void lane_word(const uint32_t (&w)[K], uint32_t prev, uint32_t (&m)[32],
+                                          const CodewordConsts& c) {
     if constexpr (K == 2 || K == 4) {
         constexpr int D = 16 / K;
         if constexpr (Q % (2 * D) >= D) {
             const uint32_t r = lane_window32<K, Q>(w, prev);
-            m[Q] = codeword<0>(r);
-            m[Q - D] = codeword<1>(r);
+            m[Q] = codeword<0, K>(r, c);
+            m[Q - D] = codeword<1, K>(r, c);
         }
     } else {
-        m[Q] = codeword<0>(lane_window<K, Q>(w, prev));
+        m[Q] = codeword<0, K>(lane_window<K, Q>(w, prev), c);
     }
 }
 template <int K, int... Q>
 __device__ __forceinline__ void lane_words_(const uint32_t (&w)[K], uint32_t prev, uint32_t (&m)[32],
-                                            std::integer_sequence<int, Q...>) {
-    (lane_word<K, Q>(w, prev, m), ...);
+                                            const CodewordConsts& c, std::integer_sequence<int, Q...>) {
+    (lane_word<K, Q>(w, prev, m, c), ...);
 }
 template <int K>
-__device__ __forceinline__ void lane_words(const uint32_t (&w)[K], uint32_t prev, uint32_t (&m)[32]) {
-    lane_words_<K>(w, prev, m, std::make_integer_sequence<int, 32>{});
+__device__ __forceinline__ void lane_words(const uint32_t (&w)[K], uint32_t prev, uint32_t (&m)[32],
+                                           const CodewordConsts& c) {
+    lane_words_<K>(w, prev, m, c, std::make_integer_sequence<int, 32>{});
 }
 
 // Tile row of value q of a lane (the format's row 2 (q / 8) + (j & 1) + 8 ((j >> 1) & 1), j = q % 8) and its column
