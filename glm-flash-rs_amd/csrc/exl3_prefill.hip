@@ -663,11 +663,15 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
     decode_a(0, a0);
     // one step: multiply (ac, B fragments of the ring) while an is decoded for step s + 1 and the ring is refilled
     // D fragments ahead (the last D of them from step s + 1's stage)
-    auto step = [&](int s, int slot, const h8_t (&ac)[4], h8_t (&an)[4]) {
+    // FAST (a trip of steps known to be in the steady state, s + NS - 1 < S for each): the stage wait is the steady
+    // one and every step issues
+    auto step = [&](int s, int slot, const h8_t (&ac)[4], h8_t (&an)[4], auto fast) {
+        constexpr bool FAST = decltype(fast)::value;
         // stage s + 1 landed (at most the stages after it in flight) and every wave is done with stage s - 1
-        wait_stages(min(S - 1, s + NS - 2) - (s + 1));
+        if constexpr (FAST) wait_vmcnt<(NS - 3) * LOADS>();
+        else wait_stages(min(S - 1, s + NS - 2) - (s + 1));
         lds_barrier();
-        if (s + NS - 1 < S) issue(s + NS - 1);           // into stage s - 1's buffer, now free
+        if (FAST || s + NS - 1 < S) issue(s + NS - 1);   // into stage s - 1's buffer, now free
         const int sn = (slot + 1) % NS;                   // the next step's slot (the last step reads a stale one,
                                                           // unused)
         {
@@ -676,6 +680,11 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
             const uint32_t* twn = reinterpret_cast<const uint32_t*>(lds + sn * STAGE + MATS * XBUF);
             uint32_t wp[4], w0[4], w1[4], st[4];
             uint32_t wk[2][K == 4 ? 1 : 4];                // K = 3, 5: words of two tiles, one read ahead
+            // the row-block count as an SGPR value opaque to the compiler at every step: each block's test is then
+            // one s_cmp / s_cbranch_scc; left visible, the tests are hoisted out of the loop as lane masks and each
+            // is rebuilt in the loop with a v_cndmask and a v_cmp (22 VALU instructions a step at 11 blocks)
+            int nbs = nblk;
+            __asm__ volatile("" : "+s"(nbs));
             if constexpr (K == 4) {
 #pragma unroll
                 for (int t4 = 0; t4 < 4; ++t4) frag4_words(twn + (stile0 + t4) * 64, lane, wp[t4], w0[t4], w1[t4]);
@@ -686,7 +695,7 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
             for (int b = 0; b < RB; ++b) {
                 const h8_t bc = ring[b % D];
                 ring[b % D] = b + D < RB ? read_b(slot, b + D) : read_b(sn, b + D - RB);
-                if (b < nblk) {
+                if (b < nbs) {
 #pragma unroll
                     for (int t4 = 0; t4 < 4; ++t4)
                         acc[t4][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac[t4], bc, acc[t4][b], 0, 0, 0);
@@ -717,15 +726,24 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
     // roles instead of being copied
     constexpr int UNR = NS % 2 == 0 ? NS : 2 * NS;
     int s = 0;
+    const std::integral_constant<bool, true> fast;
+    const std::integral_constant<bool, false> general;
+    for (; s + UNR + NS - 2 < S; s += UNR) {
+#pragma unroll
+        for (int u = 0; u < UNR; u += 2) {
+            step(s + u, u % NS, a0, a1, fast);
+            step(s + u + 1, (u + 1) % NS, a1, a0, fast);
+        }
+    }
     for (; s + UNR <= S; s += UNR) {
 #pragma unroll
         for (int u = 0; u < UNR; u += 2) {
-            step(s + u, u % NS, a0, a1);
-            step(s + u + 1, (u + 1) % NS, a1, a0);
+            step(s + u, u % NS, a0, a1, general);
+            step(s + u + 1, (u + 1) % NS, a1, a0, general);
         }
     }
     for (; s < S; ++s) {
-        step(s, s % NS, a0, a1);
+        step(s, s % NS, a0, a1, general);
 #pragma unroll
         for (int t4 = 0; t4 < 4; ++t4) a0[t4] = a1[t4];
     }
