@@ -782,8 +782,10 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
                 sc[m][2 * i + 1] = f16_to_f32((uint16_t)(vv[i] >> 16));
             }
         }
-        // the transformed accumulators carry lane_sign: fold it into the scales that multiply them (exact)
-        const float sg = lane_sign(lane);
+        // the transformed accumulators carry lane_sign: fold it into the scales that multiply them (exact), and the
+        // transform's 1/sqrt(128) as well (one multiply a value instead of two: v * (HAD svh) rounds where the
+        // reference's (v * HAD) * svh may differ in the last fp32 bit, ahead of a bf16 or fp32 result)
+        const float sg = lane_sign(lane) * HAD_SCALE;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             sc[0][i] *= sg;
@@ -826,12 +828,16 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
 #pragma unroll
                 for (int i = 0; i < 8; i += 2) {
                     // bf16 roundings two values at a time (g with u, then element i with i + 1)
-                    float g0 = gv[i] * HAD_SCALE * sc[0][i], u0 = uv[i] * HAD_SCALE * sc[1][i];
-                    float g1 = gv[i + 1] * HAD_SCALE * sc[0][i + 1], u1 = uv[i + 1] * HAD_SCALE * sc[1][i + 1];
+                    float g0 = gv[i] * sc[0][i], u0 = uv[i] * sc[1][i];
+                    float g1 = gv[i + 1] * sc[0][i + 1], u1 = uv[i + 1] * sc[1][i + 1];
                     bf16r2(g0, u0);
                     bf16r2(g1, u1);
-                    const float gg0 = fminf(g0, a.limit), uu0 = __builtin_amdgcn_fmed3f(u0, -a.limit, a.limit);
-                    const float gg1 = fminf(g1, a.limit), uu1 = __builtin_amdgcn_fmed3f(u1, -a.limit, a.limit);
+                    // min(g, limit) for the finite g here, as a med3 against a huge negative bound (fminf, or a med3
+                    // against -inf that the compiler turns back into it, adds a NaN-quieting v_max of each input)
+                    const float gg0 = __builtin_amdgcn_fmed3f(g0, -3.0e38f, a.limit);
+                    const float gg1 = __builtin_amdgcn_fmed3f(g1, -3.0e38f, a.limit);
+                    const float uu0 = __builtin_amdgcn_fmed3f(u0, -a.limit, a.limit);
+                    const float uu1 = __builtin_amdgcn_fmed3f(u1, -a.limit, a.limit);
                     // silu through the hardware exp2 / reciprocal (within an ulp or two of expf and the IEEE divide;
                     // the bf16 rounding that follows absorbs the difference)
                     const float ex0 = __builtin_amdgcn_exp2f(gg0 * -1.4426950408889634f);
@@ -855,10 +861,10 @@ __global__ void __launch_bounds__(256, BM == 256 ? 1 : 2) prefill_gemm_kernel(co
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
                         float4* dst = reinterpret_cast<float4*>(a.y + (size_t)rows_sh[row] * a.N + col0 + h * 128 + 8 * j8);
-                        dst[0] = make_float4(v[h][0] * HAD_SCALE * sc[h][0], v[h][1] * HAD_SCALE * sc[h][1],
-                                             v[h][2] * HAD_SCALE * sc[h][2], v[h][3] * HAD_SCALE * sc[h][3]);
-                        dst[1] = make_float4(v[h][4] * HAD_SCALE * sc[h][4], v[h][5] * HAD_SCALE * sc[h][5],
-                                             v[h][6] * HAD_SCALE * sc[h][6], v[h][7] * HAD_SCALE * sc[h][7]);
+                        dst[0] = make_float4(v[h][0] * sc[h][0], v[h][1] * sc[h][1], v[h][2] * sc[h][2],
+                                             v[h][3] * sc[h][3]);
+                        dst[1] = make_float4(v[h][4] * sc[h][4], v[h][5] * sc[h][5], v[h][6] * sc[h][6],
+                                             v[h][7] * sc[h][7]);
                     }
                 }
             }
