@@ -697,67 +697,61 @@ __device__ __forceinline__ void combine_shared(const float* __restrict__ w, int 
 }
 
 // Finish of the decode path: y[p] = the k-block parts of the down epilogue (Zd, already transformed and scaled) added
-// in order; with weights, out[row] = the token's slots in order, weighted. Program (token row, 128-column block), one
-// wave a slot (up to 16 at a time). Each wave loads its slot's weight (and wave 0 the first shared slot's weight and
-// output) together with the parts, so the combine adds no dependent round trip; each wave forms its weighted term
-// and wave 0 adds the terms in slot order.
+// in order; with weights, out[row] = the token's slots in order, weighted. Program (token row, 64-column block), one
+// wave a slot (up to 16 at a time), one column a lane (two a lane, over half the workgroups, measured 0.1 us slower
+// on config 2's layer: the parts' loads spread over fewer waves; one wave for all of a block's slots, 0.9 us slower).
+// Each wave loads its slot's weight (and wave 0 the first shared slot's weight and output) together with the parts,
+// so the combine adds no dependent round trip; each wave forms its weighted term and wave 0 adds the terms in slot
+// order.
 __global__ void __launch_bounds__(1024) sum_finish_kernel(const float* __restrict__ Z, float* __restrict__ y, int P,
                                                            int D, int SK, int slots, int exl3_slots,
                                                            const float* __restrict__ weights,
                                                            const float* __restrict__ shared, int shared_stride,
                                                            float* __restrict__ out) {
-    __shared__ float2 ys[16][64];
+    __shared__ float ys[16][64];
     const int row = blockIdx.x, blk = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nwv = blockDim.x >> 6;
-    const int n = blk * 128 + 2 * lane;
+    const int n = blk * 64 + lane;
     // the first shared slot's weight and output, loaded up front (wave 0 adds them last)
     const bool sh = weights && shared && exl3_slots < slots && wave == 0;
-    float sw = 0.f;
-    float2 sv = make_float2(0.f, 0.f);
+    float sw = 0.f, sv = 0.f;
     if (sh) {
         sw = weights[row * slots + exl3_slots];
-        sv = *reinterpret_cast<const float2*>(shared + (size_t)row * shared_stride + n);
+        sv = shared[(size_t)row * shared_stride + n];
     }
-    float o0 = 0.f, o1 = 0.f;
+    float o = 0.f;
     for (int s0 = 0; s0 < exl3_slots; s0 += nwv) {
         const int s = s0 + wave;
         if (s < exl3_slots) {
             const int p = row * slots + s;
             const float w = weights ? weights[p] : 0.f;
-            float2 zs[16];
-            float v0 = 0.f, v1 = 0.f;
+            float zs[16];
+            float v = 0.f;
             for (int k0 = 0; k0 < SK; k0 += 16) {           // parts in k order, sixteen in flight
 #pragma unroll
                 for (int k = 0; k < 16; ++k)
-                    if (k0 + k < SK) zs[k] = *reinterpret_cast<const float2*>(Z + ((size_t)(k0 + k) * P + p) * D + n);
+                    if (k0 + k < SK) zs[k] = Z[((size_t)(k0 + k) * P + p) * D + n];
 #pragma unroll
                 for (int k = 0; k < 16; ++k)
-                    if (k0 + k < SK) {
-                        v0 += zs[k].x;
-                        v1 += zs[k].y;
-                    }
+                    if (k0 + k < SK) v += zs[k];
             }
-            *reinterpret_cast<float2*>(y + (size_t)p * D + n) = make_float2(v0, v1);
-            ys[wave][lane] = make_float2(w * v0, w * v1);
+            y[(size_t)p * D + n] = v;
+            ys[wave][lane] = w * v;
         }
         if (weights) {
             __syncthreads();
             if (wave == 0)
-                for (int q = 0; q < nwv && s0 + q < exl3_slots; ++q) {
-                    o0 += ys[q][lane].x;
-                    o1 += ys[q][lane].y;
-                }
+                for (int q = 0; q < nwv && s0 + q < exl3_slots; ++q) o += ys[q][lane];
             __syncthreads();
         }
     }
     if (weights && wave == 0) {
         if (sh) {
-            o0 += sw * sv.x;
-            o1 += sw * sv.y;
-            combine_shared(weights + (size_t)row * slots, slots, exl3_slots + 1, shared, shared_stride, row, n, o0,
-                           o1);
+            o += sw * sv;
+            for (int s = exl3_slots + 1; s < slots; ++s)
+                o += weights[(size_t)row * slots + s] * shared[(size_t)row * shared_stride + n];
         }
-        *reinterpret_cast<float2*>(out + (size_t)row * D + n) = make_float2(o0, o1);
+        out[(size_t)row * D + n] = o;
     }
 }
 
@@ -1113,8 +1107,8 @@ hipError_t launch_sum_finish(hipStream_t s, const float* Zd, float* y, int rows,
                              int exl3_slots, const float* weights, const float* shared, int shared_stride,
                              float* out) {
     const int nwv = exl3_slots < 16 ? (exl3_slots > 0 ? exl3_slots : 1) : 16;
-    sum_finish_kernel<<<dim3(rows, D / 128), 64 * nwv, 0, s>>>(Zd, y, P, D, SK, slots, exl3_slots, weights, shared,
-                                                               shared_stride, out);
+    sum_finish_kernel<<<dim3(rows, D / 64), 64 * nwv, 0, s>>>(Zd, y, P, D, SK, slots, exl3_slots, weights, shared,
+                                                              shared_stride, out);
     return hipGetLastError();
 }
 
