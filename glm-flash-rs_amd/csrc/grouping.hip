@@ -192,6 +192,8 @@ __global__ void __launch_bounds__(1024) route_group_kernel(const float* __restri
     if (routed <= 64) route_rows<1>(logits, rows, routed, topk, pk, wt, gate);
     else if (routed <= 128) route_rows<2>(logits, rows, routed, topk, pk, wt, gate);
     else if (routed <= 256) route_rows<4>(logits, rows, routed, topk, pk, wt, gate);
+    else if (routed <= 320) route_rows<5>(logits, rows, routed, topk, pk, wt, gate);
+    else if (routed <= 512) route_rows<8>(logits, rows, routed, topk, pk, wt, gate);
     else route_rows<ROUTE_MAX_E / 64>(logits, rows, routed, topk, pk, wt, gate);
     __syncthreads();
     for (int i = threadIdx.x; i < rows * slots; i += blockDim.x) {

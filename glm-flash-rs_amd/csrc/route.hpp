@@ -166,6 +166,10 @@ __device__ __forceinline__ void route_token_regs(const float* __restrict__ l, in
     if (E <= 64) route_token_per<1>(l, E, topk, shared_id, pick, weight, g, need_weight);
     else if (E <= 128) route_token_per<2>(l, E, topk, shared_id, pick, weight, g, need_weight);
     else if (E <= 256) route_token_per<4>(l, E, topk, shared_id, pick, weight, g, need_weight);
+    // above 256: as many registers a lane as the experts need (each round scans every register, and GLM's gate takes
+    // a sigmoid of each: 288 experts in 5 instead of 16)
+    else if (E <= 320) route_token_per<5>(l, E, topk, shared_id, pick, weight, g, need_weight);
+    else if (E <= 512) route_token_per<8>(l, E, topk, shared_id, pick, weight, g, need_weight);
     else route_token_per<ROUTE_MAX_E / 64>(l, E, topk, shared_id, pick, weight, g, need_weight);
 }
 
