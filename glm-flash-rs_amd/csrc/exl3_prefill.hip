@@ -29,6 +29,7 @@
 #include "exl3_format.hpp"
 #include "launch.hpp"
 #include "prefill.hpp"
+#include "group_small.hpp"
 
 namespace gfr {
 
@@ -276,17 +277,14 @@ __global__ void __launch_bounds__(256) prefill_rot_kernel(const uint16_t* __rest
 // round, so the (slot, matrix) rows of a block fill the rounds exactly: round r is slot r (MATS = 2) or slots 2 r and
 // 2 r + 1 (MATS = 1). x * suh is exact in fp32 (bf16 times fp16), so it is one v_fma_mix_f32 from the fp16 scale;
 // the rest is rot_in's arithmetic as above, bit for bit. K / 128 even.
-template <int MATS>
-__global__ void __launch_bounds__(256) prefill_rot2_kernel(const uint16_t* __restrict__ x, int x_stride,
-                                                           const int* __restrict__ pick,
-                                                           const uint16_t* __restrict__ suh0,
-                                                           const uint16_t* __restrict__ suh1,
-                                                           uint16_t* __restrict__ out0, uint16_t* __restrict__ out1,
-                                                           int K, int rows, int slots, int exl3_slots) {
+// One wave's task (row, block pair bp); picks() returns the row's expert of slot `lane` on lanes below exl3_slots,
+// called once the token's loads are issued.
+template <int MATS, typename Picks>
+__device__ __forceinline__ void rot2_task(const uint16_t* __restrict__ x, int x_stride, Picks picks,
+                                          const uint16_t* __restrict__ suh0, const uint16_t* __restrict__ suh1,
+                                          uint16_t* __restrict__ out0, uint16_t* __restrict__ out1, int K, int row,
+                                          int bp, int slots, int exl3_slots) {
     const int lane = threadIdx.x & 63;
-    const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int KP = K / 256, row = task / KP, bp = task % KP;
-    if (row >= rows) return;
     const int j8 = l8_j(lane), r4 = l8_row(lane);
     const int blk = 2 * bp + (r4 >> 1), k = blk * 128 + 8 * j8;
     const int m = MATS == 2 ? (r4 & 1) : 0;
@@ -301,7 +299,7 @@ __global__ void __launch_bounds__(256) prefill_rot2_kernel(const uint16_t* __res
         xf[2 * i + 1] = bf16_to_f32((uint16_t)(xw[i] >> 16));
     }
     const int nrd = MATS == 2 ? exl3_slots : (exl3_slots + 1) / 2;
-    const int pk = lane < exl3_slots ? pick[row * slots + lane] : 0;
+    const int pk = picks();
     const float st = lane_sign(lane) * HAD_SCALE;
     constexpr int RC = 8;                                   // rounds a chunk: their scales in flight together
     for (int r0 = 0; r0 < nrd; r0 += RC) {
@@ -334,6 +332,61 @@ __global__ void __launch_bounds__(256) prefill_rot2_kernel(const uint16_t* __res
             if (MATS == 2 || sl < exl3_slots) store_pairs_l8(outm + (size_t)(row * slots + sl) * K, v, lane, st);
         }
     }
+}
+
+template <int MATS>
+__global__ void __launch_bounds__(256) prefill_rot2_kernel(const uint16_t* __restrict__ x, int x_stride,
+                                                           const int* __restrict__ pick,
+                                                           const uint16_t* __restrict__ suh0,
+                                                           const uint16_t* __restrict__ suh1,
+                                                           uint16_t* __restrict__ out0, uint16_t* __restrict__ out1,
+                                                           int K, int rows, int slots, int exl3_slots) {
+    const int lane = threadIdx.x & 63;
+    const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int KP = K / 256, row = task / KP, bp = task % KP;
+    if (row >= rows) return;
+    rot2_task<MATS>(x, x_stride, [&] { return lane < exl3_slots ? pick[row * slots + lane] : 0; }, suh0, suh1, out0,
+                    out1, K, row, bp, slots, exl3_slots);
+}
+
+// Route + group + item plan and the rotation of every EXL3 pair in one launch, for the windows route_group_kernel
+// takes (K / 128 even). Workgroup 0 does route_group_kernel's work (route_group_body; its dynamic LDS); the others
+// take prefill_rot2_kernel's tasks, a wave's task routing its token with the same router (route_load / route_pick on
+// the same logits, so the same picks as workgroup 0 writes) while its token loads are in flight. Nothing of one
+// part waits for the other.
+template <int MATS>
+__global__ void __launch_bounds__(512) route_group_rot_kernel(const float* __restrict__ logits, int rows, int routed,
+                                                              int topk, int* __restrict__ picks,
+                                                              float* __restrict__ weights, int* __restrict__ ids,
+                                                              int* __restrict__ count, int* __restrict__ members,
+                                                              int maxm, int bm, int* __restrict__ plan_ucnt,
+                                                              int* __restrict__ plan_items, int* __restrict__ plan,
+                                                              int plan_E, RouteGate gate,
+                                                              const uint16_t* __restrict__ x, int x_stride,
+                                                              const uint16_t* __restrict__ suh0,
+                                                              const uint16_t* __restrict__ suh1,
+                                                              uint16_t* __restrict__ out0, uint16_t* __restrict__ out1,
+                                                              int K, int exl3_slots) {
+    extern __shared__ uint32_t lds[];
+    __shared__ __attribute__((aligned(16))) int scan_scratch[16];
+    if (blockIdx.x == 0) {
+        route_group_body(lds, scan_scratch, logits, rows, routed, topk, picks, weights, ids, count, members, maxm, bm,
+                         plan_ucnt, plan_items, plan, plan_E, gate);
+        return;
+    }
+    const int task = (blockIdx.x - 1) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int KP = K / 256, row = task / KP, bp = task % KP;
+    if (row >= rows) return;
+    const int lane = threadIdx.x & 63;
+    rot2_task<MATS>(x, x_stride,
+                    [&] {
+                        int pick;
+                        float weight;
+                        route_token_regs(logits + (size_t)row * routed, routed, topk, routed, pick, weight, gate,
+                                         false);
+                        return lane < exl3_slots ? pick : 0;
+                    },
+                    suh0, suh1, out0, out1, K, row, bp, topk + 1, exl3_slots);
 }
 
 // ---- GEMM --------------------------------------------------------------------------------------------------------
@@ -970,7 +1023,7 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
                        int input_stride, const int* picks, const int* ids, const int* count, const int* members,
                        int rows, int maxm, bool shared_x, const float* combine_weights, float* combine_out,
                        bool* combined, bool planned, const float* combine_shared, int shared_stride,
-                       hipEvent_t shared_ready) {
+                       hipEvent_t shared_ready, bool rotated) {
     const PrefillDims& d = fx->d;
     if (combined) *combined = false;
     if (w->bits < 2 || w->bits > 5) return hipErrorInvalidValue;
@@ -984,7 +1037,9 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
         return hipErrorInvalidValue;
     hipError_t e;
     // rotated rows of every EXL3 pair (one copy when the two input rotations are the same)
-    if ((d.hidden / 128) % 2 == 0) {
+    if (rotated) {
+        if (shared_x || (d.hidden / 128) % 2) return hipErrorInvalidValue;   // not launch_route_group_rot's rows
+    } else if ((d.hidden / 128) % 2 == 0) {
         const int tasks = rows * (d.hidden / 256), grid = (tasks + 3) / 4;
         if (!shared_x)
             prefill_rot2_kernel<2><<<grid, 256, 0, s>>>(input, input_stride, picks, w->suh_g, w->suh_u, fx->xg, fx->xu,
@@ -1059,6 +1114,25 @@ int prefill_item_rows(const gfr_fast_experts* fx, int rows, int bits) {
     const bool split = fx->zgu && rows * fx->d.slots <= PF_SPLIT_PAIRS;
     return split ? PF_SPLIT_BM : pf_bm_for(bits);
 }
+hipError_t launch_route_group_rot(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_experts* w,
+                                  const uint16_t* input, int input_stride, const float* logits, int rows, int routed,
+                                  int topk, int* picks, float* weights, int* ids, int* count, int* members, int maxm,
+                                  const float* bias, float scale) {
+    const PrefillDims& d = fx->d;
+    const int slots = topk + 1;
+    const size_t lds = route_group_lds(rows, slots, routed + 1);
+    if (rows < 1 || rows > GROUP_SMALL_ROWS || rows > d.max_rows || routed + 1 > 1024 || slots != d.slots ||
+        lds > GROUP_LDS_MAX || (d.hidden / 128) % 2 || w->bits < 2 || w->bits > 5)
+        return hipErrorNotSupported;
+    constexpr int WG = 512;                              // route_group measured the same at 512 and 1024 threads
+    const int tasks = rows * (d.hidden / 256), grid = 1 + (tasks + WG / 64 - 1) / (WG / 64);
+    route_group_rot_kernel<2><<<grid, WG, lds, s>>>(logits, rows, routed, topk, picks, weights, ids, count, members,
+                                                    maxm, prefill_item_rows(fx, rows, w->bits), fx->ucnt, fx->items,
+                                                    fx->plan, w->experts, RouteGate{bias, scale}, input, input_stride,
+                                                    w->suh_g, w->suh_u, fx->xg, fx->xu, d.hidden, d.exl3_slots);
+    return hipGetLastError();
+}
+
 void prefill_plan_buffers(gfr_fast_experts* fx, int** ucnt, int** items, int** plan) {
     *ucnt = fx->ucnt;
     *items = fx->items;

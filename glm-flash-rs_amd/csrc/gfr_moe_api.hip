@@ -520,8 +520,15 @@ int moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uin
                            g->max_rows, m->weights, m->out, nullptr, shared, shared_stride, 0, shared_ready);
     }
     gfr_grouping* g = m->group_pre;
-    bool planned = false;
-    if (rows <= gfr::GROUP_SMALL_ROWS && g->experts <= 1024 &&
+    bool planned = false, rotated = false;
+    if ((e = gfr::launch_route_group_rot(m->pre, stream, w, input, m->hidden, logits, rows, m->routed, m->topk,
+                                         m->picks, m->weights, g->ids, g->count, g->members, g->max_rows,
+                                         m->route_bias, m->route_scale)) == hipSuccess) {
+        // route + group + item plan and the input rotation in one launch
+        planned = rotated = true;
+    } else if (e != hipErrorNotSupported) {
+        return hip_fail(e, "route + group + rotation");
+    } else if (rows <= gfr::GROUP_SMALL_ROWS && g->experts <= 1024 &&
         gfr::route_group_lds(rows, m->slots, g->experts) <= gfr::GROUP_LDS_MAX) {
         // route + group + the prefill engine's item plan in one launch (the same router, grouping and plan as the
         // separate launches below)
@@ -556,7 +563,7 @@ int moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uin
     bool combined = false;
     if ((e = gfr::prefill_run(m->pre, stream, w, input, m->hidden, m->picks, g->ids, g->count, g->members, rows,
                               g->max_rows, false, m->weights, m->out, &combined, planned, shared, shared_stride,
-                              shared_ready)) != hipSuccess)
+                              shared_ready, rotated)) != hipSuccess)
         return hip_fail(e, "prefill run");
     if (!combined && shared_ready && (e = hipStreamWaitEvent(stream, shared_ready, 0)) != hipSuccess)
         return hip_fail(e, "wait for the shared expert");
@@ -877,6 +884,9 @@ int gfr_moe_set_router(gfr_moe* m, const float* bias, float scale) {
 float* gfr_moe_output(const gfr_moe* m) { return m ? m->out : nullptr; }
 int32_t* gfr_moe_picks(const gfr_moe* m) { return m ? m->picks : nullptr; }
 float* gfr_moe_weights(const gfr_moe* m) { return m ? m->weights : nullptr; }
+uint16_t* gfr_moe_rotated(const gfr_moe* m, int mat) {
+    return m && (mat == 0 || mat == 1) ? gfr::prefill_rotated(m->pre, mat) : nullptr;
+}
 
 int gfr_moe_destroy(gfr_moe* m) {
     if (!m) return 0;

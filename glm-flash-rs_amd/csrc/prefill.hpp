@@ -19,7 +19,15 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
                        int rows, int maxm, bool shared_x, const float* combine_weights = nullptr,
                        float* combine_out = nullptr, bool* combined = nullptr, bool planned = false,
                        const float* combine_shared = nullptr, int shared_stride = 0,
-                       hipEvent_t shared_ready = nullptr);   // the stream waits on it before the combine
+                       hipEvent_t shared_ready = nullptr,    // the stream waits on it before the combine
+                       bool rotated = false);                // the rows are already rotated (launch_route_group_rot)
+// Route + group + item plan (launch_route_group's work) and prefill_run's input rotation in one launch, for a
+// window of the Moe path (the two input rotations apart); prefill_run then runs with planned and rotated. Returns
+// hipErrorNotSupported where the window does not fit the fused form (the caller then launches the parts).
+hipError_t launch_route_group_rot(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_experts* w,
+                                  const uint16_t* input, int input_stride, const float* logits, int rows, int routed,
+                                  int topk, int* picks, float* weights, int* ids, int* count, int* members, int maxm,
+                                  const float* bias, float scale);
 // The item plan of a window of `rows` at `bits`: member rows an item, and the buffers prefill_run's GEMMs read
 // (ucnt, items, plan). A caller that fills them itself (the fused route + group launch) passes planned = true.
 int prefill_item_rows(const gfr_fast_experts* fx, int rows, int bits);

@@ -57,6 +57,7 @@ def _load() -> ctypes.CDLL:
         "gfr_moe_output": ([VP], P),
         "gfr_moe_picks": ([VP], P),
         "gfr_moe_weights": ([VP], P),
+        "gfr_moe_rotated": ([VP, I], P),
         "gfr_moe_set_decode_rows": ([VP, I], I),
         "gfr_moe_create_shared": ([ctypes.POINTER(VP), I, I, I, I, I, I], I),
         "gfr_moe_run_shared": ([VP, P, P, P, P, P, I, I], I),
@@ -377,6 +378,12 @@ class Moe(_Engine):
 
     def set_decode_rows(self, n: int):
         _check(lib().gfr_moe_set_decode_rows(self._h, n))
+
+    def rotated(self, mat: int, rows: int) -> torch.Tensor:
+        """Parity probe (gfr_moe_rotated): the rotated input rows of the last prefill-engine run, [rows * (topk + 1),
+        hidden] fp16, k tiles in pair order."""
+        return _view(lib().gfr_moe_rotated(self._h, mat), (rows * (self.topk + 1), self.hidden), torch.float16,
+                     self.output.device)
 
     def set_launches(self, n: int):
         """Measurement aid (gfr_moe_set_launches): a one-row run issues only its first n launches (0: all)."""

@@ -136,6 +136,10 @@ int gfr_moe_run_router(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w
 float* gfr_moe_output(const gfr_moe* m);
 int32_t* gfr_moe_picks(const gfr_moe* m);        /* [rows][topk + 1] */
 float* gfr_moe_weights(const gfr_moe* m);        /* [rows][topk + 1] */
+/* Parity probe, no reference counterpart (as gfr_fast_experts_rotated): the rotated input rows of the last run on
+ * the prefill engine (windows above decode_rows), [rows * (topk + 1)][hidden] fp16 in the same pair order, matrix 0
+ * (gate) or 1 (up). Windows of at most 256 rows rotate them in the route + group launch. Null for mat not 0 or 1. */
+uint16_t* gfr_moe_rotated(const gfr_moe* m, int mat);
 /* Windows of at most decode_rows rows run the decode engine (default 4, at most 64), larger ones the prefill engine.
  * rows == 1 runs three launches: gate/up GEMV (router and input rotation fused), down GEMV (gate/up epilogue fused),
  * sum of the down parts + combine. */

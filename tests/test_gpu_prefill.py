@@ -216,6 +216,43 @@ def test_prefill_rotation_bitexact(gfr, oracle, hidden, slots, rows, shared_x):
                     f"matrix {m} row {r} slot {s}: {np.sum(got[r * slots + s] != want)} values differ"
 
 
+@pytest.mark.parametrize("hidden,routed,topk,rows,glm", [
+    (2048, 64, 4, 37, False),     # config 3's shape: softmax gate, 5 slots
+    (1024, 288, 8, 9, True),      # the reference's router: GLM's biased sigmoid gate over 288 experts, 9 slots
+    (512, 16, 2, 256, False),     # the largest window of the fused launch
+])
+def test_moe_fused_rotation_bitexact(gfr, oracle, hidden, routed, topk, rows, glm):
+    """Windows of at most 256 rows on the prefill engine route, group and rotate in one launch: workgroup 0 routes and
+    groups, the others route their own token again and rotate its pairs. Both routings must pick the same experts:
+    every rotated (pair, matrix) row against rot_in (exl3.cu:224-241) of the layer's pick for it, bit for bit, and
+    the softmax gate's picks against the oracle's."""
+    import synth
+    w = synth.experts(routed + 1, hidden, 256, 2, seed=hidden + rows)
+    x = synth.activations(rows, hidden, rows + 3)
+    lg = synth.logits(rows, routed, rows + 4)
+    m = gfr.Moe(hidden, 256, routed, topk, rows)
+    bias = None
+    if glm:
+        bias = torch.randn(routed, generator=torch.Generator(device="cuda").manual_seed(5), device="cuda") * 0.1
+        m.set_router(bias, 2.5)
+    m.run(w, x, lg, rows)
+    torch.cuda.synchronize()
+    # the rotating workgroups must have used the picks workgroup 0 wrote (the routers themselves against the oracle,
+    # near-ties of GLM's gate included, are tested with the decode path)
+    p = m.picks[:rows].cpu().numpy()
+    if not glm:
+        assert np.array_equal(p, oracle.route(lg.cpu().numpy(), topk, routed)[0])
+    xs = np_u16(x)
+    for mat in (0, 1):
+        got = _unpair(np_u16(m.rotated(mat, rows)))
+        suh = np_u16(w.suh_u if mat else w.suh_g)
+        for r in range(rows):
+            for s in range(topk + 1):
+                want = oracle.rot(xs[r], suh[p[r, s]])
+                assert np.array_equal(got[r * (topk + 1) + s], want), \
+                    f"matrix {mat} row {r} slot {s}: {np.sum(got[r * (topk + 1) + s] != want)} values differ"
+
+
 def test_split_window_with_many_experts(gfr, oracle):
     """A split-K window (at most 2048 pairs, 32-row items) whose routing spreads over 1023 experts with one member each
     plus a shared expert with every row: the plan holds 1023 + 32 items, more than an item count sized for 128-row
