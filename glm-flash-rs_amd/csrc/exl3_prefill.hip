@@ -29,7 +29,7 @@
 #include "exl3_format.hpp"
 #include "launch.hpp"
 #include "prefill.hpp"
-#include "group_small.hpp"
+#include "grouping_body.hpp"
 
 namespace gfr {
 
@@ -387,6 +387,39 @@ __global__ void __launch_bounds__(512) route_group_rot_kernel(const float* __res
                         return lane < exl3_slots ? pick : 0;
                     },
                     suh0, suh1, out0, out1, K, row, bp, topk + 1, exl3_slots);
+}
+
+// The large-window grouping's scatter launch (group_scatter_body, workgroups 0 .. E - 1) and the rotation
+// (prefill_rot2_kernel's tasks, the workgroups after them) in one launch: both read only the picks of the launches
+// before, and neither waits for the other.
+template <int MATS>
+__global__ void __launch_bounds__(256) group_scatter_rot_kernel(const int* __restrict__ picks, int rows, int slots,
+                                                                int E, const uint32_t* __restrict__ bits,
+                                                                const uint8_t* __restrict__ first,
+                                                                const int* __restrict__ prefix,
+                                                                const int* __restrict__ counts,
+                                                                int* __restrict__ ids, int* __restrict__ count,
+                                                                int* __restrict__ members, int maxm, int bm,
+                                                                int* __restrict__ plan_ucnt,
+                                                                int* __restrict__ plan_items, int* __restrict__ plan,
+                                                                int plan_E, const uint16_t* __restrict__ x,
+                                                                int x_stride, const uint16_t* __restrict__ suh0,
+                                                                const uint16_t* __restrict__ suh1,
+                                                                uint16_t* __restrict__ out0,
+                                                                uint16_t* __restrict__ out1, int K, int exl3_slots) {
+    __shared__ __attribute__((aligned(16))) int scan_scratch[16];
+    __shared__ int tot_sh[4];
+    if ((int)blockIdx.x < E) {
+        group_scatter_body(blockIdx.x, scan_scratch, tot_sh, picks, rows, slots, E, bits, first, prefix, counts, ids,
+                           count, members, maxm, bm, plan_ucnt, plan_items, plan, plan_E);
+        return;
+    }
+    const int lane = threadIdx.x & 63;
+    const int task = ((int)blockIdx.x - E) * 4 + (threadIdx.x >> 6);
+    const int KP = K / 256, row = task / KP, bp = task % KP;
+    if (row >= rows) return;
+    rot2_task<MATS>(x, x_stride, [&] { return lane < exl3_slots ? picks[row * slots + lane] : 0; }, suh0, suh1, out0,
+                    out1, K, row, bp, slots, exl3_slots);
 }
 
 // ---- GEMM --------------------------------------------------------------------------------------------------------
@@ -1130,6 +1163,26 @@ hipError_t launch_route_group_rot(gfr_fast_experts* fx, hipStream_t s, const gfr
                                                     maxm, prefill_item_rows(fx, rows, w->bits), fx->ucnt, fx->items,
                                                     fx->plan, w->experts, RouteGate{bias, scale}, input, input_stride,
                                                     w->suh_g, w->suh_u, fx->xg, fx->xu, d.hidden, d.exl3_slots);
+    return hipGetLastError();
+}
+
+hipError_t launch_group_large_rot(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_experts* w,
+                                  const uint16_t* input, int input_stride, const int* picks, int rows, int slots,
+                                  int E, uint32_t* bits, uint8_t* first, int* prefix, int* counts, int* ids,
+                                  int* count, int* members, int maxm) {
+    const PrefillDims& d = fx->d;
+    if (rows < 1 || rows > d.max_rows || slots != d.slots || (d.hidden / 128) % 2 || w->bits < 2 || w->bits > 5)
+        return hipErrorNotSupported;
+    const int bm = prefill_item_rows(fx, rows, w->bits);
+    hipError_t e = launch_group_large(s, picks, rows, slots, E, bits, first, prefix, counts, ids, count, members,
+                                      maxm, bm, fx->ucnt, fx->items, fx->plan, w->experts, false);
+    if (e != hipSuccess) return e;
+    const int tasks = rows * (d.hidden / 256);
+    group_scatter_rot_kernel<2><<<E + (tasks + 3) / 4, 256, 0, s>>>(picks, rows, slots, E, bits, first, prefix,
+                                                                    counts, ids, count, members, maxm, bm, fx->ucnt,
+                                                                    fx->items, fx->plan, w->experts, input,
+                                                                    input_stride, w->suh_g, w->suh_u, fx->xg, fx->xu,
+                                                                    d.hidden, d.exl3_slots);
     return hipGetLastError();
 }
 

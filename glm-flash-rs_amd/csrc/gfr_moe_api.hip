@@ -547,15 +547,22 @@ int moe_run(gfr_moe* m, hipStream_t stream, const gfr_exl3_experts* w, const uin
         if (rows <= gfr::GROUP_SMALL_ROWS) {
             if ((rc = gfr_grouping_run(g, stream, m->picks, rows))) return rc;
         } else {
-            // the three grouping launches, the last of which also writes the item plan
-            int *pu, *pi, *pp;
-            gfr::prefill_plan_buffers(m->pre, &pu, &pi, &pp);
-            if ((e = gfr::launch_group_large(stream, m->picks, rows, g->slots, g->experts, g->bits, g->first, g->prefix,
-                                             g->counts, g->ids, g->count, g->members, g->max_rows,
-                                             gfr::prefill_item_rows(m->pre, rows, w->bits), pu, pi, pp,
-                                             w->experts)) !=
-                hipSuccess)
-                return hip_fail(e, "grouping launch");
+            // the three grouping launches, the last of which also writes the item plan and rotates the input
+            if ((e = gfr::launch_group_large_rot(m->pre, stream, w, input, m->hidden, m->picks, rows, g->slots,
+                                                 g->experts, g->bits, g->first, g->prefix, g->counts, g->ids,
+                                                 g->count, g->members, g->max_rows)) == hipSuccess) {
+                rotated = true;
+            } else if (e != hipErrorNotSupported) {
+                return hip_fail(e, "grouping + rotation launches");
+            } else {
+                int *pu, *pi, *pp;
+                gfr::prefill_plan_buffers(m->pre, &pu, &pi, &pp);
+                if ((e = gfr::launch_group_large(stream, m->picks, rows, g->slots, g->experts, g->bits, g->first,
+                                                 g->prefix, g->counts, g->ids, g->count, g->members, g->max_rows,
+                                                 gfr::prefill_item_rows(m->pre, rows, w->bits), pu, pi, pp,
+                                                 w->experts)) != hipSuccess)
+                    return hip_fail(e, "grouping launch");
+            }
             planned = true;
         }
     }

@@ -10,7 +10,7 @@
 // Two paths: rows <= GROUP_SMALL_ROWS (launch.hpp) runs in one 1024-thread workgroup with the bitmap in LDS; larger windows run three
 // launches (per-256-row LDS bitmaps, per-expert popcount prefix, per-expert scatter), which also lifts the
 // reference's 8192-row limit.
-#include "group_small.hpp"
+#include "grouping_body.hpp"
 
 namespace gfr {
 
@@ -82,11 +82,7 @@ __global__ void __launch_bounds__(256) group_prefix_kernel(const uint32_t* __res
     if (threadIdx.x == 0) counts[e] = total;
 }
 
-// Launch 3, workgroup per expert: its place among the used experts, ids / count, its members and its -1 tail. A
-// thread per row: a member's position is the popcount prefix of its bitmap word plus the set bits below it in the
-// word, so no thread walks an expert's rows in sequence. With `plan` (bm rows an item) it also writes the prefill
-// engine's item plan, as prefill_plan_kernel would from the finished table: plan_ucnt[u] = members of used expert
-// u, plan_items = (u << 16) | pass for the ceil(members / bm) passes of each u in u order, plan[0] = item count.
+// Launch 3 (group_scatter_body), workgroup per expert.
 __global__ void __launch_bounds__(256) group_scatter_kernel(const int* __restrict__ picks, int rows, int slots,
                                                             int E, const uint32_t* __restrict__ bits,
                                                             const uint8_t* __restrict__ first,
@@ -98,72 +94,8 @@ __global__ void __launch_bounds__(256) group_scatter_kernel(const int* __restric
                                                             int plan_E) {
     __shared__ __attribute__((aligned(16))) int scan_scratch[16];
     __shared__ int tot_sh[4];
-    const int e = blockIdx.x, NWD = (rows + 31) >> 5;
-    int below = 0, used = 0, ibelow = 0, itotal = 0;
-    for (int q = threadIdx.x; q < E; q += blockDim.x) {
-        const int c = counts[q], np = plan && q < plan_E ? (c + bm - 1) / bm : 0;
-        used += c > 0;
-        below += (q < e) & (c > 0);
-        itotal += np;
-        ibelow += q < e ? np : 0;
-    }
-    int t[4];
-    block_scan(below, scan_scratch, &t[0]);
-    block_scan(used, scan_scratch, &t[1]);
-    if (plan) {
-        block_scan(ibelow, scan_scratch, &t[2]);
-        block_scan(itotal, scan_scratch, &t[3]);
-    }
-    if (threadIdx.x == 0)
-        for (int i = 0; i < 4; ++i) tot_sh[i] = t[i];
-    __syncthreads();
-    below = tot_sh[0];
-    used = tot_sh[1];
-    const int ce = counts[e];
-    if (e == 0 && threadIdx.x == 0) {
-        *count = used;
-        if (plan) plan[0] = tot_sh[3];
-    }
-    if (ce > 0) {
-        const int u = below;
-        if (threadIdx.x == 0) ids[u] = e;
-        if (plan) {
-            // experts at or above plan_E (a shared expert that is not EXL3) get no items
-            const int np = e < plan_E ? (ce + bm - 1) / bm : 0, first = tot_sh[2];
-            if (threadIdx.x == 0) plan_ucnt[u] = ce;
-            for (int k = threadIdx.x; k < np; k += blockDim.x) plan_items[first + k] = (u << 16) | k;
-        }
-        // rows in batches of UB a thread: every load of a batch is issued before any of its values is used (the
-        // empty asm keeps the compiler from sinking a load into the branch that uses it), so a batch costs one
-        // round trip; first[] of a row outside the expert is loaded and never used
-        constexpr int UB = 8;
-        const uint32_t* be = bits + (size_t)e * NWD;
-        const int* pe = prefix + (size_t)e * NWD;
-        const uint8_t* fe = first + (size_t)e * rows;
-        for (int r0 = threadIdx.x; r0 < rows; r0 += UB * blockDim.x) {
-            uint32_t b[UB];
-            int pos[UB], sl[UB];
-#pragma unroll
-            for (int k = 0; k < UB; ++k) {
-                const int r = min(r0 + k * (int)blockDim.x, rows - 1);
-                b[k] = be[r >> 5];
-                pos[k] = pe[r >> 5];
-                sl[k] = fe[r];
-            }
-#pragma unroll
-            for (int k = 0; k < UB; ++k) __asm__ volatile("" : "+v"(b[k]), "+v"(pos[k]), "+v"(sl[k]));
-#pragma unroll
-            for (int k = 0; k < UB; ++k) {
-                const int r = r0 + k * (int)blockDim.x;
-                if (r < rows && ((b[k] >> (r & 31)) & 1u))
-                    members[(size_t)u * maxm + pos[k] + __popc(b[k] & ((1u << (r & 31)) - 1u))] = r * 32 + sl[k];
-            }
-        }
-        for (int j = ce + threadIdx.x; j < maxm; j += blockDim.x) members[(size_t)u * maxm + j] = -1;
-    }
-    // rows [used, E) of the table: owned by the workgroup with the same index (never a used row above)
-    if (e >= used)
-        for (int j = threadIdx.x; j < maxm; j += blockDim.x) members[(size_t)e * maxm + j] = -1;
+    group_scatter_body(blockIdx.x, scan_scratch, tot_sh, picks, rows, slots, E, bits, first, prefix, counts, ids,
+                       count, members, maxm, bm, plan_ucnt, plan_items, plan, plan_E);
 }
 
 }  // namespace gfr
@@ -200,13 +132,14 @@ hipError_t launch_route_group(hipStream_t s, const float* logits, int rows, int 
 
 hipError_t launch_group_large(hipStream_t s, const int* picks, int rows, int slots, int E, uint32_t* bits,
                               uint8_t* first, int* prefix, int* counts, int* ids, int* count, int* members, int maxm,
-                              int bm, int* plan_ucnt, int* plan_items, int* plan, int plan_E) {
+                              int bm, int* plan_ucnt, int* plan_items, int* plan, int plan_E, bool scatter) {
     if ((size_t)E * 8 * 4 > GROUP_LDS_MAX) return hipErrorInvalidValue;
     group_mark_kernel<<<(rows + 255) / 256, 256, (size_t)E * 8 * 4, s>>>(picks, rows, slots, E, bits, first);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     group_prefix_kernel<<<E, 256, 0, s>>>(bits, rows, prefix, counts);
     if ((err = hipGetLastError()) != hipSuccess) return err;
+    if (!scatter) return hipSuccess;
     group_scatter_kernel<<<E, 256, 0, s>>>(picks, rows, slots, E, bits, first, prefix, counts, ids, count, members, maxm,
                                             bm, plan_ucnt, plan_items, plan, plan_E);
     return hipGetLastError();

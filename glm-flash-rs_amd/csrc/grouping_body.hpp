@@ -1,7 +1,7 @@
-// One-workgroup routing and grouping of small windows (rows <= GROUP_SMALL_ROWS), shared by the grouping
-// launches (grouping.hip) and the prefill engine's route + group + rotation launch (exl3_prefill.hip). The
-// grouping is bit-exact to glm-flash-rs native/grouping.cu's group_small and to src/grouping.rs:141-192 (contract
-// in grouping.hip).
+// Device bodies of the grouping launches, shared by the grouping kernels (grouping.hip) and the prefill engine's
+// launches that also rotate the input (exl3_prefill.hip): one-workgroup routing and grouping of small windows
+// (rows <= GROUP_SMALL_ROWS) and the per-expert scatter of large ones. The grouping is bit-exact to glm-flash-rs
+// native/grouping.cu and to src/grouping.rs:141-192 (contract in grouping.hip).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -183,6 +183,87 @@ __device__ __forceinline__ void route_group_body(uint32_t* lds, int* scan_scratc
     }
     group_small_body(pk, rows, slots, E, ids, count, members, maxm, rest, scan_scratch, bm, plan_ucnt, plan_items,
                      plan, plan_E);
+}
+
+
+// Launch 3, workgroup per expert (e; scan_scratch: 16 ints, 16-byte aligned; tot_sh: 4 ints, both LDS): its place among the used experts, ids / count, its members and its -1 tail. A
+// thread per row: a member's position is the popcount prefix of its bitmap word plus the set bits below it in the
+// word, so no thread walks an expert's rows in sequence. With `plan` (bm rows an item) it also writes the prefill
+// engine's item plan, as prefill_plan_kernel would from the finished table: plan_ucnt[u] = members of used expert
+// u, plan_items = (u << 16) | pass for the ceil(members / bm) passes of each u in u order, plan[0] = item count.
+__device__ __forceinline__ void group_scatter_body(int e, int* scan_scratch, int* tot_sh, const int* __restrict__ picks,
+                                                   int rows, int slots, int E, const uint32_t* __restrict__ bits,
+                                                   const uint8_t* __restrict__ first, const int* __restrict__ prefix,
+                                                   const int* __restrict__ counts, int* __restrict__ ids,
+                                                   int* __restrict__ count, int* __restrict__ members, int maxm,
+                                                   int bm, int* __restrict__ plan_ucnt, int* __restrict__ plan_items,
+                                                   int* __restrict__ plan, int plan_E) {
+    const int NWD = (rows + 31) >> 5;
+    int below = 0, used = 0, ibelow = 0, itotal = 0;
+    for (int q = threadIdx.x; q < E; q += blockDim.x) {
+        const int c = counts[q], np = plan && q < plan_E ? (c + bm - 1) / bm : 0;
+        used += c > 0;
+        below += (q < e) & (c > 0);
+        itotal += np;
+        ibelow += q < e ? np : 0;
+    }
+    int t[4];
+    block_scan(below, scan_scratch, &t[0]);
+    block_scan(used, scan_scratch, &t[1]);
+    if (plan) {
+        block_scan(ibelow, scan_scratch, &t[2]);
+        block_scan(itotal, scan_scratch, &t[3]);
+    }
+    if (threadIdx.x == 0)
+        for (int i = 0; i < 4; ++i) tot_sh[i] = t[i];
+    __syncthreads();
+    below = tot_sh[0];
+    used = tot_sh[1];
+    const int ce = counts[e];
+    if (e == 0 && threadIdx.x == 0) {
+        *count = used;
+        if (plan) plan[0] = tot_sh[3];
+    }
+    if (ce > 0) {
+        const int u = below;
+        if (threadIdx.x == 0) ids[u] = e;
+        if (plan) {
+            // experts at or above plan_E (a shared expert that is not EXL3) get no items
+            const int np = e < plan_E ? (ce + bm - 1) / bm : 0, first = tot_sh[2];
+            if (threadIdx.x == 0) plan_ucnt[u] = ce;
+            for (int k = threadIdx.x; k < np; k += blockDim.x) plan_items[first + k] = (u << 16) | k;
+        }
+        // rows in batches of UB a thread: every load of a batch is issued before any of its values is used (the
+        // empty asm keeps the compiler from sinking a load into the branch that uses it), so a batch costs one
+        // round trip; first[] of a row outside the expert is loaded and never used
+        constexpr int UB = 8;
+        const uint32_t* be = bits + (size_t)e * NWD;
+        const int* pe = prefix + (size_t)e * NWD;
+        const uint8_t* fe = first + (size_t)e * rows;
+        for (int r0 = threadIdx.x; r0 < rows; r0 += UB * blockDim.x) {
+            uint32_t b[UB];
+            int pos[UB], sl[UB];
+#pragma unroll
+            for (int k = 0; k < UB; ++k) {
+                const int r = min(r0 + k * (int)blockDim.x, rows - 1);
+                b[k] = be[r >> 5];
+                pos[k] = pe[r >> 5];
+                sl[k] = fe[r];
+            }
+#pragma unroll
+            for (int k = 0; k < UB; ++k) __asm__ volatile("" : "+v"(b[k]), "+v"(pos[k]), "+v"(sl[k]));
+#pragma unroll
+            for (int k = 0; k < UB; ++k) {
+                const int r = r0 + k * (int)blockDim.x;
+                if (r < rows && ((b[k] >> (r & 31)) & 1u))
+                    members[(size_t)u * maxm + pos[k] + __popc(b[k] & ((1u << (r & 31)) - 1u))] = r * 32 + sl[k];
+            }
+        }
+        for (int j = ce + threadIdx.x; j < maxm; j += blockDim.x) members[(size_t)u * maxm + j] = -1;
+    }
+    // rows [used, E) of the table: owned by the workgroup with the same index (never a used row above)
+    if (e >= used)
+        for (int j = threadIdx.x; j < maxm; j += blockDim.x) members[(size_t)e * maxm + j] = -1;
 }
 
 }  // namespace gfr

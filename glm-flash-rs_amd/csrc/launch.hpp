@@ -24,7 +24,8 @@ hipError_t launch_route_group(hipStream_t s, const float* logits, int rows, int 
 hipError_t launch_group_large(hipStream_t s, const int* picks, int rows, int slots, int E, uint32_t* bits,
                               uint8_t* first, int* prefix, int* counts, int* ids, int* count, int* members, int maxm,
                               int bm = 0, int* plan_ucnt = nullptr, int* plan_items = nullptr, int* plan = nullptr,
-                              int plan_E = 0);
+                              int plan_E = 0, bool scatter = true);
+// scatter = false: the mark and prefix launches only (the caller launches the scatter, group_scatter_body, itself)
 
 // exl3_decode.hip
 hipError_t launch_decode_tiles(hipStream_t s, const uint32_t* T, int kin, int n, int bits, uint16_t* out);

@@ -21,6 +21,13 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
                        const float* combine_shared = nullptr, int shared_stride = 0,
                        hipEvent_t shared_ready = nullptr,    // the stream waits on it before the combine
                        bool rotated = false);                // the rows are already rotated (launch_route_group_rot)
+// The large-window grouping (launch_group_large with its item plan) with prefill_run's input rotation in its last
+// launch, for a window of the Moe path whose picks are routed; prefill_run then runs with planned and rotated.
+// Returns hipErrorNotSupported where the window does not fit (the caller then launches the parts).
+hipError_t launch_group_large_rot(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_experts* w,
+                                  const uint16_t* input, int input_stride, const int* picks, int rows, int slots,
+                                  int E, uint32_t* bits, uint8_t* first, int* prefix, int* counts, int* ids,
+                                  int* count, int* members, int maxm);
 // Route + group + item plan (launch_route_group's work) and prefill_run's input rotation in one launch, for a
 // window of the Moe path (the two input rotations apart); prefill_run then runs with planned and rotated. Returns
 // hipErrorNotSupported where the window does not fit the fused form (the caller then launches the parts).

@@ -219,11 +219,14 @@ def test_prefill_rotation_bitexact(gfr, oracle, hidden, slots, rows, shared_x):
 @pytest.mark.parametrize("hidden,routed,topk,rows,glm", [
     (2048, 64, 4, 37, False),     # config 3's shape: softmax gate, 5 slots
     (1024, 288, 8, 9, True),      # the reference's router: GLM's biased sigmoid gate over 288 experts, 9 slots
-    (512, 16, 2, 256, False),     # the largest window of the fused launch
+    (512, 16, 2, 256, False),     # the largest window of the route + group + rotation launch
+    (512, 16, 2, 300, False),     # larger windows: the rotation rides on the grouping's scatter launch
+    (1024, 288, 8, 260, True),    # ... with GLM's gate, full-K items
 ])
 def test_moe_fused_rotation_bitexact(gfr, oracle, hidden, routed, topk, rows, glm):
     """Windows of at most 256 rows on the prefill engine route, group and rotate in one launch: workgroup 0 routes and
-    groups, the others route their own token again and rotate its pairs. Both routings must pick the same experts:
+    groups, the others route their own token again and rotate its pairs; larger windows rotate in the grouping's
+    scatter launch, from the routed picks. Both routings must pick the same experts:
     every rotated (pair, matrix) row against rot_in (exl3.cu:224-241) of the layer's pick for it, bit for bit, and
     the softmax gate's picks against the oracle's."""
     import synth
