@@ -256,6 +256,38 @@ def test_moe_fused_rotation_bitexact(gfr, oracle, hidden, routed, topk, rows, gl
                     f"matrix {mat} row {r} slot {s}: {np.sum(got[r * (topk + 1) + s] != want)} values differ"
 
 
+@pytest.mark.parametrize("rows", [32, 300, 1024])
+def test_moe_prefill_graph_replays(gfr, rows):
+    """A captured prefill-engine layer replays to the eager bytes, across two weight sets and routings: a small window
+    (route + group + rotation in one launch, split-K programs), a larger split-K window (the rotation in the
+    grouping's scatter launch) and a full-K window. Each replay follows eager work that clears the output."""
+    import synth
+    E, D, N, bits, topk = 16, 512, 256, 4, 2
+    ws = [synth.experts(E + 1, D, N, bits, seed=s) for s in (31, 32)]
+    xs = [synth.activations(rows, D, 33 + j) for j in range(2)]
+    lgs = [synth.logits(rows, E, 35 + j) for j in range(2)]
+    m = gfr.Moe(D, N, E, topk, rows)
+    s = torch.cuda.Stream()
+    eager = []
+    with torch.cuda.stream(s):
+        for j in range(2):
+            m.run(ws[j], xs[j], lgs[j], rows, stream=s)
+            s.synchronize()
+            eager.append(m.output[:rows].clone())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            m.run(ws[0], xs[0], lgs[0], rows, stream=s)
+            m.run(ws[1], xs[1], lgs[1], rows, stream=s)
+    assert not torch.equal(eager[0], eager[1])
+    for _ in range(3):
+        m.output.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(m.output[:rows], eager[1])
+
+
 def test_split_window_with_many_experts(gfr, oracle):
     """A split-K window (at most 2048 pairs, 32-row items) whose routing spreads over 1023 experts with one member each
     plus a shared expert with every row: the plan holds 1023 + 32 items, more than an item count sized for 128-row
