@@ -986,6 +986,10 @@ namespace gfr {
 #endif
 constexpr int PF_SPLIT_PAIRS = PF_SPLIT_PAIRS_MAX;
 constexpr int PF_SPLIT_K = 512;
+// The gate/up programs take 1024 k where the hidden size allows: measured against 512 at config 3's window (103.6–
+// 105.7 vs 105.1–107.4 us), the reference geometry's 40-row window (178.7–186.0 vs 183.1–188.9 us) and a 32-row
+// window of config 5's shape (386.8–403.3 vs 398.6–417.8 us), three alternating runs each on two boxes; 2048 lost.
+static int split_k_gateup(int hidden) { return hidden % (2 * PF_SPLIT_K) == 0 ? 2 * PF_SPLIT_K : PF_SPLIT_K; }
 constexpr int PF_SPLIT_BM = 32;
 static bool split_ok(int hidden, int inter) { return hidden % PF_SPLIT_K == 0 && inter % PF_SPLIT_K == 0; }
 static_assert(PF_SPLIT_BM <= PF_BM2 && PF_SPLIT_BM <= PF_BM3 && PF_SPLIT_BM <= PF_BM4 && PF_SPLIT_BM <= PF_BM5,
@@ -1113,7 +1117,7 @@ hipError_t prefill_run(gfr_fast_experts* fx, hipStream_t s, const gfr_exl3_exper
     a.maxm = maxm; a.slots = d.slots; a.limit = 10.f;
     if (split) {
         // gate / up partials -> epilogue (xd in pair order) -> down partials -> epilogue -> output
-        const int skg = d.hidden / PF_SPLIT_K, skd = d.inter / PF_SPLIT_K;
+        const int skg = d.hidden / split_k_gateup(d.hidden), skd = d.inter / PF_SPLIT_K;
         a.sk = skg; a.P = P; a.z = fx->zgu;
         a.x0 = fx->xg; a.x1 = shared_x ? fx->xg : fx->xu; a.t0 = w->gt; a.t1 = w->ut; a.Kin = d.hidden; a.N = d.inter;
         if ((e = launch_gemm_split<2>(w->bits, dim3(max_items * (d.inter / 128) * skg), s, a)) != hipSuccess) return e;
